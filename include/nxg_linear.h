@@ -1,0 +1,172 @@
+/* nxg_linear.h -- C ABI of the MI355X (gfx950) int8 linear-layer engine for NexteraBERT.
+ *
+ * The engine replaces the int8 path of NexteraBERT.cpp: per-token activation
+ * quantization, the W8A8 GEMM over load-time-expanded weights with int32
+ * accumulation, and the dequant/scale (+residual) epilogue, over the packed,
+ * unpadded rows of a mixed-length batch. Results are the reference's bit for bit:
+ * the same int32 block sums and the same fp32 outputs.
+ *
+ * Conventions
+ *   - Plain pointers and sizes only. Device pointers are HIP device memory on the
+ *     current device; host pointers are ordinary memory. `stream` is a hipStream_t
+ *     (NULL: the default stream); device work is ordered by it and the calls return
+ *     without waiting for it.
+ *   - Every int-returning call returns NXG_OK (0) or an NXG_E* code, the reference C
+ *     API's convention (0 ok, 1 bad input, 2 allocation, 3 compute;
+ *     src/nexterabert.cpp:1874-1899). nxg_last_error() gives the reason.
+ *   - One host thread per engine object at a time, like a nextera_context
+ *     (src/nexterabert.cpp:342-344).
+ *
+ * Buffers on the device
+ *   quantized activations of T rows x n_in inputs ("qact"):
+ *     q   int8, nxg_qact_q_bytes(T, n_in) bytes, in MFMA fragment tiles: byte (t, k) at
+ *           ((t/16)*KS + k/64)*1024 + ((t%16) + 16*((k%64)/16))*16 + k%16,
+ *         KS = ceil(n_in/64); values are the reference's u8 minus ACT_OFF; padding is 0.
+ *     sx  float, nxg_qact_sx_bytes(T, n_in) bytes, in the reference's layout
+ *           [token/4][block][token%4] (src/nexterabert.cpp:368-375), padded to 16 rows.
+ *   outputs and residuals: float [T][n_out], row-major (the (n_out, T) ggml tensor).
+ */
+#ifndef NXG_LINEAR_H
+#define NXG_LINEAR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(NXG_BUILD)
+#  define NXG_API __attribute__((visibility("default")))
+#else
+#  define NXG_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NXG_OK      0
+#define NXG_EINVAL  1   /* bad input */
+#define NXG_ENOMEM  2   /* allocation failed */
+#define NXG_EDEVICE 3   /* HIP error, missing or wrong GPU */
+
+#define NXG_BLOCK 256   /* inputs per scale block: I8_BLOCK, src/nexterabert.cpp:254 */
+
+/* ggml block types the load-time expansion decodes (ggml's type numbering, as stored in GGUF). */
+enum nxg_type {
+    NXG_TYPE_F32  = 0,
+    NXG_TYPE_F16  = 1,
+    NXG_TYPE_Q4_0 = 2,
+    NXG_TYPE_Q4_1 = 3,
+    NXG_TYPE_Q5_0 = 6,
+    NXG_TYPE_Q5_1 = 7,
+    NXG_TYPE_Q8_0 = 8,
+    NXG_TYPE_Q2_K = 10,
+    NXG_TYPE_Q3_K = 11,
+    NXG_TYPE_Q4_K = 12,
+    NXG_TYPE_Q5_K = 13,
+    NXG_TYPE_Q6_K = 14,
+    NXG_TYPE_BF16 = 30
+};
+
+/* Reason for the last failed call on this thread ("" if none). */
+NXG_API const char * nxg_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * Host side: load-time weight expansion
+ * ------------------------------------------------------------------------- */
+
+/* Would the reference run this weight on its int8 GEMM? Replaces the placement rule
+ * of nextera_load, src/nexterabert.cpp:1658-1667: use_int8, 2-D, a quantized block type,
+ * not an embedding matrix, ne0 % 32 == 0 and ne1 % 4 == 0. Returns 1 or 0. */
+NXG_API int32_t nxg_weight_is_int8(const char * name, int32_t n_dims, int32_t type,
+                                   int64_t ne0, int64_t ne1, int32_t use_int8);
+
+/* Bytes of one row of n_in values of `type` in a GGUF file (ggml_row_size); 0 if unsupported. */
+NXG_API size_t nxg_row_bytes(int32_t type, int64_t n_in);
+
+/* Decode rows of a GGUF tensor to f32 (ggml's to_float for `type`). out: n_rows * n_in floats. */
+NXG_API int32_t nxg_dequantize_rows(int32_t type, const void * data, int64_t n_in, int64_t n_rows, float * out);
+
+/* build_i8_weight, src/nexterabert.cpp:1010-1049: dequantize each of the n_out rows of
+ * `data` (ggml `type`, n_in values per row) and re-quantize every block of 256 inputs
+ * to s8 with lround(x * 127/amax).
+ *   w      out: int8  [n_out][n_in]
+ *   scale  out: float [n_blk][n_out], amax / 127
+ *   off    out: int32 [n_blk][n_out], -act_off * sum of the block's s8 values (may be NULL;
+ *               act_off is ACT_MAX + 1: 128 on VNNI builds of the reference, 64 on AVX2 ones)
+ * n_threads <= 0: all hardware threads. */
+NXG_API int32_t nxg_expand_weight(int32_t type, const void * data, int32_t n_in, int32_t n_out,
+                                  int32_t act_off, int32_t n_threads,
+                                  int8_t * w, float * scale, int32_t * off);
+
+/* Encodes n_rows rows of n_in f32 values as Q8_0, Q4_K or Q6_K GGUF blocks into
+ * nxg_row_bytes(type, n_in) * n_rows bytes at `out`. For synthetic weight files; the
+ * reference's own quantizer is ggml's (tools/quantize.cpp:201-213), whose search for
+ * K-quant scales this one-pass encoder does not reproduce. */
+NXG_API int32_t nxg_quantize_weight(int32_t type, const float * x, int64_t n_in, int64_t n_rows, void * out);
+
+/* ---------------------------------------------------------------------------
+ * Device side
+ * ------------------------------------------------------------------------- */
+
+/* Checks that the current HIP device is a gfx950 GPU. Called by every device entry
+ * point on first use; returns NXG_EDEVICE otherwise. */
+NXG_API int32_t nxg_init(void);
+
+/* Sizes of the qact buffers for T rows of n_in inputs (0 if n_in is not a positive
+ * multiple of 32 or T < 0). */
+NXG_API size_t nxg_qact_q_bytes(int32_t T, int32_t n_in);
+NXG_API size_t nxg_qact_sx_bytes(int32_t T, int32_t n_in);
+
+/* quantize_row on every row (src/nexterabert.cpp:378-403; op_copy, :453-461).
+ *   x        device float [T][n_in]
+ *   act_max  127 (VNNI builds of the reference) or 63 (AVX2-only builds), src/nexterabert.cpp:53-70
+ *   q, sx    device qact buffers (sizes above); fully written, padding included. */
+NXG_API int32_t nxg_quantize_rows(const float * x, int32_t T, int32_t n_in, int32_t act_max,
+                                  int8_t * q, float * sx, void * stream);
+
+/* The qact buffers in the reference's own format (src/nexterabert.cpp:368-375):
+ *   u8  device uint8 [T][n_in], the reference's u8 values (q + act_max + 1)
+ *   sx_ref device float, ((T+3)/4)*n_blk*4 floats, [token/4][block][token%4] */
+NXG_API int32_t nxg_qact_export(const int8_t * q, const float * sx, int32_t T, int32_t n_in, int32_t act_max,
+                                uint8_t * u8, float * sx_ref, void * stream);
+
+/* An expanded weight on the device, re-laid out once into MFMA fragment tiles. */
+typedef struct nxg_weight nxg_weight;
+
+/* Uploads an expanded weight (host w [n_out][n_in], scale [n_blk][n_out] as written by
+ * nxg_expand_weight; the i8_weight of src/nexterabert.cpp:256-261 without `off`, which
+ * the signed activations make unnecessary). n_in: positive multiple of 32; n_out >= 1.
+ * Blocks until the upload is complete. */
+NXG_API int32_t nxg_weight_create(const int8_t * w, const float * scale, int32_t n_in, int32_t n_out,
+                                  nxg_weight ** out);
+NXG_API void    nxg_weight_destroy(nxg_weight * w);
+NXG_API int32_t nxg_weight_n_in(const nxg_weight * w);
+NXG_API int32_t nxg_weight_n_out(const nxg_weight * w);
+/* Bytes of device memory the weight holds. */
+NXG_API size_t  nxg_weight_device_bytes(const nxg_weight * w);
+
+/* op_linear_i8, src/nexterabert.cpp:969-1007 (registered by builder::linear, :1121-1138):
+ *   out[t][r] = residual[t][r] + f,  f = fma((float) s_B * sx[t,B], scale[B][r], f) over B
+ * ascending, s_B the exact int32 sum of block B. Rows are the packed batch: cu_offsets
+ * (host int32, n_seqs + 1 entries, cu_offsets[0] = 0, strictly increasing -- empty
+ * sequences are refused as in src/nexterabert.cpp:1345-1347) gives T = cu_offsets[n_seqs].
+ *   q, sx     qact of the T rows (from nxg_quantize_rows)
+ *   residual  device float [T][n_out] or NULL
+ *   out       device float [T][n_out] */
+NXG_API int32_t nxg_linear_i8(const nxg_weight * w, const int8_t * q, const float * sx,
+                              const int32_t * cu_offsets, int32_t n_seqs,
+                              const float * residual, float * out, void * stream);
+
+/* The same for T rows given directly. */
+NXG_API int32_t nxg_linear_i8_rows(const nxg_weight * w, const int8_t * q, const float * sx, int32_t T,
+                                   const float * residual, float * out, void * stream);
+
+/* The int32 block sums s_B of the same GEMM: sums device int32 [n_blk][T][n_out],
+ * equal to the reference's sum_i w8*u8 + off (src/nexterabert.cpp:892-916). For tests. */
+NXG_API int32_t nxg_linear_i8_block_sums(const nxg_weight * w, const int8_t * q, int32_t T,
+                                         int32_t * sums, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NXG_LINEAR_H */

@@ -1,0 +1,344 @@
+"""nexterabert.cpp_amd -- the int8 linear-layer path of NexteraBERT.cpp on MI355X (gfx950).
+
+Python side of libnxg.so (include/nxg_linear.h). It mirrors the reference's own
+interface for the path, with torch tensors as device memory and torch's current
+stream as the HIP stream:
+
+  expand_weight(type, data, n_in, n_out)   build_i8_weight        src/nexterabert.cpp:1010-1049
+  weight_is_int8(name, ...)                 placement rule         src/nexterabert.cpp:1658-1667
+  quantize_rows(x)                          quantize_row / op_copy src/nexterabert.cpp:378-403,453-461
+  linear_i8(weight, qact, residual)         op_linear_i8           src/nexterabert.cpp:969-1007
+  Builder.linear(name, x, residual)         builder::linear        src/nexterabert.cpp:1121-1143
+
+Errors follow the reference: bad input raises ValueError (rc 1), allocation
+MemoryError (rc 2), device failures RuntimeError (rc 3). There is no CPU
+fallback: without the built library or a gfx950 GPU every device call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Dict, Optional, Sequence
+
+import numpy as np
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = _PKG / "libnxg.so"
+BLOCK = 256
+
+# ggml block types (GGUF numbering), include/nxg_linear.h
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_1 = 0, 1, 2, 3
+TYPE_Q5_0, TYPE_Q5_1, TYPE_Q8_0 = 6, 7, 8
+TYPE_Q2_K, TYPE_Q3_K, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 10, 11, 12, 13, 14
+TYPE_BF16 = 30
+
+NXG_OK, NXG_EINVAL, NXG_ENOMEM, NXG_EDEVICE = 0, 1, 2, 3
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+class NxgError(RuntimeError):
+    pass
+
+
+def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
+    """Loads libnxg.so (built by build.py); raises if it is missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(f"{p} is not built: run python nexterabert.cpp_amd/build.py "
+                                "(or __graft_entry__.build())")
+    L = ctypes.CDLL(str(p))
+    P, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
+    sigs = {
+        "nxg_last_error": ([], ctypes.c_char_p),
+        "nxg_weight_is_int8": ([ctypes.c_char_p, i32, i32, i64, i64, i32], i32),
+        "nxg_row_bytes": ([i32, i64], sz),
+        "nxg_dequantize_rows": ([i32, P, i64, i64, P], i32),
+        "nxg_expand_weight": ([i32, P, i32, i32, i32, i32, P, P, P], i32),
+        "nxg_quantize_weight": ([i32, P, i64, i64, P], i32),
+        "nxg_init": ([], i32),
+        "nxg_qact_q_bytes": ([i32, i32], sz),
+        "nxg_qact_sx_bytes": ([i32, i32], sz),
+        "nxg_quantize_rows": ([P, i32, i32, i32, P, P, P], i32),
+        "nxg_qact_export": ([P, P, i32, i32, i32, P, P, P], i32),
+        "nxg_weight_create": ([P, P, i32, i32, ctypes.POINTER(P)], i32),
+        "nxg_weight_destroy": ([P], None),
+        "nxg_weight_n_in": ([P], i32),
+        "nxg_weight_n_out": ([P], i32),
+        "nxg_weight_device_bytes": ([P], sz),
+        "nxg_linear_i8": ([P, P, P, P, i32, P, P, P], i32),
+        "nxg_linear_i8_rows": ([P, P, P, i32, P, P, P], i32),
+        "nxg_linear_i8_block_sums": ([P, P, i32, P, P], i32),
+    }
+    for name, (args, res) in sigs.items():
+        fn = getattr(L, name)
+        fn.argtypes, fn.restype = args, res
+    if path is None:
+        _lib = L
+    return L
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == NXG_OK:
+        return
+    msg = f"{what}: {load_library().nxg_last_error().decode()}"
+    if rc == NXG_EINVAL:
+        raise ValueError(msg)
+    if rc == NXG_ENOMEM:
+        raise MemoryError(msg)
+    raise NxgError(msg)
+
+
+def _np_ptr(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data
+
+
+# --- host side: load-time expansion ------------------------------------------------------------
+
+def weight_is_int8(name: str, n_dims: int, type_: int, ne0: int, ne1: int, use_int8: bool = True) -> bool:
+    """The reference's rule for putting a weight on the int8 GEMM (src/nexterabert.cpp:1658-1667)."""
+    return bool(load_library().nxg_weight_is_int8(name.encode(), n_dims, type_, ne0, ne1, int(use_int8)))
+
+
+def row_bytes(type_: int, n_in: int) -> int:
+    return int(load_library().nxg_row_bytes(type_, n_in))
+
+
+def dequantize_rows(type_: int, data: np.ndarray, n_in: int, n_rows: int) -> np.ndarray:
+    data = np.ascontiguousarray(data)
+    out = np.empty((n_rows, n_in), np.float32)
+    _check(load_library().nxg_dequantize_rows(type_, _np_ptr(data), n_in, n_rows, _np_ptr(out)), "dequantize_rows")
+    return out
+
+
+def quantize_weight(type_: int, x: np.ndarray) -> np.ndarray:
+    """Encodes f32 rows [n_rows][n_in] as GGUF blocks (Q8_0, Q4_K or Q6_K)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n_rows, n_in = x.shape
+    rb = row_bytes(type_, n_in)
+    if rb == 0:
+        raise ValueError(f"type {type_} cannot hold rows of {n_in}")
+    out = np.zeros(rb * n_rows, np.uint8)
+    _check(load_library().nxg_quantize_weight(type_, _np_ptr(x), n_in, n_rows, _np_ptr(out)), "quantize_weight")
+    return out
+
+
+@dataclass
+class I8Weight:
+    """The reference's i8_weight (src/nexterabert.cpp:256-261): s8 [n_out][n_in] with one
+    float scale and one int32 offset per (256-input block, output row)."""
+    w: np.ndarray        # int8 [n_out][n_in]
+    scale: np.ndarray    # f32 [n_blk][n_out]
+    off: np.ndarray      # i32 [n_blk][n_out]
+
+    @property
+    def n_in(self) -> int:
+        return self.w.shape[1]
+
+    @property
+    def n_out(self) -> int:
+        return self.w.shape[0]
+
+    @property
+    def n_blk(self) -> int:
+        return (self.n_in + BLOCK - 1) // BLOCK
+
+
+def expand_weight(type_: int, data: np.ndarray, n_in: int, n_out: int, act_off: int = 128,
+                  n_threads: int = 0) -> I8Weight:
+    """build_i8_weight: GGUF rows of `type_` -> I8Weight (src/nexterabert.cpp:1010-1049)."""
+    data = np.ascontiguousarray(data)
+    nb = (n_in + BLOCK - 1) // BLOCK
+    w = np.empty((n_out, n_in), np.int8)
+    scale = np.empty((nb, n_out), np.float32)
+    off = np.empty((nb, n_out), np.int32)
+    _check(load_library().nxg_expand_weight(type_, _np_ptr(data), n_in, n_out, act_off, n_threads,
+                                            _np_ptr(w), _np_ptr(scale), _np_ptr(off)), "expand_weight")
+    return I8Weight(w, scale, off)
+
+
+# --- device side -------------------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def _stream_ptr(stream=None) -> Optional[int]:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream or None
+
+
+def init() -> None:
+    """Checks that the current device is a gfx950 GPU (raises otherwise)."""
+    _check(load_library().nxg_init(), "init")
+
+
+class DeviceWeight:
+    """An I8Weight uploaded once into MFMA fragment tiles (nxg_weight)."""
+
+    def __init__(self, weight: I8Weight):
+        L = load_library()
+        w = np.ascontiguousarray(weight.w)
+        s = np.ascontiguousarray(weight.scale)
+        h = ctypes.c_void_p()
+        _check(L.nxg_weight_create(_np_ptr(w), _np_ptr(s), w.shape[1], w.shape[0], ctypes.byref(h)),
+               "weight_create")
+        self._h = h
+        self.n_in, self.n_out = w.shape[1], w.shape[0]
+        self.n_blk = (self.n_in + BLOCK - 1) // BLOCK
+        self.device_bytes = int(L.nxg_weight_device_bytes(h))
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) and self._h.value:
+            load_library().nxg_weight_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+@dataclass
+class QAct:
+    """Quantized activations of T rows (the reference's qact buffer, src/nexterabert.cpp:368-375):
+    q in MFMA fragment tiles (signed: u8 - ACT_OFF) and sx in the reference's scale layout."""
+    q: object            # torch int8, nxg_qact_q_bytes(T, n_in)
+    sx: object           # torch float32, nxg_qact_sx_bytes(T, n_in) / 4
+    T: int
+    n_in: int
+    act_max: int = 127
+
+
+def qact_alloc(T: int, n_in: int, act_max: int = 127, device="cuda") -> QAct:
+    torch = _torch()
+    L = load_library()
+    qb, sb = int(L.nxg_qact_q_bytes(T, n_in)), int(L.nxg_qact_sx_bytes(T, n_in))
+    if T > 0 and (qb == 0 or sb == 0):
+        raise ValueError(f"n_in={n_in} must be a positive multiple of 32")
+    return QAct(torch.empty(max(qb, 1), dtype=torch.int8, device=device),
+                torch.empty(max(sb // 4, 1), dtype=torch.float32, device=device), T, n_in, act_max)
+
+
+def quantize_rows(x, act_max: int = 127, out: Optional[QAct] = None, stream=None) -> QAct:
+    """quantize_row over every row of x (device f32 [T][n_in])."""
+    torch = _torch()
+    if x.dtype != torch.float32 or x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
+        raise ValueError("x must be a contiguous 2-D float32 device tensor")
+    T, n_in = x.shape
+    qa = out if out is not None else qact_alloc(T, n_in, act_max, x.device)
+    qa.T, qa.n_in, qa.act_max = T, n_in, act_max
+    _check(load_library().nxg_quantize_rows(x.data_ptr(), T, n_in, act_max, qa.q.data_ptr(), qa.sx.data_ptr(),
+                                             _stream_ptr(stream)), "quantize_rows")
+    return qa
+
+
+def export_qact(qa: QAct, stream=None):
+    """The qact in the reference's own format: (u8 [T][n_in], sx flat [(T+3)//4][n_blk][4])."""
+    torch = _torch()
+    nb = (qa.n_in + BLOCK - 1) // BLOCK
+    u8 = torch.empty((qa.T, qa.n_in), dtype=torch.uint8, device=qa.q.device)
+    sx = torch.empty(((qa.T + 3) // 4) * nb * 4, dtype=torch.float32, device=qa.q.device)
+    _check(load_library().nxg_qact_export(qa.q.data_ptr(), qa.sx.data_ptr(), qa.T, qa.n_in, qa.act_max,
+                                          u8.data_ptr(), sx.data_ptr(), _stream_ptr(stream)), "qact_export")
+    return u8, sx
+
+
+def _check_rows(t, T, n, name):
+    torch = _torch()
+    if t.dtype != torch.float32 or tuple(t.shape) != (T, n) or not t.is_contiguous() or not t.is_cuda:
+        raise ValueError(f"{name} must be a contiguous float32 device tensor of shape ({T}, {n})")
+
+
+def linear_i8(weight: DeviceWeight, qa: QAct, residual=None, cu_offsets: Optional[Sequence[int]] = None,
+              out=None, stream=None):
+    """op_linear_i8: f32 [T][n_out] = qact x weight^T with the per-block epilogue (+ residual).
+    cu_offsets: the packed batch's cumulative row offsets (n_seqs + 1 entries); T = cu_offsets[-1]."""
+    torch = _torch()
+    if qa.n_in != weight.n_in:
+        raise ValueError(f"n_in mismatch: activations {qa.n_in}, weight {weight.n_in}")
+    T = qa.T
+    if out is None:
+        out = torch.empty((T, weight.n_out), dtype=torch.float32, device=qa.q.device)
+    _check_rows(out, T, weight.n_out, "out")
+    if residual is not None:
+        _check_rows(residual, T, weight.n_out, "residual")
+    L = load_library()
+    res_ptr = residual.data_ptr() if residual is not None else None
+    if cu_offsets is not None:
+        cu = np.ascontiguousarray(cu_offsets, dtype=np.int32)
+        if cu.size < 2 or int(cu[-1]) != T:
+            raise ValueError(f"cu_offsets must end at T={T}")
+        rc = L.nxg_linear_i8(weight.handle, qa.q.data_ptr(), qa.sx.data_ptr(), _np_ptr(cu), cu.size - 1,
+                             res_ptr, out.data_ptr(), _stream_ptr(stream))
+    else:
+        rc = L.nxg_linear_i8_rows(weight.handle, qa.q.data_ptr(), qa.sx.data_ptr(), T, res_ptr,
+                                  out.data_ptr(), _stream_ptr(stream))
+    _check(rc, "linear_i8")
+    return out
+
+
+def block_sums(weight: DeviceWeight, qa: QAct, stream=None):
+    """int32 [n_blk][T][n_out]: the exact per-block sums of the GEMM."""
+    torch = _torch()
+    s = torch.empty((weight.n_blk, qa.T, weight.n_out), dtype=torch.int32, device=qa.q.device)
+    _check(load_library().nxg_linear_i8_block_sums(weight.handle, qa.q.data_ptr(), qa.T, s.data_ptr(),
+                                                   _stream_ptr(stream)), "block_sums")
+    return s
+
+
+def cu_offsets_of(lengths: Sequence[int]) -> np.ndarray:
+    """The packed batch's row offsets (the reference's layout::build, src/nexterabert.cpp:236-243)."""
+    lens = np.asarray(lengths, dtype=np.int64)
+    if lens.size == 0 or (lens <= 0).any():
+        raise ValueError("empty sequence in batch")
+    return np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+
+
+class Builder:
+    """builder::linear of the reference (src/nexterabert.cpp:1121-1143) over device weights.
+
+    Weights registered under their GGUF names run on the int8 GEMM; an f32 input is
+    quantized once and the quantized copy is shared by every linear that reads the
+    same tensor (the reference's qcache, :1068,1125-1129). Weights that the placement
+    rule keeps off the int8 path are not handled here.
+    """
+
+    def __init__(self, weights: Dict[str, DeviceWeight], act_max: int = 127):
+        self.i8 = weights
+        self.act_max = act_max
+        self.qcache: Dict[int, QAct] = {}
+
+    def int8_only(self, names: Sequence[str]) -> bool:
+        return all(n in self.i8 for n in names)
+
+    def quantized(self, x) -> QAct:
+        key = x.data_ptr()
+        qa = self.qcache.get(key)
+        if qa is None or qa.T != x.shape[0] or qa.n_in != x.shape[1]:
+            qa = quantize_rows(x, self.act_max)
+            self.qcache[key] = qa
+        return qa
+
+    def linear(self, name: str, x, residual=None, cu_offsets=None, out=None):
+        w = self.i8.get(name)
+        if w is None:
+            raise KeyError(f"{name} is not an int8 weight")
+        qa = x if isinstance(x, QAct) else self.quantized(x)
+        return linear_i8(w, qa, residual=residual, cu_offsets=cu_offsets, out=out)
+
+    def reset(self) -> None:
+        """Drops the quantized copies (the reference rebuilds its graph per forward)."""
+        self.qcache.clear()

@@ -1,0 +1,640 @@
+// nxg_linear.hip -- gfx950 kernels of the int8 linear path and their C ABI.
+//
+//   quantize_kernel  f32 rows -> int8 fragment tiles + per-(token, 256-block) scales
+//                    (the reference's quantize_row, src/nexterabert.cpp:378-403)
+//   gemm_kernel      v_mfma_i32_16x16x64_i8 GEMM; per 256-input block the int32 tile is
+//                    folded into fp32 accumulators with the reference's epilogue
+//                    f = fma((float) s * sx, sw, f) (src/nexterabert.cpp:909-916,957-958)
+//   export_kernel    int8 tiles -> the reference's u8 row layout
+//
+// Data layouts are described in include/nxg_linear.h. Weights are re-laid out once,
+// at upload, into the same fragment tiles as the activations, so that every copy
+// into LDS is a straight 1 KiB run and every LDS read is one conflict-free
+// ds_read_b128 per lane.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "nxg_linear.h"
+#include "nxg_internal.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr int BLK = NXG_BLOCK;   // inputs per scale block
+constexpr int FRAG = 1024;       // bytes of one 16-row x 64-input fragment
+constexpr int BM = 128;          // GEMM workgroup tile: rows (tokens)
+constexpr int BN = 128;          //                      columns (output features)
+constexpr int NTHREADS = 256;    // 4 waves, 2 x 2, each 64 x 64
+constexpr int STAGE_KS = 2;      // 64-input k-steps per LDS stage
+constexpr int A_STAGE = (BM / 16) * STAGE_KS * FRAG;   // 16 KiB
+constexpr int B_STAGE = (BN / 16) * STAGE_KS * FRAG;   // 16 KiB
+constexpr int N_XCD = 8;         // MI355X: 8 XCDs, workgroups dispatched round-robin
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// quantize
+// ---------------------------------------------------------------------------
+
+// The reference folds |x| with MAXPS (dst = a > b ? a : b, so a NaN operand
+// yields the second operand) over 8 lanes, lane j seeing elements j, j+8, ...
+// The result of such a fold over a sequence S is described by (nan, tail):
+//   nan   S contains a NaN
+//   tail  the fold's result from any start value: max(S) without NaN, else the
+//         max of the elements after the last NaN (NaN if the NaN is last).
+// Folding A then B gives  B.nan ? B.tail : (A.tail is NaN ? B.tail : max(A.tail, B.tail)),
+// an associative combination, so lanes can be reduced in a tree as long as the
+// earlier part stays on the left.
+struct fold {
+    float tail;
+    int   flags;   // bit 0: contains NaN, bit 1: empty
+};
+
+__device__ __forceinline__ float maxps1(float a, float b) { return a > b ? a : b; }
+
+__device__ __forceinline__ fold fold_elem(float a) {
+    fold r;
+    r.tail = a;
+    r.flags = __builtin_isnan(a) ? 1 : 0;
+    return r;
+}
+
+__device__ __forceinline__ fold fold_join(fold a, fold b) {
+    if (b.flags & 2) return a;
+    if (a.flags & 2) return b;
+    fold r;
+    r.flags = (a.flags | b.flags) & 1;
+    r.tail = ((b.flags & 1) || __builtin_isnan(a.tail)) ? b.tail : fmaxf(a.tail, b.tail);
+    return r;
+}
+
+__device__ __forceinline__ float abs_bits(float x) {
+    return __uint_as_float(__float_as_uint(x) & 0x7fffffffu);
+}
+
+// CVTPS2DQ (round to nearest even; NaN or out of int32 range -> 0x80000000),
+// + ACT_OFF with 32-bit wrap-around, then signed-16 and unsigned-8 saturation
+// (PACKSSDW, PACKUSWB), minus ACT_OFF: the reference's u8 as a signed value.
+template <int ACT_MAX>
+__device__ __forceinline__ int quant1(float x, float inv) {
+    const float y = x * inv;
+    int c;
+    if (__builtin_isnan(y) || !(fabsf(y) < 2147483648.0f)) {
+        c = INT32_MIN;
+    } else {
+        c = (int) __builtin_rintf(y);
+    }
+    const int cw = (int) ((unsigned) c + (unsigned) (ACT_MAX + 1));
+    const int u = min(max(cw, 0), 255);
+    return u - (ACT_MAX + 1);
+}
+
+// One workgroup per (16-row group, 256-input block). Wave w quantizes rows
+// 4w..4w+3 of the group; lane l holds 16 consecutive inputs (chunk l % 16) of
+// row 4w + l/16, i.e. one 16-byte piece of an MFMA fragment.
+template <int ACT_MAX>
+__global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict__ x, int T, int n_in, int KS,
+                                                       int n_blk, int8_t * __restrict__ q, float * __restrict__ sx) {
+    const int g = blockIdx.x, B = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rl = wave * 4 + (lane >> 4);
+    const int t = g * 16 + rl;
+    const int c = lane & 15;
+    const int k = B * BLK + c * 16;
+    const bool present = t < T && k < n_in;
+
+    float xv[16];   // the inputs as read
+    if (present) {
+        const v4f * src = reinterpret_cast<const v4f *>(x + (size_t) t * n_in + k);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const v4f f = __builtin_nontemporal_load(src + i);
+            xv[4 * i + 0] = f.x; xv[4 * i + 1] = f.y; xv[4 * i + 2] = f.z; xv[4 * i + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xv[i] = 0.0f;
+    }
+    float v[16];    // |x|
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = abs_bits(xv[i]);
+
+    bool any_nan = false;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) any_nan |= __builtin_isnan(v[i]);
+
+    float amax;
+    if (!__any(any_nan)) {
+        // No NaN in this wave: the fold is the plain maximum.
+        float m = v[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) m = fmaxf(m, v[i]);
+#pragma unroll
+        for (int s = 1; s < 16; s <<= 1) m = fmaxf(m, __shfl_xor(m, s));
+        amax = m;
+    } else {
+        // Exact MAXPS semantics. Element 16c + e is AVX lane e % 8, position 2c + e / 8.
+        fold f[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (present) {
+                f[j] = fold_join(fold_elem(v[j]), fold_elem(v[j + 8]));
+            } else {
+                f[j].tail = 0.0f;
+                f[j].flags = 2;
+            }
+        }
+#pragma unroll
+        for (int s = 1; s < 16; s <<= 1) {
+            const bool upper = (c & s) != 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                fold o;
+                o.tail = __shfl_xor(f[j].tail, s);
+                o.flags = __shfl_xor(f[j].flags, s);
+                f[j] = upper ? fold_join(o, f[j]) : fold_join(f[j], o);
+            }
+        }
+        // Horizontal tree of the reference: lanes (j, j+4), then (0,2), (1,3), then (0,1).
+        float m[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m[j] = maxps1(f[j].tail, f[j + 4].tail);
+        amax = maxps1(maxps1(m[0], m[2]), maxps1(m[1], m[3]));
+        if (t >= T) amax = 0.0f;
+    }
+
+    const float scale = amax / (float) ACT_MAX;
+    const float inv = amax > 0.0f ? (float) ACT_MAX / amax : 0.0f;
+
+    const int KP = KS * 64;
+    if (k < KP) {
+        int packed[4] = { 0, 0, 0, 0 };
+        if (present) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int b0 = quant1<ACT_MAX>(xv[4 * i + 0], inv) & 0xff;
+                const int b1 = quant1<ACT_MAX>(xv[4 * i + 1], inv) & 0xff;
+                const int b2 = quant1<ACT_MAX>(xv[4 * i + 2], inv) & 0xff;
+                const int b3 = quant1<ACT_MAX>(xv[4 * i + 3], inv) & 0xff;
+                packed[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            }
+        }
+        const size_t dst = ((size_t) g * KS + (k >> 6)) * FRAG + (size_t) (rl + 16 * ((k & 63) >> 4)) * 16;
+        *reinterpret_cast<int4 *>(q + dst) = make_int4(packed[0], packed[1], packed[2], packed[3]);
+    }
+    if (c == 0) {
+        sx[((size_t) (t >> 2) * n_blk + B) * 4 + (t & 3)] = t < T ? scale : 0.0f;
+    }
+}
+
+// int8 tiles -> the reference's u8 rows (q + act_off); one thread per 16 bytes.
+__global__ void export_kernel(const int8_t * __restrict__ q, int T, int n_in, int KS, int act_off,
+                              uint8_t * __restrict__ u8) {
+    const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int chunks = n_in / 16;
+    if (i >= (size_t) T * chunks) return;
+    const int t = (int) (i / chunks), k = (int) (i % chunks) * 16;
+    const size_t src = ((size_t) (t >> 4) * KS + (k >> 6)) * FRAG + (size_t) ((t & 15) + 16 * ((k & 63) >> 4)) * 16;
+    const int4 v = *reinterpret_cast<const int4 *>(q + src);
+    const int w[4] = { v.x, v.y, v.z, v.w };
+    int o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        int r = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int s = (int) (int8_t) (w[j] >> (8 * b));
+            r |= ((s + act_off) & 0xff) << (8 * b);
+        }
+        o[j] = r;
+    }
+    *reinterpret_cast<int4 *>(u8 + (size_t) t * n_in + k) = make_int4(o[0], o[1], o[2], o[3]);
+}
+
+// ---------------------------------------------------------------------------
+// GEMM
+// ---------------------------------------------------------------------------
+
+struct gemm_params {
+    const int8_t * a;     // qact tiles
+    const float *  sx;    // [MP/4][n_blk][4]
+    const int8_t * w;     // weight tiles, NP rows
+    const float *  sw;    // [n_blk][NP]
+    const float *  res;   // [T][N] or null
+    float *        out;   // [T][N]
+    int32_t *      sums;  // [n_blk][T][N] (block-sum variant)
+    int T, N, NP, KS, n_blk, MF, n_mt, n_nt;
+};
+
+// Workgroup index -> tile index. Workgroups go to the XCDs round-robin; this
+// gives each XCD a contiguous range of tiles, and tiles are numbered with the
+// column tile fastest, so the workgroups of one XCD share row tiles in its L2.
+__device__ __forceinline__ int xcd_tile(int bid, int G) {
+    const int xcd = bid % N_XCD, idx = bid / N_XCD;
+    const int q = G / N_XCD, r = G % N_XCD;
+    return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+}
+
+template <bool RES, bool SUMS, bool K256>
+__global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[2][A_STAGE + B_STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int tile = xcd_tile(blockIdx.x, p.n_mt * p.n_nt);
+    const int mt = tile / p.n_nt, nt = tile % p.n_nt;
+    const int m0 = mt * BM, n0 = nt * BN;
+
+    // Copy roles: this thread moves one 16-byte piece of 4 A and 4 B fragments
+    // per stage; fragment fi = wave + 4u holds local frag row fi / 2, k-step fi % 2.
+    const int cj = wave & 1;
+    const int8_t * a_src[4];
+    const int8_t * b_src[4];
+    bool a_ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int fl = (wave >> 1) + 2 * u;
+        const int mf = mt * (BM / 16) + fl;
+        a_ok[u] = mf < p.MF;
+        a_src[u] = p.a + ((size_t) (a_ok[u] ? mf : 0) * p.KS + cj) * FRAG + lane * 16;
+        b_src[u] = p.w + ((size_t) (nt * (BN / 16) + fl) * p.KS + cj) * FRAG + lane * 16;
+    }
+    const int lds_off = (wave + 0) * FRAG + lane * 16;   // + 4u * FRAG
+
+    // Epilogue roles: rows m0 + wm*64 + mi*16 + 4*(lane/16) + r, columns n0 + wn*64 + ni*16 + lane%16.
+    const int row_base = m0 + wm * 64 + 4 * (lane >> 4);
+    const int col_base = n0 + wn * 64 + (lane & 15);
+
+    v4i acc[4][4];
+    float f[4][4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) f[i][j][r] = 0.0f;
+
+    v4i stA[4], stB[4];
+    auto load_stage = [&](int ks) {   // global -> registers, k-steps ks + cj
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const bool ok = a_ok[u] && (K256 || ks + cj < p.KS);
+            stA[u] = ok ? *reinterpret_cast<const v4i *>(a_src[u] + (size_t) ks * FRAG) : v4i{0, 0, 0, 0};
+            stB[u] = (K256 || ks + cj < p.KS) ? *reinterpret_cast<const v4i *>(b_src[u] + (size_t) ks * FRAG)
+                                              : v4i{0, 0, 0, 0};
+        }
+    };
+    auto store_stage = [&](int buf) {   // registers -> LDS
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            *reinterpret_cast<v4i *>(&lds[buf][lds_off + 4 * u * FRAG]) = stA[u];
+            *reinterpret_cast<v4i *>(&lds[buf][A_STAGE + lds_off + 4 * u * FRAG]) = stB[u];
+        }
+    };
+    auto mma_stage = [&](int buf, bool first, int nks) {
+#pragma unroll
+        for (int j = 0; j < STAGE_KS; ++j) {
+            if (!K256 && j >= nks) break;
+            v4i a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[i] = *reinterpret_cast<const v4i *>(&lds[buf][((wm * 4 + i) * 2 + j) * FRAG + lane * 16]);
+                b[i] = *reinterpret_cast<const v4i *>(&lds[buf][A_STAGE + ((wn * 4 + i) * 2 + j) * FRAG + lane * 16]);
+            }
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni)
+                    acc[mi][ni] = (first && j == 0)
+                        ? __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], v4i{0, 0, 0, 0}, 0, 0, 0)
+                        : __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
+        }
+    };
+
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+
+    for (int B = 0; B < p.n_blk; ++B) {
+        const int ks0 = 4 * B;
+        const int nks = K256 ? 4 : min(4, p.KS - ks0);
+
+        // Scales of this block, fetched early; used after its last k-step.
+        float4 sxv[4];
+        float swv[4];
+        if (!SUMS) {
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                const int tr = row_base + mi * 16;
+                sxv[mi] = (tr >> 4) < p.MF
+                    ? *reinterpret_cast<const float4 *>(p.sx + ((size_t) (tr >> 2) * p.n_blk + B) * 4)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) swv[ni] = p.sw[(size_t) B * p.NP + col_base + ni * 16];
+        }
+
+        // first half of the block: k-steps ks0, ks0 + 1 (in buffer 0)
+        const bool two_stages = K256 || nks > 2;
+        if (two_stages) load_stage(ks0 + 2);
+        mma_stage(0, true, K256 ? 2 : min(2, nks));
+        if (two_stages) {
+            store_stage(1);
+            __syncthreads();
+            const bool more = B + 1 < p.n_blk;
+            if (more) load_stage(ks0 + 4);
+            mma_stage(1, false, K256 ? 2 : nks - 2);
+            if (more) store_stage(0);
+        } else {
+            const bool more = B + 1 < p.n_blk;
+            if (more) load_stage(ks0 + 4);   // unreachable for the last block; kept for symmetry
+            __syncthreads();
+            if (more) store_stage(0);
+        }
+
+        if (SUMS) {
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int t = row_base + mi * 16 + r, n = col_base + ni * 16;
+                        if (t < p.T && n < p.N) p.sums[((size_t) B * p.T + t) * p.N + n] = acc[mi][ni][r];
+                    }
+        } else {
+            // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                const float sxr[4] = { sxv[mi].x, sxv[mi].y, sxv[mi].z, sxv[mi].w };
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float prod = (float) acc[mi][ni][r] * sxr[r];
+                        f[mi][ni][r] = __builtin_fmaf(prod, swv[ni], f[mi][ni][r]);
+                    }
+            }
+        }
+        __syncthreads();
+    }
+
+    if (!SUMS) {
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = row_base + mi * 16 + r;
+                if (t >= p.T) continue;
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) {
+                    const int n = col_base + ni * 16;
+                    if (n >= p.N) continue;
+                    const size_t o = (size_t) t * p.N + n;
+                    const float y = RES ? p.res[o] + f[mi][ni][r] : f[mi][ni][r];
+                    __builtin_nontemporal_store(y, p.out + o);
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+int fail(int code, const char * fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char * fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    nxg_set_error(buf);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char * what) {
+    return fail(NXG_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+int check_device() {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    static thread_local int checked_dev = -1;
+    if (checked_dev == dev) return NXG_OK;
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        return fail(NXG_EDEVICE, "device %d is %s; this engine is built for gfx950 (MI355X)", dev, prop.gcnArchName);
+    }
+    checked_dev = dev;
+    return NXG_OK;
+}
+
+int launch_check(const char * what) {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? NXG_OK : hip_fail(e, what);
+}
+
+struct qact_dims {
+    int T, n_in, KS, n_blk, MP;
+};
+
+bool qact_dims_of(int T, int n_in, qact_dims & d) {
+    if (T < 0 || n_in <= 0 || n_in % 32 != 0) return false;
+    d.T = T;
+    d.n_in = n_in;
+    d.KS = ceil_div(n_in, 64);
+    d.n_blk = ceil_div(n_in, BLK);
+    d.MP = ceil_div(T, 16) * 16;
+    return true;
+}
+
+} // namespace
+
+struct nxg_weight {
+    int32_t n_in = 0, n_out = 0, n_blk = 0, KS = 0, NP = 0;
+    int8_t * w = nullptr;    // NP x KS*64 bytes in fragment tiles
+    float *  sw = nullptr;   // [n_blk][NP]
+    size_t   bytes = 0;
+};
+
+extern "C" {
+
+int32_t nxg_init(void) { return check_device(); }
+
+size_t nxg_qact_q_bytes(int32_t T, int32_t n_in) {
+    qact_dims d;
+    return qact_dims_of(T, n_in, d) ? (size_t) d.MP * d.KS * 64 : 0;
+}
+
+size_t nxg_qact_sx_bytes(int32_t T, int32_t n_in) {
+    qact_dims d;
+    return qact_dims_of(T, n_in, d) ? (size_t) d.MP * d.n_blk * sizeof(float) : 0;
+}
+
+int32_t nxg_quantize_rows(const float * x, int32_t T, int32_t n_in, int32_t act_max,
+                          int8_t * q, float * sx, void * stream) {
+    qact_dims d;
+    if (!qact_dims_of(T, n_in, d)) return fail(NXG_EINVAL, "quantize: T=%d n_in=%d (n_in must be a positive multiple of 32)", T, n_in);
+    if (act_max != 127 && act_max != 63) return fail(NXG_EINVAL, "quantize: act_max must be 127 or 63, got %d", act_max);
+    if (T == 0) return NXG_OK;
+    if (!x || !q || !sx) return fail(NXG_EINVAL, "quantize: null buffer");
+    int rc = check_device();
+    if (rc) return rc;
+    const dim3 grid(d.MP / 16, d.n_blk);
+    hipStream_t s = (hipStream_t) stream;
+    if (act_max == 127) {
+        quantize_kernel<127><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
+    } else {
+        quantize_kernel<63><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
+    }
+    return launch_check("quantize_kernel");
+}
+
+int32_t nxg_qact_export(const int8_t * q, const float * sx, int32_t T, int32_t n_in, int32_t act_max,
+                        uint8_t * u8, float * sx_ref, void * stream) {
+    qact_dims d;
+    if (!qact_dims_of(T, n_in, d)) return fail(NXG_EINVAL, "export: T=%d n_in=%d", T, n_in);
+    if (act_max != 127 && act_max != 63) return fail(NXG_EINVAL, "export: act_max must be 127 or 63");
+    if (T == 0) return NXG_OK;
+    if (!q || !sx || !u8 || !sx_ref) return fail(NXG_EINVAL, "export: null buffer");
+    int rc = check_device();
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t) stream;
+    const size_t n = (size_t) T * (n_in / 16);
+    export_kernel<<<(unsigned) ((n + 255) / 256), 256, 0, s>>>(q, T, n_in, d.KS, act_max + 1, u8);
+    rc = launch_check("export_kernel");
+    if (rc) return rc;
+    const size_t sx_n = (size_t) ((T + 3) / 4) * d.n_blk * 4;
+    const hipError_t e = hipMemcpyAsync(sx_ref, sx, sx_n * sizeof(float), hipMemcpyDeviceToDevice, s);
+    return e == hipSuccess ? NXG_OK : hip_fail(e, "export: hipMemcpyAsync");
+}
+
+int32_t nxg_weight_create(const int8_t * w, const float * scale, int32_t n_in, int32_t n_out, nxg_weight ** out) {
+    if (!out) return fail(NXG_EINVAL, "weight_create: null out");
+    *out = nullptr;
+    if (!w || !scale) return fail(NXG_EINVAL, "weight_create: null input");
+    if (n_in <= 0 || n_in % 32 != 0 || n_out <= 0) {
+        return fail(NXG_EINVAL, "weight_create: n_in=%d n_out=%d (n_in must be a positive multiple of 32)", n_in, n_out);
+    }
+    int rc = check_device();
+    if (rc) return rc;
+    nxg_weight * W = new nxg_weight();
+    W->n_in = n_in;
+    W->n_out = n_out;
+    W->n_blk = ceil_div(n_in, BLK);
+    W->KS = ceil_div(n_in, 64);
+    W->NP = ceil_div(n_out, BN) * BN;
+    const size_t wbytes = (size_t) W->NP * W->KS * 64;
+    const size_t sbytes = (size_t) W->n_blk * W->NP * sizeof(float);
+    // Re-layout on the host into fragment tiles (zero padding), then one copy.
+    std::vector<int8_t> tiled(wbytes, 0);
+    nxg_tile_rows(w, n_out, n_in, W->KS, tiled.data());
+    std::vector<float> sw((size_t) W->n_blk * W->NP, 0.0f);
+    for (int B = 0; B < W->n_blk; ++B) {
+        std::memcpy(&sw[(size_t) B * W->NP], scale + (size_t) B * n_out, sizeof(float) * n_out);
+    }
+    hipError_t e = hipMalloc((void **) &W->w, wbytes);
+    if (e != hipSuccess) { delete W; return fail(NXG_ENOMEM, "weight_create: hipMalloc(%zu): %s", wbytes, hipGetErrorString(e)); }
+    e = hipMalloc((void **) &W->sw, sbytes);
+    if (e != hipSuccess) { (void) hipFree(W->w); delete W; return fail(NXG_ENOMEM, "weight_create: hipMalloc(%zu): %s", sbytes, hipGetErrorString(e)); }
+    e = hipMemcpy(W->w, tiled.data(), wbytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(W->sw, sw.data(), sbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) { nxg_weight_destroy(W); return hip_fail(e, "weight_create: hipMemcpy"); }
+    W->bytes = wbytes + sbytes;
+    *out = W;
+    return NXG_OK;
+}
+
+void nxg_weight_destroy(nxg_weight * W) {
+    if (!W) return;
+    if (W->w) (void) hipFree(W->w);
+    if (W->sw) (void) hipFree(W->sw);
+    delete W;
+}
+
+int32_t nxg_weight_n_in(const nxg_weight * W) { return W ? W->n_in : 0; }
+int32_t nxg_weight_n_out(const nxg_weight * W) { return W ? W->n_out : 0; }
+size_t nxg_weight_device_bytes(const nxg_weight * W) { return W ? W->bytes : 0; }
+
+static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float * sx, int32_t T,
+                           const float * residual, float * out, int32_t * sums, void * stream) {
+    if (!W) return fail(NXG_EINVAL, "linear: null weight");
+    if (T < 0) return fail(NXG_EINVAL, "linear: T=%d", T);
+    if (T == 0) return NXG_OK;
+    if (!q || (!sums && (!sx || !out))) return fail(NXG_EINVAL, "linear: null buffer");
+    int rc = check_device();
+    if (rc) return rc;
+    gemm_params p;
+    p.a = q;
+    p.sx = sx;
+    p.w = W->w;
+    p.sw = W->sw;
+    p.res = residual;
+    p.out = out;
+    p.sums = sums;
+    p.T = T;
+    p.N = W->n_out;
+    p.NP = W->NP;
+    p.KS = W->KS;
+    p.n_blk = W->n_blk;
+    p.MF = ceil_div(T, 16);
+    p.n_mt = ceil_div(T, BM);
+    p.n_nt = W->NP / BN;
+    const long long G = (long long) p.n_mt * p.n_nt;
+    if (G > INT32_MAX) return fail(NXG_EINVAL, "linear: T=%d too large", T);
+    hipStream_t s = (hipStream_t) stream;
+    const bool k256 = W->KS % 4 == 0;
+    const dim3 grid((unsigned) G), block(NTHREADS);
+    if (sums) {
+        if (k256) gemm_kernel<false, true, true><<<grid, block, 0, s>>>(p);
+        else      gemm_kernel<false, true, false><<<grid, block, 0, s>>>(p);
+    } else if (residual) {
+        if (k256) gemm_kernel<true, false, true><<<grid, block, 0, s>>>(p);
+        else      gemm_kernel<true, false, false><<<grid, block, 0, s>>>(p);
+    } else {
+        if (k256) gemm_kernel<false, false, true><<<grid, block, 0, s>>>(p);
+        else      gemm_kernel<false, false, false><<<grid, block, 0, s>>>(p);
+    }
+    return launch_check("gemm_kernel");
+}
+
+int32_t nxg_linear_i8_rows(const nxg_weight * W, const int8_t * q, const float * sx, int32_t T,
+                           const float * residual, float * out, void * stream) {
+    return launch_gemm(W, q, sx, T, residual, out, nullptr, stream);
+}
+
+int32_t nxg_linear_i8(const nxg_weight * W, const int8_t * q, const float * sx,
+                      const int32_t * cu_offsets, int32_t n_seqs,
+                      const float * residual, float * out, void * stream) {
+    if (!cu_offsets || n_seqs <= 0) return fail(NXG_EINVAL, "linear: need cu_offsets and n_seqs >= 1");
+    if (cu_offsets[0] != 0) return fail(NXG_EINVAL, "linear: cu_offsets[0] = %d, expected 0", cu_offsets[0]);
+    for (int i = 0; i < n_seqs; ++i) {
+        if (cu_offsets[i + 1] <= cu_offsets[i]) {
+            return fail(NXG_EINVAL, "linear: empty or negative sequence %d (cu_offsets %d -> %d)", i,
+                        cu_offsets[i], cu_offsets[i + 1]);
+        }
+    }
+    return launch_gemm(W, q, sx, cu_offsets[n_seqs], residual, out, nullptr, stream);
+}
+
+int32_t nxg_linear_i8_block_sums(const nxg_weight * W, const int8_t * q, int32_t T, int32_t * sums, void * stream) {
+    if (!sums) return fail(NXG_EINVAL, "block_sums: null output");
+    return launch_gemm(W, q, nullptr, T, nullptr, nullptr, sums, stream);
+}
+
+} // extern "C"

@@ -1,0 +1,162 @@
+"""numpy front end of the CPU oracle (liboracle.so, built from nx_oracle.cpp).
+
+TEST INFRASTRUCTURE ONLY: imported by the tests, the smoke check and the
+CPU-baseline leg of bench.py, as the checker. The product never imports it.
+
+Array conventions follow the reference's int8 path (src/nexterabert.cpp):
+  activations  x   f32 [T][n_in]
+  quantized    q   u8  [T][n_in]  (value + ACT_OFF)
+               sx  f32 [(T+3)//4][n_blk][4]  flattened  (src/nexterabert.cpp:372-375)
+  weights      w   s8  [n_out][n_in]
+               scale f32 [n_blk][n_out], off i32 [n_blk][n_out]  (src/nexterabert.cpp:256-261)
+  output       y   f32 [T][n_out]
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "liboracle.so"
+_lib = None
+
+BLOCK = 256
+
+
+def build(force: bool = False) -> Path:
+    """Compile liboracle.so with the Makefile next to this file."""
+    if force or not _LIB_PATH.exists():
+        subprocess.run(["make", "-s", "-B" if force else "liboracle.so"], cwd=_HERE, check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(_LIB_PATH))
+        P = ctypes.c_void_p
+        i32 = ctypes.c_int
+        L.orc_n_blocks.argtypes, L.orc_n_blocks.restype = [i32], i32
+        L.orc_qact_bytes.argtypes, L.orc_qact_bytes.restype = [i32, i32], ctypes.c_size_t
+        L.orc_quantize_rows_scalar.argtypes = [P, i32, i32, i32, P, P]
+        L.orc_quantize_rows_scalar.restype = None
+        L.orc_quantize_rows_simd.argtypes = [P, i32, i32, i32, P, P]
+        L.orc_quantize_rows_simd.restype = i32
+        L.orc_expand_rows.argtypes = [P, i32, i32, i32, P, P, P]
+        L.orc_expand_rows.restype = None
+        L.orc_dequant_q8_0.argtypes = [P, ctypes.c_int64, P]
+        L.orc_dequant_q8_0.restype = None
+        L.orc_block_sums.argtypes = [P, P, i32, i32, P, i32, P]
+        L.orc_block_sums.restype = None
+        L.orc_linear_scalar.argtypes = [P, P, P, i32, i32, P, P, i32, P, P]
+        L.orc_linear_scalar.restype = None
+        L.orc_linear_simd.argtypes = [P, P, P, i32, i32, P, P, i32, P, P, i32]
+        L.orc_linear_simd.restype = i32
+        L.orc_vnni_flavour.argtypes, L.orc_vnni_flavour.restype = [], ctypes.c_char_p
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def n_blocks(n_in: int) -> int:
+    return (n_in + BLOCK - 1) // BLOCK
+
+
+def sx_index(t: int, B: int, n_blk: int) -> int:
+    return ((t // 4) * n_blk + B) * 4 + t % 4
+
+
+def sx_len(T: int, n_in: int) -> int:
+    return ((T + 3) // 4) * n_blocks(n_in) * 4
+
+
+def sx_matrix(sx: np.ndarray, T: int, n_in: int) -> np.ndarray:
+    """The flat [(T+3)//4][n_blk][4] scale layout as a [T][n_blk] matrix."""
+    nb = n_blocks(n_in)
+    g = sx.reshape((T + 3) // 4, nb, 4).transpose(0, 2, 1).reshape(-1, nb)
+    return g[:T]
+
+
+def quantize_rows(x: np.ndarray, act_max: int = 127, simd: bool = False):
+    """quantize_row over every row of x (src/nexterabert.cpp:378-403). Returns (q u8, sx flat)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, n_in = x.shape
+    assert n_in % 8 == 0
+    q = np.empty((T, n_in), np.uint8)
+    sx = np.zeros(sx_len(T, n_in), np.float32)
+    if simd:
+        rc = lib().orc_quantize_rows_simd(_p(x), T, n_in, act_max, _p(q), _p(sx))
+        if rc != 0:
+            raise RuntimeError("AVX2 not available on this CPU")
+    else:
+        lib().orc_quantize_rows_scalar(_p(x), T, n_in, act_max, _p(q), _p(sx))
+    return q, sx
+
+
+def expand_rows(rows: np.ndarray, act_off: int = 128):
+    """build_i8_weight on dequantized f32 rows (src/nexterabert.cpp:1030-1042)."""
+    rows = np.ascontiguousarray(rows, dtype=np.float32)
+    n_out, n_in = rows.shape
+    nb = n_blocks(n_in)
+    w = np.empty((n_out, n_in), np.int8)
+    scale = np.empty((nb, n_out), np.float32)
+    off = np.empty((nb, n_out), np.int32)
+    lib().orc_expand_rows(_p(rows), n_in, n_out, act_off, _p(w), _p(scale), _p(off))
+    return w, scale, off
+
+
+def dequant_q8_0(data: np.ndarray, n: int) -> np.ndarray:
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    assert data.size == n // 32 * 34
+    out = np.empty(n, np.float32)
+    lib().orc_dequant_q8_0(_p(data), n, _p(out))
+    return out
+
+
+def block_sums(w, off, q) -> np.ndarray:
+    """Per-block int32 sums [n_blk][T][n_out] = sum w8*u8 + off."""
+    n_out, n_in = w.shape
+    T = q.shape[0]
+    s = np.empty((n_blocks(n_in), T, n_out), np.int32)
+    lib().orc_block_sums(_p(w), _p(off), n_in, n_out, _p(q), T, _p(s))
+    return s
+
+
+def linear(w, scale, off, q, sx, res=None, simd: bool = False, n_threads: int = 1) -> np.ndarray:
+    """op_linear_i8 (src/nexterabert.cpp:969-1007). Returns f32 [T][n_out]."""
+    n_out, n_in = w.shape
+    T = q.shape[0]
+    out = np.empty((T, n_out), np.float32)
+    if res is not None:
+        res = np.ascontiguousarray(res, dtype=np.float32)
+        assert res.shape == (T, n_out)
+    args = (_p(w), _p(scale), _p(off), n_in, n_out, _p(q), _p(sx), T, _p(res), _p(out))
+    if simd:
+        rc = lib().orc_linear_simd(*args, n_threads)
+        if rc != 0:
+            raise RuntimeError(f"orc_linear_simd failed ({rc}): no VNNI on this CPU or n_in % 32 != 0")
+    else:
+        lib().orc_linear_scalar(*args)
+    return out
+
+
+def vnni_flavour() -> str:
+    return lib().orc_vnni_flavour().decode()
+
+
+def default_threads() -> int:
+    """The reference's default pool size: all cores but ~10% (src/nexterabert.cpp:1519-1524)."""
+    try:
+        hw = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        hw = os.cpu_count() or 1
+    return max(1, hw - hw // 10)
