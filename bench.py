@@ -1,0 +1,352 @@
+#!/usr/bin/env python3
+"""Benchmark of the int8 linear path of NexteraBERT.cpp on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--rows M] [--no-cpu]
+
+A step is one pass of the path over every int8 projection of the 18-layer encoder
+for one packed batch of M rows (default 65,536: one long sequence): for each layer,
+each distinct activation a linear reads is quantized once (the reference's
+quantize_row), then every projection runs the W8A8 GEMM with the per-block fp32
+epilogue (+ residual where the reference adds one). Projections that read the same
+activation are concatenated along N into one GEMM (exact per output column), so
+the 140 linears run as 92 GEMMs. HRA q/k/v run on M/4 block rows. Weights are
+N(0, 0.02), Q8_0-encoded, expanded to int8 on the host; activations N(0, 1); all
+inputs are resident in HBM before timing starts.
+
+Output: one JSON line. `value` is int8 TOPS of the whole step (quantization
+included, 2 ops per MAC of the GEMMs); `roofline` describes the GEMM kernel from
+HIP events around every GEMM launch of the timed steps; `cpu_baseline` times the
+CPU oracle (the same path on VPDPBUSD, the reference's instruction) on a row
+sample on this host. The 1,024-token encoder line is the same path at M=1024,
+replayed from a HIP graph.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "int8 linear TOPS (% of MFMA peak) + encoder tokens/s at 1,024-token seqs"
+PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POPS
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class LinearPath:
+    """Every int8 projection of the encoder over M packed rows, on device buffers."""
+
+    def __init__(self, nxg, M: int, fuse: bool = True, weights=None, seed: int = 0):
+        import torch
+        import nexterabert_cpp_amd.model as model
+        self.nxg, self.torch, self.M = nxg, torch, M
+        rng = np.random.default_rng(seed)
+        gen = torch.Generator(device="cuda").manual_seed(seed)
+        self.layers = []
+        self.host_weights = {}
+        self.dev_weights = {} if weights is None else weights
+        self.inputs, self.qacts, self.outs = {}, {}, {}
+        rows_block = (M + model.HRA_BLOCK - 1) // model.HRA_BLOCK
+        self.residual = torch.randn(M, model.N_EMBD, device="cuda", generator=gen)
+        self.ops = 0
+        self.gemm_bytes = 0
+        self.quant_bytes = 0
+        for l, kind in enumerate(model.BLOCK_TYPES):
+            steps = []
+            seen = set()
+            for g in model.layer_groups(l, kind, fuse):
+                rows = rows_block if g.block_rows else M
+                key = (g.input, g.n_in, rows)
+                if key not in self.inputs:
+                    self.inputs[key] = torch.randn(rows, g.n_in, device="cuda", generator=gen)
+                    self.qacts[key] = nxg.qact_alloc(rows, g.n_in)
+                okey = (g.n_out, rows)
+                if okey not in self.outs:
+                    self.outs[okey] = torch.empty(rows, g.n_out, device="cuda")
+                wname = g.name if len(g.specs) == 1 else f"blocks.{l}.{g.name}"
+                if wname not in self.dev_weights:
+                    parts = []
+                    for s in g.specs:
+                        rows_f = (0.02 * rng.standard_normal((s.n_out, s.n_in))).astype(np.float32)
+                        data = nxg.quantize_weight(nxg.TYPE_Q8_0, rows_f)
+                        parts.append(nxg.expand_weight(nxg.TYPE_Q8_0, data, s.n_in, s.n_out))
+                    W = nxg.I8Weight(np.concatenate([p.w for p in parts]),
+                                     np.ascontiguousarray(np.concatenate([p.scale for p in parts], 1)),
+                                     np.ascontiguousarray(np.concatenate([p.off for p in parts], 1)))
+                    self.host_weights[wname] = W
+                    self.dev_weights[wname] = nxg.DeviceWeight(W)
+                first = key not in seen
+                seen.add(key)
+                res = g.residual
+                steps.append((key, first, wname, okey, res, g))
+                self.ops += 2 * rows * g.n_in * g.n_out
+                nb = (g.n_in + 255) // 256
+                self.gemm_bytes += (rows * g.n_in + 4 * rows * nb + g.n_out * g.n_in + 4 * g.n_out * nb
+                                    + 4 * rows * g.n_out * (2 if res else 1))
+                if first:
+                    self.quant_bytes += 5 * rows * g.n_in + 4 * rows * nb
+            self.layers.append(steps)
+        self.n_gemm = sum(len(s) for s in self.layers)
+        self.n_quant = sum(1 for s in self.layers for st in s if st[1])
+
+    def step(self, gemm_events=None, quant_events=None):
+        nxg, torch = self.nxg, self.torch
+        for steps in self.layers:
+            for key, first, wname, okey, res, g in steps:
+                qa = self.qacts[key]
+                if first:
+                    if quant_events is not None:
+                        e0 = torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                    nxg.quantize_rows(self.inputs[key], out=qa)
+                    if quant_events is not None:
+                        e1 = torch.cuda.Event(enable_timing=True)
+                        e1.record()
+                        quant_events.append((e0, e1))
+                if gemm_events is not None:
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                nxg.linear_i8(self.dev_weights[wname], qa, residual=self.residual if res else None,
+                              out=self.outs[okey])
+                if gemm_events is not None:
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e1.record()
+                    gemm_events.append((e0, e1, g))
+
+
+def time_steps(path, steps: int, warmup: int):
+    torch = path.torch
+    for _ in range(warmup):
+        path.step()
+    torch.cuda.synchronize()
+    gemm_ev, quant_ev = [], []
+    t0 = time.perf_counter()
+    s0 = torch.cuda.Event(enable_timing=True)
+    s1 = torch.cuda.Event(enable_timing=True)
+    s0.record()
+    for _ in range(steps):
+        path.step(gemm_ev, quant_ev)
+    s1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = s0.elapsed_time(s1)
+    gemm_ms = sum(a.elapsed_time(b) for a, b, _ in gemm_ev)
+    quant_ms = sum(a.elapsed_time(b) for a, b in quant_ev)
+    return total_ms / steps, wall / steps * 1e3, gemm_ms / steps, quant_ms / steps, gemm_ev
+
+
+def time_graph(path, steps: int, warmup: int):
+    """The step captured once in a HIP graph and replayed; checked against eager."""
+    torch = path.torch
+    path.step()
+    torch.cuda.synchronize()
+    eager = {k: v.clone() for k, v in path.outs.items()}
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        path.step()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        path.step()
+    for _ in range(max(1, warmup)):
+        g.replay()
+    torch.cuda.synchronize()
+    for k, v in path.outs.items():
+        if not torch.equal(v.view(torch.int32), eager[k].view(torch.int32)):
+            raise RuntimeError("graph replay differs from eager execution")
+    s0 = torch.cuda.Event(enable_timing=True)
+    s1 = torch.cuda.Event(enable_timing=True)
+    s0.record()
+    for _ in range(steps):
+        g.replay()
+    s1.record()
+    torch.cuda.synchronize()
+    return s0.elapsed_time(s1) / steps
+
+
+def cpu_baseline(path, rows: int, reps: int):
+    """The CPU oracle (VPDPBUSD GEMM + AVX2 quantizer, threaded like the reference's pool)
+    over the same 92 GEMMs at `rows` rows (HRA block rows at rows/4)."""
+    from oracle import oracle as orc
+    import nexterabert_cpp_amd.model as model
+    orc.build()
+    if not orc.vnni_flavour():
+        return None
+    try:
+        hw = len(os.sched_getaffinity(0))
+    except AttributeError:
+        hw = os.cpu_count() or 1
+    n_threads = min(16, hw)
+    n_threads = max(1, n_threads - n_threads // 10)
+    rng = np.random.default_rng(1)
+    rb = (rows + 3) // 4
+    xs = {}
+    for steps in path.layers:
+        for key, first, wname, okey, res, g in steps:
+            r = rb if g.block_rows else rows
+            k = (key[0], key[1], r)
+            if k not in xs:
+                xs[k] = rng.standard_normal((r, key[1])).astype(np.float32)
+    resid = rng.standard_normal((rows, model.N_EMBD)).astype(np.float32)
+    ops = 0
+
+    def one_pass():
+        nonlocal ops
+        ops = 0
+        for steps in path.layers:
+            q = {}
+            for key, first, wname, okey, res, g in steps:
+                r = rb if g.block_rows else rows
+                k = (key[0], key[1], r)
+                if k not in q:
+                    q[k] = orc.quantize_rows(xs[k], simd=True, n_threads=n_threads)
+                W = path.host_weights[wname]
+                orc.linear(W.w, W.scale, W.off, q[k][0], q[k][1], res=resid if res else None,
+                           simd=True, n_threads=n_threads)
+                ops += 2 * r * g.n_in * g.n_out
+
+    one_pass()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        one_pass()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(ops / med / 1e12, 4),
+        "unit": "TOPS",
+        "cores": n_threads,
+        "kind": "port",
+        "sample": (f"all 140 encoder int8 linears as 92 GEMMs + activation quantization at {rows} rows "
+                   f"(HRA q/k/v at {rb}), CPU oracle on {orc.vnni_flavour()}, median of {reps} passes "
+                   f"after 1 warm-up, {med:.2f} s per pass"),
+        "tokens_per_s": round(rows / med, 1),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--rows", type=int, default=65536, help="packed rows M of the timed workload")
+    ap.add_argument("--no-fuse", action="store_true", help="one GEMM per linear (140) instead of 92")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-rows", type=int, default=2048)
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-encoder1024", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="run one plain device copy of this many MiB first (PMC counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the linear path shards by rows with no exchange; see the design notes)", file=sys.stderr)
+        return 2
+
+    import torch
+    import __graft_entry__
+    nxg = __graft_entry__.load_package()
+    torch.cuda.set_device(0)
+    nxg.init()
+
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib * (1 << 20) // 4
+        a = torch.empty(n, device="cuda")
+        b = torch.empty(n, device="cuda")
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+
+    t0 = time.perf_counter()
+    path = LinearPath(nxg, args.rows, fuse=not args.no_fuse)
+    torch.cuda.synchronize()
+    log(f"setup {time.perf_counter() - t0:.1f} s: M={args.rows}, {path.n_gemm} GEMMs + {path.n_quant} "
+        f"quantizations per step, {path.ops / 1e12:.3f} T int8 ops")
+
+    ms, wall_ms, gemm_ms, quant_ms, gemm_ev = time_steps(path, args.steps, args.warmup)
+    log(f"timed {args.steps} steps: {ms:.3f} ms/step (wall {wall_ms:.3f}), GEMMs {gemm_ms:.3f} ms, "
+        f"quantize {quant_ms:.3f} ms")
+
+    value = path.ops / (ms * 1e-3) / 1e12
+    gemm_tops = path.ops / (gemm_ms * 1e-3) / 1e12
+    n_launch = path.n_gemm
+    avg_launch_s = gemm_ms * 1e-3 / n_launch
+    ops_per_launch = path.ops / n_launch
+    bytes_per_launch = path.gemm_bytes / n_launch
+    ai = path.ops / path.gemm_bytes
+    ridge = PEAK_INT8_TOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if ai >= ridge:
+        roof = {"bound": "mfma", "achieved": round(ops_per_launch / avg_launch_s / 1e12, 2),
+                "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": round(bytes_per_launch / avg_launch_s / 1e9, 1),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["traffic"] = None
+    roof["kernel"] = "gemm_kernel (nxg_linear_i8)"
+    roof["per_launch"] = {"algorithmic_ops": int(ops_per_launch), "algorithmic_bytes": int(bytes_per_launch),
+                          "avg_us": round(avg_launch_s * 1e6, 2), "arith_intensity": round(ai, 1)}
+
+    enc = None
+    if not args.no_encoder1024:
+        p1k = LinearPath(nxg, 1024, fuse=not args.no_fuse, weights=path.dev_weights)
+        p1k.host_weights = path.host_weights
+        ms1k = time_graph(p1k, max(args.steps, 20), args.warmup)
+        enc = {"tokens_per_s": round(1024 / (ms1k * 1e-3), 1), "ms_per_step": round(ms1k, 4),
+               "int8_tops": round(p1k.ops / (ms1k * 1e-3) / 1e12, 2), "rows": 1024,
+               "mode": "HIP graph replay of the step"}
+        log(f"encoder linear path at 1024 tokens: {ms1k:.3f} ms -> {enc['tokens_per_s']:.0f} tokens/s")
+        del p1k
+
+    cpu = None
+    if not args.no_cpu:
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(path, args.cpu_rows, args.cpu_reps)
+        log(f"cpu baseline {time.perf_counter() - t0:.1f} s: {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (N(0,1) activations, N(0,0.02) weights -> Q8_0 -> int8)",
+        "config": {"workload": f"all 140 encoder int8 projections, one {args.rows}-token sequence",
+                   "rows": args.rows, "gemm_launches": path.n_gemm, "quantize_launches": path.n_quant,
+                   "fused_shared_inputs": not args.no_fuse, "weights": "Q8_0 expanded to int8",
+                   "parallelism": "single GPU"},
+        "pct_of_mfma_peak": round(100 * value / PEAK_INT8_TOPS, 2),
+        "tokens_per_s": round(args.rows / (ms * 1e-3), 1),
+        "gemm_only": {"int8_tops": round(gemm_tops, 2), "pct_of_mfma_peak": round(100 * gemm_tops / PEAK_INT8_TOPS, 2),
+                      "ms_per_step": round(gemm_ms, 4)},
+        "quantize": {"ms_per_step": round(quant_ms, 4),
+                     "gb_per_s": round(path.quant_bytes / (quant_ms * 1e-3) / 1e9, 1)},
+        "encoder_1024": enc,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -159,6 +159,29 @@ int orc_quantize_rows_simd(const float * x, int T, int n_in, int act_max, uint8_
     return 0;
 }
 
+// The same over n_threads threads, rows in groups of 16 (a multiple of 4) so that threads write
+// disjoint scale groups (the reference quantizes rows inside its multi-threaded
+// row ops, src/nexterabert.cpp:414-439).
+int orc_quantize_rows_simd_mt(const float * x, int T, int n_in, int act_max, uint8_t * q, float * sx, int n_threads) {
+    if (!__builtin_cpu_supports("avx2")) return -1;
+    const int n_blk = n_blocks(n_in);
+    std::atomic<int> next(0);
+    auto work = [&]() {
+        for (;;) {
+            const int t0 = next.fetch_add(16);
+            if (t0 >= T) break;
+            const int n = std::min(16, T - t0);
+            quantize_rows_avx2(x + (size_t) t0 * n_in, n, n_in, act_max, q + (size_t) t0 * n_in,
+                               sx + (size_t) (t0 / 4) * n_blk * 4);
+        }
+    };
+    std::vector<std::thread> pool;
+    for (int i = 1; i < n_threads; ++i) pool.emplace_back(work);
+    work();
+    for (std::thread & th : pool) th.join();
+    return 0;
+}
+
 // build_i8_weight from already dequantized rows (row-major n_out x n_in f32):
 // src/nexterabert.cpp:1030-1042. scale/off are [n_blk][n_out].
 void orc_expand_rows(const float * rows, int n_in, int n_out, int act_off,

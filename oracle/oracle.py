@@ -48,6 +48,8 @@ def lib() -> ctypes.CDLL:
         L.orc_quantize_rows_scalar.restype = None
         L.orc_quantize_rows_simd.argtypes = [P, i32, i32, i32, P, P]
         L.orc_quantize_rows_simd.restype = i32
+        L.orc_quantize_rows_simd_mt.argtypes = [P, i32, i32, i32, P, P, i32]
+        L.orc_quantize_rows_simd_mt.restype = i32
         L.orc_expand_rows.argtypes = [P, i32, i32, i32, P, P, P]
         L.orc_expand_rows.restype = None
         L.orc_dequant_q8_0.argtypes = [P, ctypes.c_int64, P]
@@ -86,7 +88,7 @@ def sx_matrix(sx: np.ndarray, T: int, n_in: int) -> np.ndarray:
     return g[:T]
 
 
-def quantize_rows(x: np.ndarray, act_max: int = 127, simd: bool = False):
+def quantize_rows(x: np.ndarray, act_max: int = 127, simd: bool = False, n_threads: int = 1):
     """quantize_row over every row of x (src/nexterabert.cpp:378-403). Returns (q u8, sx flat)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     T, n_in = x.shape
@@ -94,7 +96,10 @@ def quantize_rows(x: np.ndarray, act_max: int = 127, simd: bool = False):
     q = np.empty((T, n_in), np.uint8)
     sx = np.zeros(sx_len(T, n_in), np.float32)
     if simd:
-        rc = lib().orc_quantize_rows_simd(_p(x), T, n_in, act_max, _p(q), _p(sx))
+        if n_threads > 1:
+            rc = lib().orc_quantize_rows_simd_mt(_p(x), T, n_in, act_max, _p(q), _p(sx), n_threads)
+        else:
+            rc = lib().orc_quantize_rows_simd(_p(x), T, n_in, act_max, _p(q), _p(sx))
         if rc != 0:
             raise RuntimeError("AVX2 not available on this CPU")
     else:

@@ -193,12 +193,17 @@ def test_config1_single_linear(nxg, orc, torch, dev):
     assert (u8 == q_ref).all() and (bits(sx) == bits(sx_ref)).all()
     assert (s == orc.block_sums(W.w, W.off, q_ref)).all()
     assert (bits(y) == bits(orc.linear(W.w, W.scale, W.off, q_ref, sx_ref))).all()
-    # the fp32 gate of the task: within 1e-6 relative of a float64 evaluation of the same sums
+    # Tolerance cross-check against float64: the fp32 chain rounds each of the 4 block terms
+    # twice and the running sum once per block, so its error is bounded by a few units of
+    # 2^-24 of the sum of the terms' magnitudes (not of |y|, which can cancel to ~0).
     ref64 = np.zeros_like(y, dtype=np.float64)
+    mag = np.zeros_like(y, dtype=np.float64)
     sxm = orc.sx_matrix(sx_ref, 128, 1024).astype(np.float64)
     for B in range(4):
-        ref64 += s[B].astype(np.float64) * sxm[:, B:B + 1] * W.scale[B].astype(np.float64)[None, :]
-    assert np.max(np.abs(y - ref64) / np.maximum(np.abs(ref64), 1e-30)) < 1e-5
+        term = s[B].astype(np.float64) * sxm[:, B:B + 1] * W.scale[B].astype(np.float64)[None, :]
+        ref64 += term
+        mag += np.abs(term)
+    assert np.max(np.abs(y - ref64) / np.maximum(mag, 1e-30)) < 1e-6
 
 
 def test_batch_invariance(nxg, torch, dev):
