@@ -36,12 +36,9 @@ constexpr int FRAG = 1024;       // bytes of one 16-row x 64-input fragment
 constexpr int BM = 128;          // GEMM workgroup tile: rows (tokens)
 constexpr int BN = 128;          //                      columns (output features)
 constexpr int NTHREADS = 256;    // 4 waves, 2 x 2, each 64 x 64
-constexpr int STAGE_KS = 2;      // 64-input k-steps per LDS stage
-constexpr int A_STAGE = (BM / 16) * STAGE_KS * FRAG;   // 16 KiB
-constexpr int B_STAGE = (BN / 16) * STAGE_KS * FRAG;   // 16 KiB
 constexpr int N_XCD = 8;         // MI355X: 8 XCDs, workgroups dispatched round-robin
 
-inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+__host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 // ---------------------------------------------------------------------------
 // quantize
@@ -246,31 +243,87 @@ __device__ __forceinline__ int xcd_tile(int bid, int G) {
     return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
 }
 
+// LDS ring: four slots, one 64-input k-step each: 8 A fragments, 8 B fragments
+// and (slot 3 only) the block's scales: sx of the tile's 32 row groups, then sw of
+// its 128 columns.
+constexpr int SLOT_AB = (BM / 16 + BN / 16) * FRAG;   // 16 KiB
+constexpr int SLOT = SLOT_AB + 1024;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land at
+// LDS address lds + 16 l (global_load_lds_dwordx4; M0 holds the wave's LDS base).
+// Issued from inline asm so that the compiler's wait-count pass does not track it
+// (it would drain every prefetch at the loop back-edge); each use is synchronized
+// explicitly with wait_vm before the barrier that precedes its readers.
+__device__ __forceinline__ void dma16(const void * gptr, const void * lds) {
+    const uint32_t la = (uint32_t) (uintptr_t) (lds_void *) lds;
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(gptr), "s"(la) : "memory", "m0");
+}
+
+// Waits until at most n of this wave's vector-memory loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+// Workgroup barrier for the LDS ring. __syncthreads() (and any fence on LDS) makes
+// every wave wait for all of its outstanding loads, since LDS-DMA writes count as
+// pending LDS stores -- including the prefetches of later k-steps that must stay in
+// flight. Here the LDS-DMA of the k-step about to be read is waited for explicitly
+// (wait_vm) before the barrier, and the barrier itself only drains this wave's own
+// LDS reads and writes. The "memory" clobber keeps the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <bool RES, bool SUMS, bool K256>
 __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
-    __shared__ __attribute__((aligned(16))) int8_t lds[2][A_STAGE + B_STAGE];
+    __shared__ __attribute__((aligned(1024))) int8_t s0[SLOT];
+    __shared__ __attribute__((aligned(1024))) int8_t s1[SLOT];
+    __shared__ __attribute__((aligned(1024))) int8_t s2[SLOT];
+    __shared__ __attribute__((aligned(1024))) int8_t s3[SLOT];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int tile = xcd_tile(blockIdx.x, p.n_mt * p.n_nt);
     const int mt = tile / p.n_nt, nt = tile % p.n_nt;
     const int m0 = mt * BM, n0 = nt * BN;
 
-    // Copy roles: this thread moves one 16-byte piece of 4 A and 4 B fragments
-    // per stage; fragment fi = wave + 4u holds local frag row fi / 2, k-step fi % 2.
-    const int cj = wave & 1;
-    const int8_t * a_src[4];
-    const int8_t * b_src[4];
-    bool a_ok[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int fl = (wave >> 1) + 2 * u;
-        const int mf = mt * (BM / 16) + fl;
-        a_ok[u] = mf < p.MF;
-        a_src[u] = p.a + ((size_t) (a_ok[u] ? mf : 0) * p.KS + cj) * FRAG + lane * 16;
-        b_src[u] = p.w + ((size_t) (nt * (BN / 16) + fl) * p.KS + cj) * FRAG + lane * 16;
+    // Copy roles: wave w moves fragments w and w+4 of A and of B (1 KiB each, one
+    // global_load_lds_dwordx4 per fragment and k-step). Fragment rows past the last
+    // row of A re-read its last fragment row (those output rows are never stored), so
+    // that every wave issues exactly 4 loads per k-step: the vmcnt waits below count on it.
+    const int8_t * a_src0 = p.a + ((size_t) min(mt * (BM / 16) + wave, p.MF - 1) * p.KS) * FRAG + lane * 16;
+    const int8_t * a_src1 = p.a + ((size_t) min(mt * (BM / 16) + wave + 4, p.MF - 1) * p.KS) * FRAG + lane * 16;
+    const int8_t * b_src0 = p.w + ((size_t) (nt * (BN / 16) + wave) * p.KS) * FRAG + lane * 16;
+    const int8_t * b_src1 = b_src0 + (size_t) 4 * p.KS * FRAG;
+    // Scale roles (wave 0): lane l < 32 -> sx row group l of the tile, l >= 32 -> sw columns 4(l-32)..+3.
+    const float * scl_src;
+    size_t scl_step;   // per block
+    if (lane < 32) {
+        const int g = min(m0 / 4 + lane, ceil_div(p.MF * 16, 4) - 1);
+        scl_src = p.sx + (size_t) g * p.n_blk * 4;
+        scl_step = 4;
+    } else {
+        scl_src = p.sw + n0 + 4 * (lane - 32);
+        scl_step = (size_t) p.NP;
     }
-    const int lds_off = (wave + 0) * FRAG + lane * 16;   // + 4u * FRAG
+
+    // Loads k-step ks (all k-steps exist up to KS - 1; later ones are never fetched).
+    auto issue = [&](int8_t * slot, int ks, bool scales) {
+        if (ks >= p.KS) return;
+        const size_t o = (size_t) ks * FRAG;
+        dma16(a_src0 + o, slot + wave * FRAG);
+        dma16(a_src1 + o, slot + (wave + 4) * FRAG);
+        dma16(b_src0 + o, slot + (8 + wave) * FRAG);
+        dma16(b_src1 + o, slot + (12 + wave) * FRAG);
+        if (!SUMS && scales && wave == 0) dma16(scl_src + (size_t) (ks >> 2) * scl_step, slot + SLOT_AB);
+    };
 
     // Epilogue roles: rows m0 + wm*64 + mi*16 + 4*(lane/16) + r, columns n0 + wn*64 + ni*16 + lane%16.
     const int row_base = m0 + wm * 64 + 4 * (lane >> 4);
@@ -285,82 +338,62 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) f[i][j][r] = 0.0f;
 
-    v4i stA[4], stB[4];
-    auto load_stage = [&](int ks) {   // global -> registers, k-steps ks + cj
+    auto mma = [&](const int8_t * slot, bool first) {
+        v4i a[4], b[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const bool ok = a_ok[u] && (K256 || ks + cj < p.KS);
-            stA[u] = ok ? *reinterpret_cast<const v4i *>(a_src[u] + (size_t) ks * FRAG) : v4i{0, 0, 0, 0};
-            stB[u] = (K256 || ks + cj < p.KS) ? *reinterpret_cast<const v4i *>(b_src[u] + (size_t) ks * FRAG)
-                                              : v4i{0, 0, 0, 0};
+        for (int i = 0; i < 4; ++i) {
+            a[i] = *reinterpret_cast<const v4i *>(slot + (wm * 4 + i) * FRAG + lane * 16);
+            b[i] = *reinterpret_cast<const v4i *>(slot + (8 + wn * 4 + i) * FRAG + lane * 16);
         }
-    };
-    auto store_stage = [&](int buf) {   // registers -> LDS
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            *reinterpret_cast<v4i *>(&lds[buf][lds_off + 4 * u * FRAG]) = stA[u];
-            *reinterpret_cast<v4i *>(&lds[buf][A_STAGE + lds_off + 4 * u * FRAG]) = stB[u];
-        }
-    };
-    auto mma_stage = [&](int buf, bool first, int nks) {
+        for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int j = 0; j < STAGE_KS; ++j) {
-            if (!K256 && j >= nks) break;
-            v4i a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                a[i] = *reinterpret_cast<const v4i *>(&lds[buf][((wm * 4 + i) * 2 + j) * FRAG + lane * 16]);
-                b[i] = *reinterpret_cast<const v4i *>(&lds[buf][A_STAGE + ((wn * 4 + i) * 2 + j) * FRAG + lane * 16]);
-            }
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni)
-                    acc[mi][ni] = (first && j == 0)
-                        ? __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], v4i{0, 0, 0, 0}, 0, 0, 0)
-                        : __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
-        }
+            for (int ni = 0; ni < 4; ++ni)
+                acc[mi][ni] = first
+                    ? __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], v4i{0, 0, 0, 0}, 0, 0, 0)
+                    : __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
     };
 
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
+    // Wait for k-step ks's slot: the loads of later k-steps (up to two, 4 per wave each,
+    // plus one scale load on wave 0) may stay in flight.
+    auto arrive = [&](int ks) {
+        const int later = min(2, p.KS - 1 - ks);
+        if (later >= 2) wait_vm<8>();
+        else if (later == 1) wait_vm<4>();
+        else wait_vm<0>();
+        lds_barrier();
+    };
 
+    issue(s0, 0, false);
+    issue(s1, 1, false);
+    issue(s2, 2, false);
     for (int B = 0; B < p.n_blk; ++B) {
         const int ks0 = 4 * B;
-        const int nks = K256 ? 4 : min(4, p.KS - ks0);
-
-        // Scales of this block, fetched early; used after its last k-step.
-        float4 sxv[4];
-        float swv[4];
-        if (!SUMS) {
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
-                const int tr = row_base + mi * 16;
-                sxv[mi] = (tr >> 4) < p.MF
-                    ? *reinterpret_cast<const float4 *>(p.sx + ((size_t) (tr >> 2) * p.n_blk + B) * 4)
-                    : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) swv[ni] = p.sw[(size_t) B * p.NP + col_base + ni * 16];
+        arrive(ks0);
+        issue(s3, ks0 + 3, true);
+        mma(s0, true);
+        if (K256 || ks0 + 1 < p.KS) {
+            arrive(ks0 + 1);
+            issue(s0, ks0 + 4, false);
+            mma(s1, false);
         }
-
-        // first half of the block: k-steps ks0, ks0 + 1 (in buffer 0)
-        const bool two_stages = K256 || nks > 2;
-        if (two_stages) load_stage(ks0 + 2);
-        mma_stage(0, true, K256 ? 2 : min(2, nks));
-        if (two_stages) {
-            store_stage(1);
-            __syncthreads();
-            const bool more = B + 1 < p.n_blk;
-            if (more) load_stage(ks0 + 4);
-            mma_stage(1, false, K256 ? 2 : nks - 2);
-            if (more) store_stage(0);
-        } else {
-            const bool more = B + 1 < p.n_blk;
-            if (more) load_stage(ks0 + 4);   // unreachable for the last block; kept for symmetry
-            __syncthreads();
-            if (more) store_stage(0);
+        if (K256 || ks0 + 2 < p.KS) {
+            arrive(ks0 + 2);
+            issue(s1, ks0 + 5, false);
+            mma(s2, false);
+        }
+        if (K256 || ks0 + 3 < p.KS) {
+            arrive(ks0 + 3);
+            issue(s2, ks0 + 6, false);
+            mma(s3, false);
+        } else if (!SUMS) {
+            // partial last block: its scales travel with k-step ks0 + 3, which does not
+            // exist; fetch them now (the slot is free: its last reader passed a barrier)
+            wait_vm<0>();
+            lds_barrier();
+            if (wave == 0) dma16(scl_src + (size_t) B * scl_step, s3 + SLOT_AB);
+            wait_vm<0>();
+            lds_barrier();
         }
 
         if (SUMS) {
@@ -375,9 +408,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
                     }
         } else {
             // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
+            const float * scl = reinterpret_cast<const float *>(s3 + SLOT_AB);
+            float swv[4];
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) swv[ni] = scl[128 + wn * 64 + ni * 16 + (lane & 15)];
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi) {
-                const float sxr[4] = { sxv[mi].x, sxv[mi].y, sxv[mi].z, sxv[mi].w };
+                const float4 sx4 = *reinterpret_cast<const float4 *>(scl + 4 * (wm * 16 + mi * 4 + (lane >> 4)));
+                const float sxr[4] = { sx4.x, sx4.y, sx4.z, sx4.w };
 #pragma unroll
                 for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
@@ -387,7 +425,6 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
                     }
             }
         }
-        __syncthreads();
     }
 
     if (!SUMS) {
