@@ -37,6 +37,9 @@ constexpr int BM = 128;          // GEMM workgroup tile: rows (tokens)
 constexpr int BN = 128;          //                      columns (output features)
 constexpr int NTHREADS = 256;    // 4 waves, 2 x 2, each 64 x 64
 constexpr int N_XCD = 8;         // MI355X: 8 XCDs, workgroups dispatched round-robin
+#ifndef NXG_WG_PER_CU
+#define NXG_WG_PER_CU 2          // persistent GEMM workgroups per CU (0: one workgroup per tile)
+#endif
 
 __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
@@ -232,20 +235,32 @@ struct gemm_params {
     float *        out;   // [T][N]
     int32_t *      sums;  // [n_blk][T][N] (block-sum variant)
     int T, N, NP, KS, n_blk, MF, n_mt, n_nt;
+    int G;                // tiles: n_mt * n_nt
 };
 
-// Workgroup index -> tile index. Workgroups go to the XCDs round-robin; this
-// gives each XCD a contiguous range of tiles, and tiles are numbered with the
-// column tile fastest, so the workgroups of one XCD share row tiles in its L2.
-__device__ __forceinline__ int xcd_tile(int bid, int G) {
-    const int xcd = bid % N_XCD, idx = bid / N_XCD;
-    const int q = G / N_XCD, r = G % N_XCD;
-    return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
-}
+// Tiles of one workgroup. Workgroups are dispatched to the 8 XCDs round-robin
+// (workgroup w runs on XCD w % 8). Each XCD owns a contiguous range of tile
+// numbers, dealt out round-robin to its workgroups; tiles are numbered with the
+// column tile fastest, so the workgroups of an XCD work on neighbouring row tiles
+// at the same time and share them (and the whole weight) in that XCD's L2.
+struct tile_walk {
+    int first, stride, count;
+    __device__ tile_walk(int wg, int n_wg, int G) {
+        const int xcd = wg % N_XCD, idx = wg / N_XCD;
+        const int per = n_wg / N_XCD + (xcd < n_wg % N_XCD ? 1 : 0);     // workgroups on this XCD
+        const int q = G / N_XCD, r = G % N_XCD;
+        const int lo = xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q;
+        const int n = q + (xcd < r ? 1 : 0);                              // tiles of this XCD
+        first = lo + idx;
+        stride = per;
+        count = idx < n ? (n - idx + per - 1) / per : 0;
+    }
+    __device__ int tile(int i) const { return first + i * stride; }
+};
 
 // LDS ring: four slots, one 64-input k-step each: 8 A fragments, 8 B fragments
-// and (slot 3 only) the block's scales: sx of the tile's 32 row groups, then sw of
-// its 128 columns.
+// and (slot 3 only) the block's scales: sx of the tile's 128 rows (as 32 groups of
+// 4), then sw of its 128 columns.
 constexpr int SLOT_AB = (BM / 16 + BN / 16) * FRAG;   // 16 KiB
 constexpr int SLOT = SLOT_AB + 1024;
 
@@ -280,6 +295,14 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// One workgroup: 4 waves (2 x 2), each computing a 64 x 64 piece of a 128 x 128
+// output tile with v_mfma_i32_16x16x64_i8, the weight fragment as the MFMA's A
+// operand and the activation fragment as its B operand. A lane then holds, for
+// each 16 x 16 piece, 4 consecutive output features of one token: out[t][n..n+3].
+// Per 256-input block the int32 sums are folded into fp32 with the reference's
+// step f = fma((float) s * sx[t], sw[n], f); the block's scales come through LDS.
+// With K256 (n_in a multiple of 256) a workgroup walks several tiles and its LDS
+// ring runs on across them; otherwise it computes one tile.
 template <bool RES, bool SUMS, bool K256>
 __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
     __shared__ __attribute__((aligned(1024))) int8_t s0[SLOT];
@@ -290,53 +313,65 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    const int tile = xcd_tile(blockIdx.x, p.n_mt * p.n_nt);
-    const int mt = tile / p.n_nt, nt = tile % p.n_nt;
-    const int m0 = mt * BM, n0 = nt * BN;
+    const tile_walk walk(blockIdx.x, gridDim.x, p.G);
+    if (walk.count == 0) return;
+    const int n_steps = walk.count * p.KS;   // k-steps of all this workgroup's tiles
 
-    // Copy roles: wave w moves fragments w and w+4 of A and of B (1 KiB each, one
-    // global_load_lds_dwordx4 per fragment and k-step). Fragment rows past the last
-    // row of A re-read its last fragment row (those output rows are never stored), so
-    // that every wave issues exactly 4 loads per k-step: the vmcnt waits below count on it.
-    const int8_t * a_src0 = p.a + ((size_t) min(mt * (BM / 16) + wave, p.MF - 1) * p.KS) * FRAG + lane * 16;
-    const int8_t * a_src1 = p.a + ((size_t) min(mt * (BM / 16) + wave + 4, p.MF - 1) * p.KS) * FRAG + lane * 16;
-    const int8_t * b_src0 = p.w + ((size_t) (nt * (BN / 16) + wave) * p.KS) * FRAG + lane * 16;
-    const int8_t * b_src1 = b_src0 + (size_t) 4 * p.KS * FRAG;
-    // Scale roles (wave 0): lane l < 32 -> sx row group l of the tile, l >= 32 -> sw columns 4(l-32)..+3.
-    const float * scl_src;
-    size_t scl_step;   // per block
-    if (lane < 32) {
-        const int g = min(m0 / 4 + lane, ceil_div(p.MF * 16, 4) - 1);
-        scl_src = p.sx + (size_t) g * p.n_blk * 4;
-        scl_step = 4;
-    } else {
-        scl_src = p.sw + n0 + 4 * (lane - 32);
-        scl_step = (size_t) p.NP;
-    }
-
-    // Loads k-step ks (all k-steps exist up to KS - 1; later ones are never fetched).
-    auto issue = [&](int8_t * slot, int ks, bool scales) {
-        if (ks >= p.KS) return;
-        const size_t o = (size_t) ks * FRAG;
-        dma16(a_src0 + o, slot + wave * FRAG);
-        dma16(a_src1 + o, slot + (wave + 4) * FRAG);
-        dma16(b_src0 + o, slot + (8 + wave) * FRAG);
-        dma16(b_src1 + o, slot + (12 + wave) * FRAG);
-        if (!SUMS && scales && wave == 0) dma16(scl_src + (size_t) (ks >> 2) * scl_step, slot + SLOT_AB);
+    // Scales of block B of tile (mt, nt) for lane l of wave 0: l < 32 sx of row group
+    // l of the tile, l >= 32 sw of columns 4(l-32)..+3.
+    auto scale_src = [&](int mt, int nt, int B) -> const float * {
+        if (lane < 32) {
+            const int grp = min(mt * (BM / 4) + lane, p.MF * 4 - 1);
+            return p.sx + ((size_t) grp * p.n_blk + B) * 4;
+        }
+        return p.sw + (size_t) B * p.NP + nt * BN + 4 * (lane - 32);
     };
 
-    // Epilogue roles: rows m0 + wm*64 + mi*16 + 4*(lane/16) + r, columns n0 + wn*64 + ni*16 + lane%16.
-    const int row_base = m0 + wm * 64 + 4 * (lane >> 4);
-    const int col_base = n0 + wn * 64 + (lane & 15);
+    // The load stream: k-steps in order, across this workgroup's tiles. Wave w moves
+    // fragments w and w+4 of A and of B, 1 KiB each. A fragment rows past the last
+    // row of A re-read its last fragment row (those output rows are never stored),
+    // so that every wave issues exactly 4 loads per k-step: the waits count on it.
+    // Wave 0 also loads a block's scales with the block's last k-step (slot 3).
+    int iss_it = 0, iss_ks = 0;          // next k-step to load
+    int iss_mt = 0, iss_nt = 0;
+    const int8_t * ia0 = nullptr;
+    const int8_t * ia1 = nullptr;
+    const int8_t * ib0 = nullptr;
+    auto issue_tile = [&]() {            // per-lane sources of k-step 0 of tile iss_it
+        const int tile = walk.tile(iss_it);
+        iss_mt = tile / p.n_nt;
+        iss_nt = tile - iss_mt * p.n_nt;
+        ia0 = p.a + (size_t) min(iss_mt * (BM / 16) + wave, p.MF - 1) * p.KS * FRAG + lane * 16;
+        ia1 = p.a + (size_t) min(iss_mt * (BM / 16) + wave + 4, p.MF - 1) * p.KS * FRAG + lane * 16;
+        ib0 = p.w + (size_t) (iss_nt * (BN / 16) + wave) * p.KS * FRAG + lane * 16;
+    };
+    issue_tile();
+    auto issue = [&](int8_t * slot) {
+        if (iss_it >= walk.count) return;
+        const size_t o = (size_t) iss_ks * FRAG;
+        dma16(ia0 + o, slot + wave * FRAG);
+        dma16(ia1 + o, slot + (wave + 4) * FRAG);
+        dma16(ib0 + o, slot + (8 + wave) * FRAG);
+        dma16(ib0 + o + (size_t) 4 * p.KS * FRAG, slot + (12 + wave) * FRAG);
+        if (!SUMS && wave == 0 && (iss_ks & 3) == 3) dma16(scale_src(iss_mt, iss_nt, iss_ks >> 2), s3 + SLOT_AB);
+        if (++iss_ks == p.KS) {
+            iss_ks = 0;
+            if (++iss_it < walk.count) issue_tile();
+        }
+    };
+
+    // Wait for k-step g's slot: the loads of later k-steps (up to two, 4 per wave each,
+    // plus one scale load on wave 0) may stay in flight.
+    auto arrive = [&](int g) {
+        const int later = min(2, n_steps - 1 - g);
+        if (later >= 2) wait_vm<8>();
+        else if (later == 1) wait_vm<4>();
+        else wait_vm<0>();
+        lds_barrier();
+    };
 
     v4i acc[4][4];
     float f[4][4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) f[i][j][r] = 0.0f;
 
     auto mma = [&](const int8_t * slot, bool first) {
         v4i a[4], b[4];
@@ -350,99 +385,136 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni)
                 acc[mi][ni] = first
-                    ? __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], v4i{0, 0, 0, 0}, 0, 0, 0)
-                    : __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
+                    ? __builtin_amdgcn_mfma_i32_16x16x64_i8(b[ni], a[mi], v4i{0, 0, 0, 0}, 0, 0, 0)
+                    : __builtin_amdgcn_mfma_i32_16x16x64_i8(b[ni], a[mi], acc[mi][ni], 0, 0, 0);
     };
 
-    // Wait for k-step ks's slot: the loads of later k-steps (up to two, 4 per wave each,
-    // plus one scale load on wave 0) may stay in flight.
-    auto arrive = [&](int ks) {
-        const int later = min(2, p.KS - 1 - ks);
-        if (later >= 2) wait_vm<8>();
-        else if (later == 1) wait_vm<4>();
-        else wait_vm<0>();
-        lds_barrier();
-    };
+    issue(s0);
+    issue(s1);
+    issue(s2);
+    for (int it = 0; it < walk.count; ++it) {
+        const int tile = walk.tile(it);
+        const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
+        // this lane's outputs: token t0 + mi*16, features n0 + ni*16 + 0..3
+        const int t0 = mt * BM + wm * 64 + (lane & 15);
+        const int n0 = nt * BN + wn * 64 + 4 * (lane >> 4);
 
-    issue(s0, 0, false);
-    issue(s1, 1, false);
-    issue(s2, 2, false);
-    for (int B = 0; B < p.n_blk; ++B) {
-        const int ks0 = 4 * B;
-        arrive(ks0);
-        issue(s3, ks0 + 3, true);
-        mma(s0, true);
-        if (K256 || ks0 + 1 < p.KS) {
-            arrive(ks0 + 1);
-            issue(s0, ks0 + 4, false);
-            mma(s1, false);
-        }
-        if (K256 || ks0 + 2 < p.KS) {
-            arrive(ks0 + 2);
-            issue(s1, ks0 + 5, false);
-            mma(s2, false);
-        }
-        if (K256 || ks0 + 3 < p.KS) {
-            arrive(ks0 + 3);
-            issue(s2, ks0 + 6, false);
-            mma(s3, false);
-        } else if (!SUMS) {
-            // partial last block: its scales travel with k-step ks0 + 3, which does not
-            // exist; fetch them now (the slot is free: its last reader passed a barrier)
-            wait_vm<0>();
-            lds_barrier();
-            if (wave == 0) dma16(scl_src + (size_t) B * scl_step, s3 + SLOT_AB);
-            wait_vm<0>();
-            lds_barrier();
-        }
-
-        if (SUMS) {
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int t = row_base + mi * 16 + r, n = col_base + ni * 16;
-                        if (t < p.T && n < p.N) p.sums[((size_t) B * p.T + t) * p.N + n] = acc[mi][ni][r];
-                    }
-        } else {
-            // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
-            const float * scl = reinterpret_cast<const float *>(s3 + SLOT_AB);
-            float swv[4];
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) swv[ni] = scl[128 + wn * 64 + ni * 16 + (lane & 15)];
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
-                const float4 sx4 = *reinterpret_cast<const float4 *>(scl + 4 * (wm * 16 + mi * 4 + (lane >> 4)));
-                const float sxr[4] = { sx4.x, sx4.y, sx4.z, sx4.w };
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float prod = (float) acc[mi][ni][r] * sxr[r];
-                        f[mi][ni][r] = __builtin_fmaf(prod, swv[ni], f[mi][ni][r]);
-                    }
+        const int g0 = it * p.KS;
+        for (int B = 0; B < p.n_blk; ++B) {
+            const int g = g0 + 4 * B;
+            const int nks = K256 ? 4 : min(4, p.KS - 4 * B);
+            arrive(g);
+            issue(s3);
+            mma(s0, true);
+            if (K256 || nks > 1) {
+                arrive(g + 1);
+                issue(s0);
+                mma(s1, false);
             }
-        }
-    }
+            if (K256 || nks > 2) {
+                arrive(g + 2);
+                issue(s1);
+                mma(s2, false);
+            }
+            if (K256 || nks > 3) {
+                arrive(g + 3);
+                issue(s2);
+                mma(s3, false);
+            } else if (!SUMS) {
+                // Partial last block (one tile per workgroup here): there is no k-step
+                // 4B+3 to bring its scales, so fetch them now. s3's scale area is free:
+                // its last readers (block B-1's epilogue) have all passed arrive(4B).
+                if (wave == 0) dma16(scale_src(mt, nt, B), s3 + SLOT_AB);
+                wait_vm<0>();
+                lds_barrier();
+            }
 
-    if (!SUMS) {
+            if (SUMS) {
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
+                for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = row_base + mi * 16 + r;
-                if (t >= p.T) continue;
+                    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int t = t0 + mi * 16, n = n0 + ni * 16 + r;
+                            if (t < p.T && n < p.N) p.sums[((size_t) B * p.T + t) * p.N + n] = acc[mi][ni][r];
+                        }
+            } else {
+                // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
+                const float * scl = reinterpret_cast<const float *>(s3 + SLOT_AB);
+                float sxv[4];
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi) sxv[mi] = scl[wm * 64 + mi * 16 + (lane & 15)];
 #pragma unroll
                 for (int ni = 0; ni < 4; ++ni) {
-                    const int n = col_base + ni * 16;
-                    if (n >= p.N) continue;
-                    const size_t o = (size_t) t * p.N + n;
-                    const float y = RES ? p.res[o] + f[mi][ni][r] : f[mi][ni][r];
-                    __builtin_nontemporal_store(y, p.out + o);
+                    const float4 sw4 = *reinterpret_cast<const float4 *>(scl + 128 + wn * 64 + ni * 16 + 4 * (lane >> 4));
+                    const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
+#pragma unroll
+                    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float prod = (float) acc[mi][ni][r] * sxv[mi];
+                            // block 0 starts from f = 0: fma(prod, sw, +0.0)
+                            f[mi][ni][r] = __builtin_fmaf(prod, swr[r], B == 0 ? 0.0f : f[mi][ni][r]);
+                        }
                 }
             }
+        }
+
+        if (!SUMS) {
+            if ((p.N & 3) == 0) {
+                // Full-line stores through LDS. After the tile's last epilogue slot 3 is
+                // free (the next tile's k-step 3 is loaded only after the next barrier):
+                // each wave owns 4352 bytes of it, 16 rows of 64 floats at a 272-byte
+                // pitch. Per 16-token piece mi: write it in MFMA order (lane: token
+                // lane%16, features 16ni + 4(lane/16) + 0..3), read it back as 4 rows of
+                // 256 bytes per instruction, and store whole 128-byte lines.
+                lds_barrier();
+                float * stg = reinterpret_cast<float *>(s3 + wave * 4352);
+                const int trow = lane & 15, tcol = 4 * (lane >> 4);
+                const int rrow = lane >> 4, rcol = 4 * (lane & 15);
+                const int tbase = mt * BM + wm * 64, nb = nt * BN + wn * 64 + rcol;
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+                    for (int ni = 0; ni < 4; ++ni) {
+                        const v4f y = { f[mi][ni][0], f[mi][ni][1], f[mi][ni][2], f[mi][ni][3] };
+                        *reinterpret_cast<v4f *>(stg + trow * 68 + 16 * ni + tcol) = y;
+                    }
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int row = 4 * q + rrow;
+                        v4f y = *reinterpret_cast<const v4f *>(stg + row * 68 + rcol);
+                        const int t = tbase + mi * 16 + row;
+                        if (t < p.T && nb < p.N) {
+                            const size_t o = (size_t) t * p.N + nb;
+                            if (RES) y = *reinterpret_cast<const v4f *>(p.res + o) + y;
+                            __builtin_nontemporal_store(y, reinterpret_cast<v4f *>(p.out + o));
+                        }
+                    }
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                }
+            } else {
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi) {
+                    const int t = t0 + mi * 16;
+                    if (t >= p.T) continue;
+#pragma unroll
+                    for (int ni = 0; ni < 4; ++ni) {
+                        const int n = n0 + ni * 16;
+                        const size_t o = (size_t) t * p.N + n;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if (n + r < p.N) {
+                                const float y = RES ? p.res[o + r] + f[mi][ni][r] : f[mi][ni][r];
+                                __builtin_nontemporal_store(y, p.out + o + r);
+                            }
+                        }
+                    }
+                }
+            }
+        }
     }
 }
 
@@ -465,6 +537,8 @@ int hip_fail(hipError_t e, const char * what) {
     return fail(NXG_EDEVICE, "%s: %s", what, hipGetErrorString(e));
 }
 
+thread_local int g_cus = 0;   // compute units of the checked device
+
 int check_device() {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
@@ -478,8 +552,11 @@ int check_device() {
         return fail(NXG_EDEVICE, "device %d is %s; this engine is built for gfx950 (MI355X)", dev, prop.gcnArchName);
     }
     checked_dev = dev;
+    g_cus = prop.multiProcessorCount;
     return NXG_OK;
 }
+
+int device_cus() { return g_cus > 0 ? g_cus : 256; }
 
 int launch_check(const char * what) {
     const hipError_t e = hipGetLastError();
@@ -633,10 +710,15 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     p.n_mt = ceil_div(T, BM);
     p.n_nt = W->NP / BN;
     const long long G = (long long) p.n_mt * p.n_nt;
-    if (G > INT32_MAX) return fail(NXG_EINVAL, "linear: T=%d too large", T);
+    if (G > INT32_MAX / 2) return fail(NXG_EINVAL, "linear: T=%d too large", T);
+    p.G = (int) G;
     hipStream_t s = (hipStream_t) stream;
     const bool k256 = W->KS % 4 == 0;
-    const dim3 grid((unsigned) G), block(NTHREADS);
+    // K256: persistent workgroups, two per CU (the LDS ring needs 68 KiB of the 160);
+    // otherwise one workgroup per tile.
+    const int n_wg = (k256 && NXG_WG_PER_CU > 0) ? (int) std::min<long long>(G, (long long) NXG_WG_PER_CU * device_cus())
+                                                 : (int) G;
+    const dim3 grid((unsigned) n_wg), block(NTHREADS);
     if (sums) {
         if (k256) gemm_kernel<false, true, true><<<grid, block, 0, s>>>(p);
         else      gemm_kernel<false, true, false><<<grid, block, 0, s>>>(p);
