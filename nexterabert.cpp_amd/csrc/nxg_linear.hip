@@ -101,75 +101,87 @@ __device__ __forceinline__ int quant1(float x, float inv) {
 }
 
 // One workgroup per (16-row group, 256-input block). Wave w quantizes rows
-// 4w..4w+3 of the group; lane l holds 16 consecutive inputs (chunk l % 16) of
-// row 4w + l/16, i.e. one 16-byte piece of an MFMA fragment.
+// 4w..4w+3; the 16 lanes of a row read its 256 inputs as 4 contiguous 256-byte
+// pieces, so lane c holds inputs 64i + 4c + e (i, e = 0..3). The int8 results are
+// gathered in LDS in fragment order and each wave stores one 1 KiB fragment.
 template <int ACT_MAX>
 __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict__ x, int T, int n_in, int KS,
                                                        int n_blk, int8_t * __restrict__ q, float * __restrict__ sx) {
+    __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
+
     const int g = blockIdx.x, B = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rl = wave * 4 + (lane >> 4);
+    const int rl = wave * 4 + (lane >> 4);     // row within the 16-row group
     const int t = g * 16 + rl;
     const int c = lane & 15;
-    const int k = B * BLK + c * 16;
-    const bool present = t < T && k < n_in;
+    const int kb = B * BLK;                    // first input of the block
 
-    float xv[16];   // the inputs as read
-    if (present) {
-        const v4f * src = reinterpret_cast<const v4f *>(x + (size_t) t * n_in + k);
+    float xv[4][4];                            // [i][e]: input kb + 64i + 4c + e
+    bool present[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const v4f f = __builtin_nontemporal_load(src + i);
-            xv[4 * i + 0] = f.x; xv[4 * i + 1] = f.y; xv[4 * i + 2] = f.z; xv[4 * i + 3] = f.w;
+    for (int i = 0; i < 4; ++i) {
+        present[i] = t < T && kb + 64 * i + 4 * c < n_in;
+        if (present[i]) {
+            const v4f f = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(x + (size_t) t * n_in + kb + 64 * i + 4 * c));
+            xv[i][0] = f.x; xv[i][1] = f.y; xv[i][2] = f.z; xv[i][3] = f.w;
+        } else {
+            xv[i][0] = xv[i][1] = xv[i][2] = xv[i][3] = 0.0f;
         }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) xv[i] = 0.0f;
     }
-    float v[16];    // |x|
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = abs_bits(xv[i]);
 
     bool any_nan = false;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) any_nan |= __builtin_isnan(v[i]);
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) any_nan |= __builtin_isnan(xv[i][e]);
 
     float amax;
     if (!__any(any_nan)) {
         // No NaN in this wave: the fold is the plain maximum.
-        float m = v[0];
+        float m = 0.0f;
 #pragma unroll
-        for (int i = 1; i < 16; ++i) m = fmaxf(m, v[i]);
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int s = 1; s < 16; s <<= 1) m = fmaxf(m, __shfl_xor(m, s));
+            for (int e = 0; e < 4; ++e) m = fmaxf(m, abs_bits(xv[i][e]));
+#pragma unroll
+        for (int sft = 1; sft < 16; sft <<= 1) m = fmaxf(m, __shfl_xor(m, sft));
         amax = m;
     } else {
-        // Exact MAXPS semantics. Element 16c + e is AVX lane e % 8, position 2c + e / 8.
-        fold f[8];
+        // Exact MAXPS semantics. Input kb + k is AVX lane k % 8 at position k / 8; for
+        // this lane k = 64i + 4c + e: AVX lane 4(c%2) + e, position 8i + c/2. Fold the
+        // 8 lanes of one parity for each i (ordered by c/2), then the four i in order.
+        fold acc[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (present) {
-                f[j] = fold_join(fold_elem(v[j]), fold_elem(v[j + 8]));
-            } else {
-                f[j].tail = 0.0f;
-                f[j].flags = 2;
+        for (int e = 0; e < 4; ++e) { acc[e].tail = 0.0f; acc[e].flags = 2; }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                fold fi;
+                if (present[i]) {
+                    fi = fold_elem(abs_bits(xv[i][e]));
+                } else {
+                    fi.tail = 0.0f;
+                    fi.flags = 2;
+                }
+#pragma unroll
+                for (int sft = 2; sft < 16; sft <<= 1) {
+                    fold o;
+                    o.tail = __shfl_xor(fi.tail, sft);
+                    o.flags = __shfl_xor(fi.flags, sft);
+                    fi = (c & sft) ? fold_join(o, fi) : fold_join(fi, o);
+                }
+                acc[e] = fold_join(acc[e], fi);
             }
         }
-#pragma unroll
-        for (int s = 1; s < 16; s <<= 1) {
-            const bool upper = (c & s) != 0;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                fold o;
-                o.tail = __shfl_xor(f[j].tail, s);
-                o.flags = __shfl_xor(f[j].flags, s);
-                f[j] = upper ? fold_join(o, f[j]) : fold_join(f[j], o);
-            }
-        }
-        // Horizontal tree of the reference: lanes (j, j+4), then (0,2), (1,3), then (0,1).
+        // acc[e] is AVX lane 4(c%2) + e. The reference's horizontal tree: lanes
+        // (j, j+4), then (0,2), (1,3), then (0,1).
         float m[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) m[j] = maxps1(f[j].tail, f[j + 4].tail);
+        for (int e = 0; e < 4; ++e) {
+            const float other = __shfl_xor(acc[e].tail, 1);
+            m[e] = (c & 1) ? maxps1(other, acc[e].tail) : maxps1(acc[e].tail, other);
+        }
         amax = maxps1(maxps1(m[0], m[2]), maxps1(m[1], m[3]));
         if (t >= T) amax = 0.0f;
     }
@@ -177,24 +189,26 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict_
     const float scale = amax / (float) ACT_MAX;
     const float inv = amax > 0.0f ? (float) ACT_MAX / amax : 0.0f;
 
-    const int KP = KS * 64;
-    if (k < KP) {
-        int packed[4] = { 0, 0, 0, 0 };
-        if (present) {
+    // Quantize and place in LDS: input kb + 64i + 4c + e goes to fragment i, lane
+    // rl + 16 (c/4), byte 4 (c%4) + e. Padding (absent inputs, rows >= T) is 0.
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int b0 = quant1<ACT_MAX>(xv[4 * i + 0], inv) & 0xff;
-                const int b1 = quant1<ACT_MAX>(xv[4 * i + 1], inv) & 0xff;
-                const int b2 = quant1<ACT_MAX>(xv[4 * i + 2], inv) & 0xff;
-                const int b3 = quant1<ACT_MAX>(xv[4 * i + 3], inv) & 0xff;
-                packed[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-            }
+    for (int i = 0; i < 4; ++i) {
+        int packed = 0;
+        if (present[i]) {
+            packed = (quant1<ACT_MAX>(xv[i][0], inv) & 0xff) | ((quant1<ACT_MAX>(xv[i][1], inv) & 0xff) << 8)
+                   | ((quant1<ACT_MAX>(xv[i][2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(xv[i][3], inv) & 0xff) << 24);
         }
-        const size_t dst = ((size_t) g * KS + (k >> 6)) * FRAG + (size_t) (rl + 16 * ((k & 63) >> 4)) * 16;
-        *reinterpret_cast<int4 *>(q + dst) = make_int4(packed[0], packed[1], packed[2], packed[3]);
+        stage[(i * FRAG + (rl + 16 * (c >> 2)) * 16) / 4 + (c & 3)] = packed;
     }
     if (c == 0) {
         sx[((size_t) (t >> 2) * n_blk + B) * 4 + (t & 3)] = t < T ? scale : 0.0f;
+    }
+    __syncthreads();
+    // wave w stores fragment w of the block (k-step 4B + w), if it exists
+    const int ks = 4 * B + wave;
+    if (ks < KS) {
+        const int4 v = reinterpret_cast<const int4 *>(stage)[wave * 64 + lane];
+        *reinterpret_cast<int4 *>(q + ((size_t) g * KS + ks) * FRAG + lane * 16) = v;
     }
 }
 
