@@ -237,6 +237,45 @@ def cpu_baseline(path, rows: int, reps: int):
     }
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "gemm_traffic_config5.json"
+
+
+def pmc_summary(fetch_csv: str, write_csv: str, calib_mib: int, out_path: Path) -> dict:
+    """HBM traffic per launch of the GEMM and quantize kernels from two rocprofv3 --pmc
+    runs of this script (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by
+    what the same counter reads for the calibration copy of calib_mib MiB (a device to
+    device copy, dispatched by the HIP runtime as its copy-buffer kernel)."""
+    import csv
+
+    def per_kernel(path, counter):
+        vals = {"gemm": [], "quant": [], "copy": []}
+        for row in csv.DictReader(open(path)):
+            if row["Counter_Name"] != counter:
+                continue
+            name, v = row["Kernel_Name"], float(row["Counter_Value"])
+            if "gemm_kernel" in name:
+                vals["gemm"].append(v)
+            elif "quantize_kernel" in name:
+                vals["quant"].append(v)
+            elif "copy" in name.lower():
+                vals["copy"].append(v)
+        # the calibration copy is the largest copy dispatch (weight uploads are smaller)
+        return {k: ((max(v) if k == "copy" else sum(v) / len(v)) if v else None) for k, v in vals.items()}
+
+    f = per_kernel(fetch_csv, "FETCH_SIZE")
+    w = per_kernel(write_csv, "WRITE_SIZE")
+    kib = calib_mib * 1024.0
+    fs, ws = kib / f["copy"], kib / w["copy"]
+    res = {"fetch_scale": round(fs, 4), "write_scale": round(ws, 4),
+           "calibration": f"plain device copy of {calib_mib} MiB (reads and writes {calib_mib} MiB)"}
+    for k in ("gemm", "quant"):
+        res[k] = {"fetch_bytes_per_launch": int(f[k] * fs * 1024), "write_bytes_per_launch": int(w[k] * ws * 1024),
+                  "hbm_bytes_per_launch": int((f[k] * fs + w[k] * ws) * 1024),
+                  "raw_fetch_kib": round(f[k], 1), "raw_write_kib": round(w[k], 1)}
+    out_path.write_text(json.dumps(res, indent=2) + "\n")
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -250,7 +289,14 @@ def main() -> int:
     ap.add_argument("--no-encoder1024", action="store_true")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one plain device copy of this many MiB first (PMC counter calibration)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarize two rocprofv3 --pmc counter_collection.csv files of a run with "
+                         "--calib-copy-mib into " + str(TRAFFIC_FILE.relative_to(ROOT)) + " and exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        res = pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.calib_copy_mib or 512, TRAFFIC_FILE)
+        print(json.dumps(res))
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the linear path shards by rows with no exchange; see the design notes)", file=sys.stderr)
@@ -296,6 +342,11 @@ def main() -> int:
                 "peak": PEAK_HBM_GBS, "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     roof["traffic"] = None
+    if TRAFFIC_FILE.exists() and args.rows == 65536 and not args.no_fuse:
+        tr = json.loads(TRAFFIC_FILE.read_text())
+        roof["traffic"] = tr["gemm"]["hbm_bytes_per_launch"]
+        roof["traffic_source"] = (f"{TRAFFIC_FILE.relative_to(ROOT)}: rocprofv3 FETCH_SIZE x {tr['fetch_scale']} + "
+                                  f"WRITE_SIZE x {tr['write_scale']} per GEMM launch of this workload")
     roof["kernel"] = "gemm_kernel (nxg_linear_i8)"
     roof["per_launch"] = {"algorithmic_ops": int(ops_per_launch), "algorithmic_bytes": int(bytes_per_launch),
                           "avg_us": round(avg_launch_s * 1e6, 2), "arith_intensity": round(ai, 1)}
