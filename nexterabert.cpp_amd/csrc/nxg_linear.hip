@@ -21,6 +21,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "nxg_linear.h"
@@ -533,6 +534,240 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
 }
 
 // ---------------------------------------------------------------------------
+// GEMM for n_in % 256 == 0 and N % 4 == 0: the projections of the encoder
+// ---------------------------------------------------------------------------
+
+// A 64-bit pointer that the compiler can see is the same in every lane, so that it
+// lives in an SGPR pair.
+__device__ __forceinline__ const int8_t * uniform_ptr(const int8_t * ptr) {
+    const uint64_t v = (uint64_t) (uintptr_t) ptr;
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) v);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (v >> 32));
+    return reinterpret_cast<const int8_t *>((uintptr_t) (((uint64_t) hi << 32) | lo));
+}
+
+// dma16 from a scalar base: lane l copies the 16 bytes at base + voff_l to LDS
+// address lds + 16 l. The address arithmetic stays on the scalar unit.
+__device__ __forceinline__ void dma16s(const int8_t * base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :: "v"(voff), "s"(base), "s"(lds) : "memory", "m0");
+}
+
+// The same tiles, warps and per-block epilogue as gemm_kernel, with a load
+// schedule that has no data-dependent branches inside a tile:
+//  - k-step g of the walk lives in ring slot g % 4; because a tile has a multiple
+//    of 4 k-steps, the slot of each k-step of a block is a compile-time constant;
+//  - at k-step g (after its barrier) each wave loads its 4 fragments of k-step
+//    g + 3, the last three k-steps of a tile loading the first three of the next
+//    tile (past the last tile, the last tile again: harmless re-reads that keep the
+//    counts constant); wave 0 adds block B's scales at k-step 4B;
+//  - the wait at each k-step is therefore a constant vmcnt: 8, or 9 on wave 0 for
+//    the two k-steps whose later loads include its scale load;
+//  - the output phase first waits for all loads (the next tile's first three
+//    k-steps are then in LDS, so its first block waits only at k-step 3) and only
+//    then issues its stores, which the later waits count but no longer wait behind.
+// The residual rows are loaded after the tile's last MFMAs, under the last epilogue.
+template <bool RES>
+__global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
+    __shared__ __attribute__((aligned(1024))) int8_t ring[4 * SLOT];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const tile_walk walk(blockIdx.x, gridDim.x, p.G);
+    if (walk.count == 0) return;
+    const int nb = p.KS >> 2;                        // 256-input blocks per tile
+    const size_t frow = (size_t) p.KS * FRAG;        // bytes of one fragment row
+    const uint32_t ring_lds = (uint32_t) (uintptr_t) (lds_void *) ring;
+    const uint32_t lane16 = (uint32_t) lane * 16;
+
+    struct frag_rows {                               // this wave's 4 fragment rows of a tile
+        const int8_t * a0;
+        const int8_t * a1;
+        const int8_t * w0;
+        const int8_t * w1;
+    };
+    // Tile i of the walk (clamped to the last one). A fragment rows past the last
+    // row of A re-read its last fragment row; those output rows are never stored.
+    auto rows_of = [&](int i) {
+        const int tile = walk.tile(min(i, walk.count - 1));
+        const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
+        frag_rows r;
+        r.a0 = uniform_ptr(p.a + (size_t) min(mt * (BM / 16) + wave, p.MF - 1) * frow);
+        r.a1 = uniform_ptr(p.a + (size_t) min(mt * (BM / 16) + wave + 4, p.MF - 1) * frow);
+        r.w0 = uniform_ptr(p.w + (size_t) (nt * (BN / 16) + wave) * frow);
+        r.w1 = uniform_ptr(p.w + (size_t) (nt * (BN / 16) + wave + 4) * frow);
+        return r;
+    };
+    // k-step ks of a tile into ring slot j: A fragments w and w + 4 of the slot,
+    // then B fragments w and w + 4.
+    auto issue = [&](const frag_rows & r, int ks, int j) {
+        const uint32_t vo = lane16 + (uint32_t) ks * FRAG;
+        const uint32_t m = ring_lds + (uint32_t) (j * SLOT + wave * FRAG);
+        dma16s(r.a0, vo, m);
+        dma16s(r.a1, vo, m + 4 * FRAG);
+        dma16s(r.w0, vo, m + 8 * FRAG);
+        dma16s(r.w1, vo, m + 12 * FRAG);
+    };
+    // Waits for k-step j of a block (j = 1, 2: wave 0 has its scale load among the
+    // later ones), then the barrier that publishes the slot to all waves.
+    auto arrive = [&](int j) {
+        if ((j == 1 || j == 2) && wave == 0) wait_vm<9>();
+        else wait_vm<8>();
+        lds_barrier();
+    };
+
+    v4i acc[4][4];
+    float f[4][4][4];
+    auto mma = [&](int j, bool first) {
+        const int8_t * slot = ring + j * SLOT;
+        v4i a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] = *reinterpret_cast<const v4i *>(slot + (wm * 4 + i) * FRAG + lane * 16);
+            b[i] = *reinterpret_cast<const v4i *>(slot + (8 + wn * 4 + i) * FRAG + lane * 16);
+        }
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni)
+                acc[mi][ni] = first
+                    ? __builtin_amdgcn_mfma_i32_16x16x64_i8(b[ni], a[mi], v4i{0, 0, 0, 0}, 0, 0, 0)
+                    : __builtin_amdgcn_mfma_i32_16x16x64_i8(b[ni], a[mi], acc[mi][ni], 0, 0, 0);
+    };
+
+    {
+        const frag_rows r0 = rows_of(0);
+        issue(r0, 0, 0);
+        issue(r0, 1, 1);
+        issue(r0, 2, 2);
+        wait_vm<0>();
+    }
+    for (int it = 0; it < walk.count; ++it) {
+        const int tile = walk.tile(it);
+        const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
+        const frag_rows cur = rows_of(it), nxt = rows_of(it + 1);
+        // wave 0's scale loads: lane l < 32 the sx of row group l of the tile, lane
+        // l >= 32 the sw of columns 4(l-32)..+3; block B adds B * sstep bytes.
+        const float * ssrc;
+        size_t sstep;
+        if (lane < 32) {
+            ssrc = p.sx + (size_t) min(mt * (BM / 4) + lane, p.MF * 4 - 1) * p.n_blk * 4;
+            sstep = 16;
+        } else {
+            ssrc = p.sw + (size_t) nt * BN + 4 * (lane - 32);
+            sstep = (size_t) p.NP * sizeof(float);
+        }
+        v4f rv[4][4];                                // residual rows (RES)
+        const int rrow = lane >> 4, rcol = 4 * (lane & 15);
+        const int tbase = mt * BM + wm * 64, ncol = nt * BN + wn * 64 + rcol;
+        const bool col_ok = ncol < p.N;
+        // Residual rows of pieces m0 and m0 + 1 (half before the last epilogue, half
+        // after it, to stay within the register budget). Full row tiles: a scalar row
+        // base plus one 32-bit lane offset; the last row tile clamps rows to T - 1
+        // (never stored). Columns past N read the last 4 columns (never stored).
+        auto load_res = [&](int m0) {
+            const int row0 = mt * BM + wm * 64;
+            const uint32_t col = (uint32_t) min(ncol, p.N - 4);
+            if (row0 + 64 <= p.T) {
+                const uint32_t lo = (uint32_t) rrow * (uint32_t) p.N + col;
+#pragma unroll
+                for (int mi = m0; mi < m0 + 2; ++mi)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        rv[mi][q] = *reinterpret_cast<const v4f *>(p.res + (size_t) (row0 + mi * 16 + 4 * q) * p.N + lo);
+            } else {
+#pragma unroll
+                for (int mi = m0; mi < m0 + 2; ++mi)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int t = min(row0 + mi * 16 + 4 * q + rrow, p.T - 1);
+                        rv[mi][q] = *reinterpret_cast<const v4f *>(p.res + (size_t) t * p.N + col);
+                    }
+            }
+        };
+
+        // One 256-input block: its 4 k-steps, then the epilogue. LAST: the tile's last
+        // block, whose k-steps 1..3 load the next tile's first three.
+        auto run_block = [&](int B, auto last_tag) {
+            constexpr bool last = decltype(last_tag)::value;
+            // k-step 4B (slot 0). In block 0 k-steps 0..2 are already in LDS.
+            if (B > 0) arrive(0); else lds_barrier();
+            issue(cur, 4 * B + 3, 3);
+            if (wave == 0) dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, ring + 3 * SLOT + SLOT_AB);
+            mma(0, true);
+            // k-step 4B + 1 (slot 1)
+            if (B > 0) arrive(1); else lds_barrier();
+            if (last) issue(nxt, 0, 0); else issue(cur, 4 * B + 4, 0);
+            mma(1, false);
+            // k-step 4B + 2 (slot 2)
+            if (B > 0) arrive(2); else lds_barrier();
+            if (last) issue(nxt, 1, 1); else issue(cur, 4 * B + 5, 1);
+            mma(2, false);
+            // k-step 4B + 3 (slot 3, with the block's scales)
+            arrive(3);
+            if (last) issue(nxt, 2, 2); else issue(cur, 4 * B + 6, 2);
+            mma(3, false);
+            if (RES && last) load_res(0);
+
+            // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
+            const float * scl = reinterpret_cast<const float *>(ring + 3 * SLOT + SLOT_AB);
+            float sxv[4];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) sxv[mi] = scl[wm * 64 + mi * 16 + (lane & 15)];
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const float4 sw4 = *reinterpret_cast<const float4 *>(scl + 128 + wn * 64 + ni * 16 + 4 * (lane >> 4));
+                const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float prod = (float) acc[mi][ni][r] * sxv[mi];
+                        // block 0 starts from f = 0: fma(prod, sw, +0.0)
+                        f[mi][ni][r] = __builtin_fmaf(prod, swr[r], B == 0 ? 0.0f : f[mi][ni][r]);
+                    }
+            }
+            if (RES && last) load_res(2);
+        };
+        for (int B = 0; B < nb - 1; ++B) run_block(B, std::false_type{});
+        run_block(nb - 1, std::true_type{});
+
+        // Output through LDS, whole 128-byte lines per store. Slot 3 is free once
+        // every wave has passed this barrier (the next tile's k-step 3 is loaded only
+        // after its first barrier); each wave owns 4352 bytes of it, 16 rows of 64
+        // floats at a 272-byte pitch. Per 16-token piece mi: write it in MFMA order
+        // (lane: token lane%16, features 16ni + 4(lane/16) + 0..3), read it back as 4
+        // rows of 256 bytes per instruction and store whole lines.
+        lds_barrier();
+        wait_vm<0>();
+        float * stg = reinterpret_cast<float *>(ring + 3 * SLOT + wave * 4352);
+        const int trow = lane & 15, tcol = 4 * (lane >> 4);
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const v4f y = { f[mi][ni][0], f[mi][ni][1], f[mi][ni][2], f[mi][ni][3] };
+                *reinterpret_cast<v4f *>(stg + trow * 68 + 16 * ni + tcol) = y;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int row = 4 * q + rrow;
+                v4f y = *reinterpret_cast<const v4f *>(stg + row * 68 + rcol);
+                const int t = tbase + mi * 16 + row;
+                if (t < p.T && col_ok) {
+                    if (RES) y = rv[mi][q] + y;
+                    __builtin_nontemporal_store(y, reinterpret_cast<v4f *>(p.out + (size_t) t * p.N + ncol));
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+    }
+    wait_vm<0>();
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
@@ -736,6 +971,9 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     if (sums) {
         if (k256) gemm_kernel<false, true, true><<<grid, block, 0, s>>>(p);
         else      gemm_kernel<false, true, false><<<grid, block, 0, s>>>(p);
+    } else if (k256 && NXG_WG_PER_CU > 0 && p.N % 4 == 0) {
+        if (residual) gemm_k256<true><<<grid, block, 0, s>>>(p);
+        else          gemm_k256<false><<<grid, block, 0, s>>>(p);
     } else if (residual) {
         if (k256) gemm_kernel<true, false, true><<<grid, block, 0, s>>>(p);
         else      gemm_kernel<true, false, false><<<grid, block, 0, s>>>(p);
