@@ -123,6 +123,13 @@ NXG_API size_t nxg_qact_sx_bytes(int32_t T, int32_t n_in);
 NXG_API int32_t nxg_quantize_rows(const float * x, int32_t T, int32_t n_in, int32_t act_max,
                                   int8_t * q, float * sx, void * stream);
 
+/* op_relu_sqr with an int8 consumer (src/nexterabert.cpp:484-505, quantized by
+ * for_rows, :414-438; chosen by row_op(..., int8_only(c_proj)), :1287-1288): every
+ * element becomes r*r with r = x > 0 ? x : 0 (a NaN gives 0), then quantize_row as
+ * nxg_quantize_rows. Same arguments. */
+NXG_API int32_t nxg_quantize_rows_relu2(const float * x, int32_t T, int32_t n_in, int32_t act_max,
+                                        int8_t * q, float * sx, void * stream);
+
 /* The qact buffers in the reference's own format (src/nexterabert.cpp:368-375):
  *   u8  device uint8 [T][n_in], the reference's u8 values (q + act_max + 1)
  *   sx_ref device float, ((T+3)/4)*n_blk*4 floats, [token/4][block][token%4] */
@@ -159,6 +166,21 @@ NXG_API int32_t nxg_linear_i8(const nxg_weight * w, const int8_t * q, const floa
 /* The same for T rows given directly. */
 NXG_API int32_t nxg_linear_i8_rows(const nxg_weight * w, const int8_t * q, const float * sx, int32_t T,
                                    const float * residual, float * out, void * stream);
+
+/* The MLP's c_fc -> relu^2 -> int8 in one pass (src/nexterabert.cpp:1286-1288: linear
+ * of c_fc, then op_relu_sqr quantized for the int8 c_proj): the fp32 linear output f of
+ * nxg_linear_i8 (no residual) is never written; q_out, sx_out receive exactly what
+ * nxg_quantize_rows_relu2 would produce from it, a qact of T rows by n_out inputs
+ * (sizes nxg_qact_q_bytes(T, n_out), nxg_qact_sx_bytes(T, n_out)), padding included.
+ * Needs n_in % 256 == 0 and n_out % 32 == 0 (NXG_EINVAL otherwise); act_max is that of
+ * the consumer, 127 or 63. */
+NXG_API int32_t nxg_linear_i8_relu2_q8(const nxg_weight * w, const int8_t * q, const float * sx,
+                                       const int32_t * cu_offsets, int32_t n_seqs, int32_t act_max,
+                                       int8_t * q_out, float * sx_out, void * stream);
+
+/* The same for T rows given directly. */
+NXG_API int32_t nxg_linear_i8_relu2_q8_rows(const nxg_weight * w, const int8_t * q, const float * sx, int32_t T,
+                                            int32_t act_max, int8_t * q_out, float * sx_out, void * stream);
 
 /* The int32 block sums s_B of the same GEMM: sums device int32 [n_blk][T][n_out],
  * equal to the reference's sum_i w8*u8 + off (src/nexterabert.cpp:892-916). For tests. */

@@ -65,6 +65,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_qact_q_bytes": ([i32, i32], sz),
         "nxg_qact_sx_bytes": ([i32, i32], sz),
         "nxg_quantize_rows": ([P, i32, i32, i32, P, P, P], i32),
+        "nxg_quantize_rows_relu2": ([P, i32, i32, i32, P, P, P], i32),
         "nxg_qact_export": ([P, P, i32, i32, i32, P, P, P], i32),
         "nxg_weight_create": ([P, P, i32, i32, ctypes.POINTER(P)], i32),
         "nxg_weight_destroy": ([P], None),
@@ -74,6 +75,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_linear_i8": ([P, P, P, P, i32, P, P, P], i32),
         "nxg_linear_i8_rows": ([P, P, P, i32, P, P, P], i32),
         "nxg_linear_i8_block_sums": ([P, P, i32, P, P], i32),
+        "nxg_linear_i8_relu2_q8": ([P, P, P, P, i32, i32, P, P, P], i32),
+        "nxg_linear_i8_relu2_q8_rows": ([P, P, P, i32, i32, P, P, P], i32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(L, name)
@@ -232,17 +235,26 @@ def qact_alloc(T: int, n_in: int, act_max: int = 127, device="cuda") -> QAct:
                 torch.empty(max(sb // 4, 1), dtype=torch.float32, device=device), T, n_in, act_max)
 
 
-def quantize_rows(x, act_max: int = 127, out: Optional[QAct] = None, stream=None) -> QAct:
-    """quantize_row over every row of x (device f32 [T][n_in])."""
+def _quantize(fn_name: str, x, act_max: int, out: Optional[QAct], stream) -> QAct:
     torch = _torch()
     if x.dtype != torch.float32 or x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
         raise ValueError("x must be a contiguous 2-D float32 device tensor")
     T, n_in = x.shape
     qa = out if out is not None else qact_alloc(T, n_in, act_max, x.device)
     qa.T, qa.n_in, qa.act_max = T, n_in, act_max
-    _check(load_library().nxg_quantize_rows(x.data_ptr(), T, n_in, act_max, qa.q.data_ptr(), qa.sx.data_ptr(),
-                                             _stream_ptr(stream)), "quantize_rows")
+    fn = getattr(load_library(), fn_name)
+    _check(fn(x.data_ptr(), T, n_in, act_max, qa.q.data_ptr(), qa.sx.data_ptr(), _stream_ptr(stream)), fn_name)
     return qa
+
+
+def quantize_rows(x, act_max: int = 127, out: Optional[QAct] = None, stream=None) -> QAct:
+    """quantize_row over every row of x (device f32 [T][n_in])."""
+    return _quantize("nxg_quantize_rows", x, act_max, out, stream)
+
+
+def quantize_rows_relu2(x, act_max: int = 127, out: Optional[QAct] = None, stream=None) -> QAct:
+    """op_relu_sqr quantized for an int8 consumer: quantize_row of relu(x)^2 per row."""
+    return _quantize("nxg_quantize_rows_relu2", x, act_max, out, stream)
 
 
 def export_qact(qa: QAct, stream=None):
@@ -288,6 +300,30 @@ def linear_i8(weight: DeviceWeight, qa: QAct, residual=None, cu_offsets: Optiona
                                   out.data_ptr(), _stream_ptr(stream))
     _check(rc, "linear_i8")
     return out
+
+
+def linear_i8_relu2_q8(weight: DeviceWeight, qa: QAct, act_max: int = 127,
+                       cu_offsets: Optional[Sequence[int]] = None, out: Optional[QAct] = None,
+                       stream=None) -> QAct:
+    """c_fc -> relu^2 -> int8 in one pass: the qact (T rows by n_out inputs) that
+    quantize_rows_relu2 would make from linear_i8(weight, qa), without the fp32 rows."""
+    if qa.n_in != weight.n_in:
+        raise ValueError(f"n_in mismatch: activations {qa.n_in}, weight {weight.n_in}")
+    T = qa.T
+    res = out if out is not None else qact_alloc(T, weight.n_out, act_max, qa.q.device)
+    res.T, res.n_in, res.act_max = T, weight.n_out, act_max
+    L = load_library()
+    if cu_offsets is not None:
+        cu = np.ascontiguousarray(cu_offsets, dtype=np.int32)
+        if cu.size < 2 or int(cu[-1]) != T:
+            raise ValueError(f"cu_offsets must end at T={T}")
+        rc = L.nxg_linear_i8_relu2_q8(weight.handle, qa.q.data_ptr(), qa.sx.data_ptr(), _np_ptr(cu), cu.size - 1,
+                                      act_max, res.q.data_ptr(), res.sx.data_ptr(), _stream_ptr(stream))
+    else:
+        rc = L.nxg_linear_i8_relu2_q8_rows(weight.handle, qa.q.data_ptr(), qa.sx.data_ptr(), T, act_max,
+                                           res.q.data_ptr(), res.sx.data_ptr(), _stream_ptr(stream))
+    _check(rc, "linear_i8_relu2_q8")
+    return res
 
 
 def block_sums(weight: DeviceWeight, qa: QAct, stream=None):
@@ -338,6 +374,20 @@ class Builder:
             raise KeyError(f"{name} is not an int8 weight")
         qa = x if isinstance(x, QAct) else self.quantized(x)
         return linear_i8(w, qa, residual=residual, cu_offsets=cu_offsets, out=out)
+
+    def mlp(self, fc: str, proj: str, h, x, cu_offsets=None, out=None):
+        """x + c_proj(relu(c_fc(h))^2) (src/nexterabert.cpp:1284-1289). With both weights
+        int8, relu^2 is quantized where c_fc's output is made (one fused pass when the
+        shapes allow it, else c_fc in fp32 then quantize_rows_relu2)."""
+        w_fc, w_proj = self.i8.get(fc), self.i8.get(proj)
+        if w_fc is None or w_proj is None:
+            raise KeyError(f"{fc} and {proj} must both be int8 weights")
+        qa = h if isinstance(h, QAct) else self.quantized(h)
+        if w_fc.n_in % 256 == 0 and w_fc.n_out % 32 == 0:
+            r = linear_i8_relu2_q8(w_fc, qa, self.act_max, cu_offsets=cu_offsets)
+        else:
+            r = quantize_rows_relu2(linear_i8(w_fc, qa, cu_offsets=cu_offsets), self.act_max)
+        return linear_i8(w_proj, r, residual=x, cu_offsets=cu_offsets, out=out)
 
     def reset(self) -> None:
         """Drops the quantized copies (the reference rebuilds its graph per forward)."""

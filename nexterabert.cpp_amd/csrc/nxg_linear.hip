@@ -37,6 +37,8 @@ constexpr int FRAG = 1024;       // bytes of one 16-row x 64-input fragment
 constexpr int BM = 128;          // GEMM workgroup tile: rows (tokens)
 constexpr int BN = 128;          //                      columns (output features)
 constexpr int NTHREADS = 256;    // 4 waves, 2 x 2, each 64 x 64
+constexpr int WBN = 256;         // relu^2 -> int8 GEMM tile columns: one 256-input block of the next linear
+constexpr int WTHREADS = 512;    // relu^2 -> int8 GEMM: 8 waves, 2 x 4, each 64 x 64
 constexpr int N_XCD = 8;         // MI355X: 8 XCDs, workgroups dispatched round-robin
 #ifndef NXG_WG_PER_CU
 #define NXG_WG_PER_CU 2          // persistent GEMM workgroups per CU (0: one workgroup per tile)
@@ -105,7 +107,9 @@ __device__ __forceinline__ int quant1(float x, float inv) {
 // 4w..4w+3; the 16 lanes of a row read its 256 inputs as 4 contiguous 256-byte
 // pieces, so lane c holds inputs 64i + 4c + e (i, e = 0..3). The int8 results are
 // gathered in LDS in fragment order and each wave stores one 1 KiB fragment.
-template <int ACT_MAX>
+// RELU2: the rows are relu(x)^2 of the input (x > 0 ? x : 0, NaN giving 0, then
+// r * r), the reference's op_relu_sqr with an int8 consumer (src/nexterabert.cpp:484-505).
+template <int ACT_MAX, bool RELU2>
 __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict__ x, int T, int n_in, int KS,
                                                        int n_blk, int8_t * __restrict__ q, float * __restrict__ sx) {
     __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
@@ -125,6 +129,13 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict_
         if (present[i]) {
             const v4f f = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(x + (size_t) t * n_in + kb + 64 * i + 4 * c));
             xv[i][0] = f.x; xv[i][1] = f.y; xv[i][2] = f.z; xv[i][3] = f.w;
+            if (RELU2) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float r = xv[i][e] > 0.0f ? xv[i][e] : 0.0f;
+                    xv[i][e] = r * r;
+                }
+            }
         } else {
             xv[i][0] = xv[i][1] = xv[i][2] = xv[i][3] = 0.0f;
         }
@@ -251,6 +262,10 @@ struct gemm_params {
     int32_t *      sums;  // [n_blk][T][N] (block-sum variant)
     int T, N, NP, KS, n_blk, MF, n_mt, n_nt;
     int G;                // tiles: n_mt * n_nt
+    // relu^2 -> int8 output (gemm_wide): the next linear's activation tiles, N channels
+    int8_t *       qo;    // MF x KSo fragments
+    float *        sxo;   // [MP/4][n_nt][4]
+    int KSo;              // ceil(N / 64)
 };
 
 // Tiles of one workgroup. Workgroups are dispatched to the 8 XCDs round-robin
@@ -768,6 +783,245 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
 }
 
 // ---------------------------------------------------------------------------
+// Wide GEMM with the relu^2 -> int8 output: 128 x 256 tiles, n_in % 256 == 0
+// ---------------------------------------------------------------------------
+
+constexpr int WSLOT = (BM / 16 + WBN / 16) * FRAG;   // 24 KiB: 8 A + 16 B fragments
+constexpr int WSCALE = 4 * (BM + WBN);               // sx of 128 rows, then sw of 256 columns
+
+// Across the four 16-lane rows of a wave: lane l gets the maximum of lanes
+// l % 16 + 16 r, r = 0..3 (values without NaN).
+__device__ __forceinline__ float rows_max(float m) {
+    // ([lo, lo], [hi, hi]): row r now holds max(row r % 2, row r % 2 + 2)
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_int(m), __float_as_int(m), false, false);
+    m = fmaxf(__int_as_float(h[0]), __int_as_float(h[1]));
+    // ([r0, r0, r2, r2], [r1, r1, r3, r3]): every row the maximum of the four
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_int(m), __float_as_int(m), false, false);
+    return fmaxf(__int_as_float(q[0]), __int_as_float(q[1]));
+}
+
+// 4 x 4 transpose of (16-lane row, register): on entry row g of d[j] holds item (g, j),
+// on exit row j of d[g] holds it. permlane32_swap(a, b) gives ([a.lo, b.lo], [a.hi, b.hi])
+// in 32-lane halves, permlane16_swap(a, b) gives ([a.r0, b.r0, a.r2, b.r2],
+// [a.r1, b.r1, a.r3, b.r3]) in 16-lane rows.
+__device__ __forceinline__ void rows_transpose(int (&d)[4]) {
+    const auto s02 = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+    const auto s13 = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+    const auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+    const auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    d[0] = s01[0]; d[1] = s01[1]; d[2] = s23[0]; d[3] = s23[1];
+}
+
+// relu(linear(x))^2 quantized for the next linear, the reference's op_relu_sqr feeding
+// an int8 linear (src/nexterabert.cpp:484-505 through for_rows' quantize_row, :414-438;
+// the MLP's c_fc -> c_proj, :1284-1289). One workgroup per CU: 8 waves (2 x 4), each
+// computing the same 64 x 64 piece as in gemm_k256, over a 128 x 256 tile -- exactly one
+// 256-input block of the next linear, so a row's block amax is reduced here (over the
+// lanes of a wave, then over the 4 waves through LDS) and each wave stores whole 1 KiB
+// activation fragments; the fp32 rows are never written. The k-step schedule is
+// gemm_k256's: ring slot g % 4; after k-step g's barrier each wave loads its A fragment
+// and its 2 B fragments of k-step g + 3, the last three k-steps of a tile loading the
+// first three of the next; constant waits (6 later loads; 7 on waves 0 and 1 at the two
+// k-steps whose later loads include their scale loads). The block scales have an LDS
+// area of their own.
+template <int ACT_MAX>
+__global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
+    __shared__ __attribute__((aligned(1024))) int8_t ring[4 * WSLOT];
+    __shared__ __attribute__((aligned(16))) float scl[WSCALE / 4];
+    __shared__ __attribute__((aligned(16))) float am[2 * 64 * 4];   // row maxima [wm][row][wn]
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const tile_walk walk(blockIdx.x, gridDim.x, p.G);
+    if (walk.count == 0) return;
+    const int nb = p.KS >> 2;                        // 256-input blocks per tile
+    const size_t frow = (size_t) p.KS * FRAG;        // bytes of one fragment row
+    const uint32_t ring_lds = (uint32_t) (uintptr_t) (lds_void *) ring;
+    const uint32_t lane16 = (uint32_t) lane * 16;
+
+    struct frag_rows {                               // this wave's 3 fragment rows of a tile
+        const int8_t * a;
+        const int8_t * w0;
+        const int8_t * w1;
+    };
+    auto rows_of = [&](int i) {                      // tile i of the walk (clamped)
+        const int tile = walk.tile(min(i, walk.count - 1));
+        const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
+        frag_rows r;
+        r.a = uniform_ptr(p.a + (size_t) min(mt * (BM / 16) + wave, p.MF - 1) * frow);
+        r.w0 = uniform_ptr(p.w + (size_t) (nt * (WBN / 16) + wave) * frow);
+        r.w1 = uniform_ptr(p.w + (size_t) (nt * (WBN / 16) + wave + 8) * frow);
+        return r;
+    };
+    // k-step ks of a tile into ring slot j: A fragment w, B fragments w and w + 8.
+    auto issue = [&](const frag_rows & r, int ks, int j) {
+        const uint32_t vo = lane16 + (uint32_t) ks * FRAG;
+        const uint32_t m = ring_lds + (uint32_t) (j * WSLOT + wave * FRAG);
+        dma16s(r.a, vo, m);
+        dma16s(r.w0, vo, m + 8 * FRAG);
+        dma16s(r.w1, vo, m + 16 * FRAG);
+    };
+    auto arrive = [&](int j) {
+        if ((j == 1 || j == 2) && wave < 2) wait_vm<7>();
+        else wait_vm<6>();
+        lds_barrier();
+    };
+
+    v4i acc[4][4];
+    float f[4][4][4];
+    auto mma = [&](int j, bool first) {
+        const int8_t * slot = ring + j * WSLOT;
+        v4i a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] = *reinterpret_cast<const v4i *>(slot + (wm * 4 + i) * FRAG + lane * 16);
+            b[i] = *reinterpret_cast<const v4i *>(slot + (8 + wn * 4 + i) * FRAG + lane * 16);
+        }
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni)
+                acc[mi][ni] = first
+                    ? __builtin_amdgcn_mfma_i32_16x16x64_i8(b[ni], a[mi], v4i{0, 0, 0, 0}, 0, 0, 0)
+                    : __builtin_amdgcn_mfma_i32_16x16x64_i8(b[ni], a[mi], acc[mi][ni], 0, 0, 0);
+    };
+
+    {
+        const frag_rows r0 = rows_of(0);
+        issue(r0, 0, 0);
+        issue(r0, 1, 1);
+        issue(r0, 2, 2);
+        wait_vm<0>();
+    }
+    for (int it = 0; it < walk.count; ++it) {
+        const int tile = walk.tile(it);
+        const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
+        const frag_rows cur = rows_of(it), nxt = rows_of(it + 1);
+        // Scale loads of block B (B * sstep bytes on): wave 0 lane l < 32 the sx of row
+        // group l, wave 0 lane l >= 32 the sw of columns 4(l-32)..+3, wave 1 lane l < 32
+        // the sw of columns 128 + 4l..+3; lane l lands at scl + 16 l (+ 1024 on wave 1).
+        const float * ssrc;
+        size_t sstep;
+        if (wave == 0 && lane < 32) {
+            ssrc = p.sx + (size_t) min(mt * (BM / 4) + lane, p.MF * 4 - 1) * p.n_blk * 4;
+            sstep = 16;
+        } else {
+            ssrc = p.sw + (size_t) nt * WBN + (wave == 0 ? 4 * (lane - 32) : 128 + 4 * lane);
+            sstep = (size_t) p.NP * sizeof(float);
+        }
+        const int tbase = mt * BM + wm * 64;
+
+        auto run_block = [&](int B, auto last_tag) {
+            constexpr bool last = decltype(last_tag)::value;
+            // k-step 4B (slot 0). In block 0 k-steps 0..2 are already in LDS.
+            if (B > 0) arrive(0); else lds_barrier();
+            issue(cur, 4 * B + 3, 3);
+            if (wave == 0) {
+                dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl);
+            } else if (wave == 1 && lane < 32) {
+                dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, reinterpret_cast<const char *>(scl) + 1024);
+            }
+            mma(0, true);
+            // k-step 4B + 1 (slot 1)
+            if (B > 0) arrive(1); else lds_barrier();
+            if (last) issue(nxt, 0, 0); else issue(cur, 4 * B + 4, 0);
+            mma(1, false);
+            // k-step 4B + 2 (slot 2)
+            if (B > 0) arrive(2); else lds_barrier();
+            if (last) issue(nxt, 1, 1); else issue(cur, 4 * B + 5, 1);
+            mma(2, false);
+            // k-step 4B + 3 (slot 3); the block's scales arrive with it
+            arrive(3);
+            if (last) issue(nxt, 2, 2); else issue(cur, 4 * B + 6, 2);
+            mma(3, false);
+
+            // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
+            float sxv[4];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) sxv[mi] = scl[wm * 64 + mi * 16 + (lane & 15)];
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const float4 sw4 = *reinterpret_cast<const float4 *>(scl + BM + wn * 64 + ni * 16 + 4 * (lane >> 4));
+                const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float prod = (float) acc[mi][ni][r] * sxv[mi];
+                        // block 0 starts from f = 0: fma(prod, sw, +0.0)
+                        f[mi][ni][r] = __builtin_fmaf(prod, swr[r], B == 0 ? 0.0f : f[mi][ni][r]);
+                    }
+            }
+        };
+        for (int B = 0; B < nb - 1; ++B) run_block(B, std::false_type{});
+        run_block(nb - 1, std::true_type{});
+
+        // Every load of this wave first: the next tile's first three k-steps (its block
+        // 0 then waits only at k-step 3, and the stores below stand behind no load it
+        // waits for).
+        wait_vm<0>();
+        {
+            // relu(f)^2 in place: f > 0 ? f : 0 (a NaN gives 0), then r * r.
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float x = f[mi][ni][r] > 0.0f ? f[mi][ni][r] : 0.0f;
+                        f[mi][ni][r] = x * x;
+                    }
+            // Row maxima (values >= 0, no NaN: the reference's MAXPS fold is the plain
+            // maximum here): over this lane's 16 values, the wave's 4 lanes of the row,
+            // then the 4 waves of the row through LDS, am[wm][row][wn].
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                float m = 0.0f;
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) m = fmaxf(m, f[mi][ni][r]);
+                m = rows_max(m);
+                if (lane < 16) am[(wm * 64 + mi * 16 + lane) * 4 + wn] = m;
+            }
+            lds_barrier();
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                const int t = tbase + mi * 16 + (lane & 15);
+                const v4f a4 = *reinterpret_cast<const v4f *>(am + (wm * 64 + mi * 16 + (lane & 15)) * 4);
+                const bool row_ok = t < p.T;
+                const float amax = row_ok ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
+                const float scale = amax / (float) ACT_MAX;
+                const float inv = amax > 0.0f ? (float) ACT_MAX / amax : 0.0f;
+                // column 16ni + 4(lane/16) + r of the wave's 64: byte r of d[ni]
+                int d[4];
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) {
+                    const int n = nt * WBN + wn * 64 + ni * 16 + 4 * (lane >> 4);
+                    int packed = 0;
+                    if (row_ok && n < p.N) {
+                        packed = (quant1<ACT_MAX>(f[mi][ni][0], inv) & 0xff) | ((quant1<ACT_MAX>(f[mi][ni][1], inv) & 0xff) << 8)
+                               | ((quant1<ACT_MAX>(f[mi][ni][2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(f[mi][ni][3], inv) & 0xff) << 24);
+                    }
+                    d[ni] = packed;
+                }
+                // lane c + 16 j now gets columns 16 j + 0..15 of row c: one fragment lane
+                rows_transpose(d);
+                const int rf = mt * (BM / 16) + wm * 4 + mi, kf = nt * (WBN / 64) + wn;
+                if (rf < p.MF) {
+                    if (kf < p.KSo) {
+                        *reinterpret_cast<v4i *>(p.qo + ((size_t) rf * p.KSo + kf) * FRAG + lane * 16) = v4i{d[0], d[1], d[2], d[3]};
+                    }
+                    if (wn == 0 && lane < 16) p.sxo[((size_t) (t >> 2) * p.n_nt + nt) * 4 + (t & 3)] = scale;
+                }
+            }
+        }
+    }
+    wait_vm<0>();
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
@@ -849,8 +1103,8 @@ size_t nxg_qact_sx_bytes(int32_t T, int32_t n_in) {
     return qact_dims_of(T, n_in, d) ? (size_t) d.MP * d.n_blk * sizeof(float) : 0;
 }
 
-int32_t nxg_quantize_rows(const float * x, int32_t T, int32_t n_in, int32_t act_max,
-                          int8_t * q, float * sx, void * stream) {
+static int32_t launch_quantize(const float * x, int32_t T, int32_t n_in, int32_t act_max,
+                               int8_t * q, float * sx, void * stream, bool relu2) {
     qact_dims d;
     if (!qact_dims_of(T, n_in, d)) return fail(NXG_EINVAL, "quantize: T=%d n_in=%d (n_in must be a positive multiple of 32)", T, n_in);
     if (act_max != 127 && act_max != 63) return fail(NXG_EINVAL, "quantize: act_max must be 127 or 63, got %d", act_max);
@@ -861,11 +1115,23 @@ int32_t nxg_quantize_rows(const float * x, int32_t T, int32_t n_in, int32_t act_
     const dim3 grid(d.MP / 16, d.n_blk);
     hipStream_t s = (hipStream_t) stream;
     if (act_max == 127) {
-        quantize_kernel<127><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
+        if (relu2) quantize_kernel<127, true><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
+        else       quantize_kernel<127, false><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
     } else {
-        quantize_kernel<63><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
+        if (relu2) quantize_kernel<63, true><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
+        else       quantize_kernel<63, false><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
     }
     return launch_check("quantize_kernel");
+}
+
+int32_t nxg_quantize_rows(const float * x, int32_t T, int32_t n_in, int32_t act_max,
+                          int8_t * q, float * sx, void * stream) {
+    return launch_quantize(x, T, n_in, act_max, q, sx, stream, false);
+}
+
+int32_t nxg_quantize_rows_relu2(const float * x, int32_t T, int32_t n_in, int32_t act_max,
+                                int8_t * q, float * sx, void * stream) {
+    return launch_quantize(x, T, n_in, act_max, q, sx, stream, true);
 }
 
 int32_t nxg_qact_export(const int8_t * q, const float * sx, int32_t T, int32_t n_in, int32_t act_max,
@@ -901,7 +1167,7 @@ int32_t nxg_weight_create(const int8_t * w, const float * scale, int32_t n_in, i
     W->n_out = n_out;
     W->n_blk = ceil_div(n_in, BLK);
     W->KS = ceil_div(n_in, 64);
-    W->NP = ceil_div(n_out, BN) * BN;
+    W->NP = ceil_div(n_out, WBN) * WBN;   // whole tiles of the widest kernel
     const size_t wbytes = (size_t) W->NP * W->KS * 64;
     const size_t sbytes = (size_t) W->n_blk * W->NP * sizeof(float);
     // Re-layout on the host into fragment tiles (zero padding), then one copy.
@@ -934,12 +1200,33 @@ int32_t nxg_weight_n_in(const nxg_weight * W) { return W ? W->n_in : 0; }
 int32_t nxg_weight_n_out(const nxg_weight * W) { return W ? W->n_out : 0; }
 size_t nxg_weight_device_bytes(const nxg_weight * W) { return W ? W->bytes : 0; }
 
+// Where a GEMM writes: fp32 rows (+ residual), per-block int32 sums, or relu^2
+// quantized for the next linear.
+struct gemm_out {
+    const float * residual = nullptr;
+    float *       out = nullptr;
+    int32_t *     sums = nullptr;
+    int8_t *      qo = nullptr;
+    float *       sxo = nullptr;
+    int           act_max = 127;
+};
+
 static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float * sx, int32_t T,
-                           const float * residual, float * out, int32_t * sums, void * stream) {
+                           const gemm_out & o, void * stream) {
     if (!W) return fail(NXG_EINVAL, "linear: null weight");
     if (T < 0) return fail(NXG_EINVAL, "linear: T=%d", T);
     if (T == 0) return NXG_OK;
-    if (!q || (!sums && (!sx || !out))) return fail(NXG_EINVAL, "linear: null buffer");
+    if (!q || (!o.sums && !sx) || (!o.sums && !o.qo && !o.out) || (o.qo && !o.sxo)) {
+        return fail(NXG_EINVAL, "linear: null buffer");
+    }
+    const bool k256 = W->KS % 4 == 0;
+    if (o.qo) {
+        if (!k256 || W->n_out % 32 != 0) {
+            return fail(NXG_EINVAL, "linear_relu2_q8: needs n_in %% 256 == 0 and n_out %% 32 == 0 (n_in=%d n_out=%d)",
+                        W->n_in, W->n_out);
+        }
+        if (o.act_max != 127 && o.act_max != 63) return fail(NXG_EINVAL, "linear_relu2_q8: act_max must be 127 or 63, got %d", o.act_max);
+    }
     int rc = check_device();
     if (rc) return rc;
     gemm_params p;
@@ -947,34 +1234,47 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     p.sx = sx;
     p.w = W->w;
     p.sw = W->sw;
-    p.res = residual;
-    p.out = out;
-    p.sums = sums;
+    p.res = o.residual;
+    p.out = o.out;
+    p.sums = o.sums;
+    p.qo = o.qo;
+    p.sxo = o.sxo;
     p.T = T;
     p.N = W->n_out;
     p.NP = W->NP;
     p.KS = W->KS;
+    p.KSo = ceil_div(p.N, 64);
     p.n_blk = W->n_blk;
     p.MF = ceil_div(T, 16);
     p.n_mt = ceil_div(T, BM);
-    p.n_nt = W->NP / BN;
+    hipStream_t s = (hipStream_t) stream;
+    if (o.qo) {
+        // relu^2 -> int8: 128 x 256 tiles (a whole 256-column block), one workgroup per CU
+        p.n_nt = ceil_div(p.N, WBN);
+        const long long G = (long long) p.n_mt * p.n_nt;
+        if (G > INT32_MAX / 2) return fail(NXG_EINVAL, "linear: T=%d too large", T);
+        p.G = (int) G;
+        const dim3 grid((unsigned) std::min<long long>(G, device_cus())), block(WTHREADS);
+        if (o.act_max == 127) gemm_relu2_q8<127><<<grid, block, 0, s>>>(p);
+        else                  gemm_relu2_q8<63><<<grid, block, 0, s>>>(p);
+        return launch_check("gemm_relu2_q8");
+    }
+    p.n_nt = ceil_div(p.N, BN);
     const long long G = (long long) p.n_mt * p.n_nt;
     if (G > INT32_MAX / 2) return fail(NXG_EINVAL, "linear: T=%d too large", T);
     p.G = (int) G;
-    hipStream_t s = (hipStream_t) stream;
-    const bool k256 = W->KS % 4 == 0;
     // K256: persistent workgroups, two per CU (the LDS ring needs 68 KiB of the 160);
     // otherwise one workgroup per tile.
     const int n_wg = (k256 && NXG_WG_PER_CU > 0) ? (int) std::min<long long>(G, (long long) NXG_WG_PER_CU * device_cus())
                                                  : (int) G;
     const dim3 grid((unsigned) n_wg), block(NTHREADS);
-    if (sums) {
+    if (o.sums) {
         if (k256) gemm_kernel<false, true, true><<<grid, block, 0, s>>>(p);
         else      gemm_kernel<false, true, false><<<grid, block, 0, s>>>(p);
     } else if (k256 && NXG_WG_PER_CU > 0 && p.N % 4 == 0) {
-        if (residual) gemm_k256<true><<<grid, block, 0, s>>>(p);
-        else          gemm_k256<false><<<grid, block, 0, s>>>(p);
-    } else if (residual) {
+        if (o.residual) gemm_k256<true><<<grid, block, 0, s>>>(p);
+        else            gemm_k256<false><<<grid, block, 0, s>>>(p);
+    } else if (o.residual) {
         if (k256) gemm_kernel<true, false, true><<<grid, block, 0, s>>>(p);
         else      gemm_kernel<true, false, false><<<grid, block, 0, s>>>(p);
     } else {
@@ -984,14 +1284,8 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     return launch_check("gemm_kernel");
 }
 
-int32_t nxg_linear_i8_rows(const nxg_weight * W, const int8_t * q, const float * sx, int32_t T,
-                           const float * residual, float * out, void * stream) {
-    return launch_gemm(W, q, sx, T, residual, out, nullptr, stream);
-}
-
-int32_t nxg_linear_i8(const nxg_weight * W, const int8_t * q, const float * sx,
-                      const int32_t * cu_offsets, int32_t n_seqs,
-                      const float * residual, float * out, void * stream) {
+// Rows of a packed batch: the total of cu_offsets, after checking it.
+static int32_t packed_rows(const int32_t * cu_offsets, int32_t n_seqs, int32_t & T) {
     if (!cu_offsets || n_seqs <= 0) return fail(NXG_EINVAL, "linear: need cu_offsets and n_seqs >= 1");
     if (cu_offsets[0] != 0) return fail(NXG_EINVAL, "linear: cu_offsets[0] = %d, expected 0", cu_offsets[0]);
     for (int i = 0; i < n_seqs; ++i) {
@@ -1000,12 +1294,49 @@ int32_t nxg_linear_i8(const nxg_weight * W, const int8_t * q, const float * sx,
                         cu_offsets[i], cu_offsets[i + 1]);
         }
     }
-    return launch_gemm(W, q, sx, cu_offsets[n_seqs], residual, out, nullptr, stream);
+    T = cu_offsets[n_seqs];
+    return NXG_OK;
+}
+
+int32_t nxg_linear_i8_rows(const nxg_weight * W, const int8_t * q, const float * sx, int32_t T,
+                           const float * residual, float * out, void * stream) {
+    gemm_out o;
+    o.residual = residual;
+    o.out = out;
+    return launch_gemm(W, q, sx, T, o, stream);
+}
+
+int32_t nxg_linear_i8(const nxg_weight * W, const int8_t * q, const float * sx,
+                      const int32_t * cu_offsets, int32_t n_seqs,
+                      const float * residual, float * out, void * stream) {
+    int32_t T = 0;
+    const int32_t rc = packed_rows(cu_offsets, n_seqs, T);
+    return rc ? rc : nxg_linear_i8_rows(W, q, sx, T, residual, out, stream);
+}
+
+int32_t nxg_linear_i8_relu2_q8_rows(const nxg_weight * W, const int8_t * q, const float * sx, int32_t T,
+                                    int32_t act_max, int8_t * q_out, float * sx_out, void * stream) {
+    gemm_out o;
+    o.qo = q_out;
+    o.sxo = sx_out;
+    o.act_max = act_max;
+    if (!q_out || !sx_out) return fail(NXG_EINVAL, "linear_relu2_q8: null output");
+    return launch_gemm(W, q, sx, T, o, stream);
+}
+
+int32_t nxg_linear_i8_relu2_q8(const nxg_weight * W, const int8_t * q, const float * sx,
+                               const int32_t * cu_offsets, int32_t n_seqs, int32_t act_max,
+                               int8_t * q_out, float * sx_out, void * stream) {
+    int32_t T = 0;
+    const int32_t rc = packed_rows(cu_offsets, n_seqs, T);
+    return rc ? rc : nxg_linear_i8_relu2_q8_rows(W, q, sx, T, act_max, q_out, sx_out, stream);
 }
 
 int32_t nxg_linear_i8_block_sums(const nxg_weight * W, const int8_t * q, int32_t T, int32_t * sums, void * stream) {
     if (!sums) return fail(NXG_EINVAL, "block_sums: null output");
-    return launch_gemm(W, q, nullptr, T, nullptr, nullptr, sums, stream);
+    gemm_out o;
+    o.sums = sums;
+    return launch_gemm(W, q, nullptr, T, o, stream);
 }
 
 } // extern "C"

@@ -107,6 +107,15 @@ def quantize_rows(x: np.ndarray, act_max: int = 127, simd: bool = False, n_threa
     return q, sx
 
 
+def relu2(x: np.ndarray) -> np.ndarray:
+    """op_relu_sqr (src/nexterabert.cpp:484-505): r = x > 0 ? x : 0 (MAXPS with zero as
+    the second operand, so a NaN gives 0), then r * r rounded to f32."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        r = np.where(x > np.float32(0), x, np.float32(0)).astype(np.float32)
+        return (r * r).astype(np.float32)
+
+
 def expand_rows(rows: np.ndarray, act_off: int = 128):
     """build_i8_weight on dequantized f32 rows (src/nexterabert.cpp:1030-1042)."""
     rows = np.ascontiguousarray(rows, dtype=np.float32)

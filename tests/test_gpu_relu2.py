@@ -1,0 +1,185 @@
+"""GPU parity at shapes with many tiles, and of the fused c_fc -> relu^2 -> int8 path.
+
+The fp32 GEMM is checked in full against the oracle at shapes of at least 256 tiles
+(persistent workgroups walking several tiles each: full, ragged and partial tiles, one
+and several 256-input blocks). The relu^2 output runs on 128 x 256 tiles; it is compared
+bit for bit with the CPU oracle (linear, then relu^2, then quantize_row) and, raw buffers
+with padding included, with the two-step GPU path (fp32 linear, then relu^2 quantize).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "no GPU"
+    return t
+
+
+@pytest.fixture(scope="module")
+def dev(torch, nxg):
+    nxg.init()
+    return torch.device("cuda:0")
+
+
+def make_weight(nxg, rng, n_in, n_out, std=0.02):
+    rows = (std * rng.standard_normal((n_out, n_in))).astype(np.float32)
+    return nxg.expand_weight(8, nxg.quantize_weight(8, rows), n_in, n_out)
+
+
+def quant(nxg, torch, orc, x):
+    qa = nxg.quantize_rows(torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda())
+    q_ref, sx_ref = orc.quantize_rows(x)
+    u8, _ = nxg.export_qact(qa)
+    assert (u8.cpu().numpy() == q_ref).all()
+    return qa, q_ref, sx_ref
+
+
+# (T, n_in, n_out): at least 256 tiles of 128 x 128
+LARGE_SHAPES = [(8192, 512, 1024),     # full tiles, 2 blocks
+               (8000, 256, 1152),     # last row tile half, last column tile half
+               (16384, 256, 512)]     # one block per tile (4 blocks: the relu^2 tests)
+
+
+@pytest.mark.parametrize("T,n_in,n_out", LARGE_SHAPES)
+def test_large_linear_matches_oracle(nxg, orc, torch, dev, T, n_in, n_out):
+    say(f"large linear T={T} n_in={n_in} n_out={n_out}")
+    rng = np.random.default_rng(T + n_in + n_out)
+    x = rng.standard_normal((T, n_in)).astype(np.float32)
+    res = rng.standard_normal((T, n_out)).astype(np.float32)
+    W = make_weight(nxg, rng, n_in, n_out)
+    qa, q_ref, sx_ref = quant(nxg, torch, orc, x)
+    dw = nxg.DeviceWeight(W)
+    y = nxg.linear_i8(dw, qa).cpu().numpy()
+    yr = nxg.linear_i8(dw, qa, residual=torch.from_numpy(res).cuda()).cpu().numpy()
+    y_ref = orc.linear(W.w, W.scale, W.off, q_ref, sx_ref, simd=bool(orc.vnni_flavour()),
+                       n_threads=orc.default_threads())
+    assert (bits(y) == bits(y_ref)).all()
+    # y = res + f (src/nexterabert.cpp:957-958): one f32 add on the oracle-checked f
+    assert (bits(yr) == bits(res + y_ref)).all()
+
+
+@pytest.mark.parametrize("act_max", [127, 63])
+def test_quantize_relu2_matches_oracle(nxg, orc, torch, dev, act_max):
+    say(f"quantize_relu2 act_max={act_max}")
+    rng = np.random.default_rng(21 + act_max)
+    T, n_in = 333, 2304 + 32
+    x = (rng.standard_normal((T, n_in)) * np.exp(rng.standard_normal((T, 1)) * 3)).astype(np.float32)
+    specials = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-30, -1e-30, 2e19, -3e38], np.float32)
+    for t in range(0, T, 3):
+        k = rng.integers(1, 5)
+        x[t, rng.integers(0, n_in, k)] = specials[rng.integers(0, len(specials), k)]
+    x[4] = -1.0                      # whole row non-positive: amax 0
+    qa = nxg.quantize_rows_relu2(torch.from_numpy(x).cuda(), act_max)
+    u8, sx = nxg.export_qact(qa)
+    q_ref, sx_ref = orc.quantize_rows(orc.relu2(x), act_max)
+    assert (u8.cpu().numpy() == q_ref).all()
+    assert (bits(sx.cpu().numpy()) == bits(sx_ref)).all()
+
+
+# (T, n_in, n_out) for c_fc -> relu^2 -> int8; n_out % 32 == 0, n_in % 256 == 0
+RELU2_SHAPES = [(4096, 1024, 2304),   # the MLP's c_fc, 4 blocks, 9 column tiles
+                (777, 512, 320),      # ragged rows, a 64-column last tile, KSo = 5
+                (33, 256, 96),        # one row tile, n_out % 64 = 32
+                (1, 1024, 256)]
+
+
+@pytest.mark.parametrize("T,n_in,n_out", RELU2_SHAPES)
+def test_linear_relu2_q8(nxg, orc, torch, dev, T, n_in, n_out):
+    rng = np.random.default_rng(T * 3 + n_in + n_out)
+    x = rng.standard_normal((T, n_in)).astype(np.float32)
+    W = make_weight(nxg, rng, n_in, n_out, std=0.05)
+    qa, q_ref, sx_ref = quant(nxg, torch, orc, x)
+    dw = nxg.DeviceWeight(W)
+    # the oracle: linear, relu^2, quantize_row
+    y_ref = orc.linear(W.w, W.scale, W.off, q_ref, sx_ref, simd=bool(orc.vnni_flavour()),
+                       n_threads=orc.default_threads())
+    for act_max in (127, 63):
+        say(f"linear_relu2_q8 T={T} n_in={n_in} n_out={n_out} act_max={act_max}")
+        fused = nxg.linear_i8_relu2_q8(dw, qa, act_max)
+        # two steps on the GPU: fp32 rows, then relu^2 + quantize
+        two = nxg.quantize_rows_relu2(nxg.linear_i8(dw, qa), act_max)
+        torch.cuda.synchronize()
+        assert torch.equal(fused.q, two.q), "activation tiles (padding included) differ from the two-step path"
+        assert torch.equal(fused.sx.view(torch.int32), two.sx.view(torch.int32)), "scales differ from the two-step path"
+        r_ref, rsx_ref = orc.quantize_rows(orc.relu2(y_ref), act_max)
+        u8, sx = nxg.export_qact(fused)
+        assert (u8.cpu().numpy() == r_ref).all()
+        assert (bits(sx.cpu().numpy()) == bits(rsx_ref)).all()
+
+
+def test_linear_relu2_q8_packed_batch(nxg, orc, torch, dev):
+    say("linear_relu2_q8 with cu_offsets")
+    rng = np.random.default_rng(8)
+    lengths = [300, 17, 1000, 129]
+    cu = nxg.cu_offsets_of(lengths)
+    T, n_in, n_out = int(cu[-1]), 1024, 512
+    x = rng.standard_normal((T, n_in)).astype(np.float32)
+    W = make_weight(nxg, rng, n_in, n_out)
+    qa, _, _ = quant(nxg, torch, orc, x)
+    dw = nxg.DeviceWeight(W)
+    a = nxg.linear_i8_relu2_q8(dw, qa, cu_offsets=cu)
+    b = nxg.linear_i8_relu2_q8(dw, qa)
+    torch.cuda.synchronize()
+    assert torch.equal(a.q, b.q) and torch.equal(a.sx.view(torch.int32), b.sx.view(torch.int32))
+    # each sequence alone gives the same rows
+    s0, s1 = int(cu[2]), int(cu[3])
+    qs, _, _ = quant(nxg, torch, orc, x[s0:s1])
+    c = nxg.linear_i8_relu2_q8(dw, qs)
+    uc, sc = nxg.export_qact(c)
+    ua, sa = nxg.export_qact(a)
+    torch.cuda.synchronize()
+    assert torch.equal(uc, ua[s0:s1])
+    n_blk = (n_out + 255) // 256
+    sa_m = orc.sx_matrix(sa.cpu().numpy(), T, n_out)
+    sc_m = orc.sx_matrix(sc.cpu().numpy(), s1 - s0, n_out)
+    assert (bits(sa_m[s0:s1]) == bits(sc_m)).all() and sa_m.shape[1] == n_blk
+
+
+@pytest.mark.parametrize("n_in_fc", [1024, 96])
+def test_builder_mlp(nxg, orc, torch, dev, n_in_fc):
+    """x + c_proj(relu(c_fc(h))^2): fused when n_in % 256 == 0, fp32 then quantize otherwise."""
+    say(f"builder mlp n_in={n_in_fc}")
+    rng = np.random.default_rng(n_in_fc)
+    T, n_hidden = 400, 2304
+    h = rng.standard_normal((T, n_in_fc)).astype(np.float32)
+    x = rng.standard_normal((T, n_in_fc)).astype(np.float32)
+    W_fc = make_weight(nxg, rng, n_in_fc, n_hidden)
+    W_proj = make_weight(nxg, rng, n_hidden, n_in_fc)
+    b = nxg.Builder({"fc": nxg.DeviceWeight(W_fc), "proj": nxg.DeviceWeight(W_proj)})
+    y = b.mlp("fc", "proj", torch.from_numpy(h).cuda(), torch.from_numpy(x).cuda()).cpu().numpy()
+    qh, sh = orc.quantize_rows(h)
+    simd = bool(orc.vnni_flavour())
+    u = orc.linear(W_fc.w, W_fc.scale, W_fc.off, qh, sh, simd=simd, n_threads=orc.default_threads())
+    qr, sr = orc.quantize_rows(orc.relu2(u))
+    y_ref = orc.linear(W_proj.w, W_proj.scale, W_proj.off, qr, sr, res=x, simd=simd, n_threads=orc.default_threads())
+    assert (bits(y) == bits(y_ref)).all()
+
+
+def test_relu2_q8_bad_shapes_raise(nxg, torch, dev):
+    rng = np.random.default_rng(0)
+    x = torch.randn(64, 96, device="cuda")
+    qa = nxg.quantize_rows(x)
+    dw = nxg.DeviceWeight(make_weight(nxg, rng, 96, 64))      # n_in % 256 != 0
+    with pytest.raises(ValueError, match="n_in % 256"):
+        nxg.linear_i8_relu2_q8(dw, qa)
+    x2 = torch.randn(64, 256, device="cuda")
+    dw2 = nxg.DeviceWeight(make_weight(nxg, rng, 256, 100))   # n_out % 32 != 0
+    # the wrapper refuses to size such an output; the C entry point refuses the shape
+    with pytest.raises(ValueError, match="multiple of 32"):
+        nxg.linear_i8_relu2_q8(dw2, nxg.quantize_rows(x2))
+    with pytest.raises(ValueError, match="n_out % 32"):
+        nxg.linear_i8_relu2_q8(dw2, nxg.quantize_rows(x2), out=nxg.qact_alloc(64, 128))

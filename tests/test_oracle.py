@@ -166,6 +166,33 @@ def test_quantize_subnormal_row_maps_to_zero(orc):
     assert sx[0] == np.float32(np.float32(1e-41) / np.float32(127))
 
 
+# --- op_relu_sqr ----------------------------------------------------------------
+
+def test_relu2_closed_form(orc):
+    # MAXPS(x, 0) returns the second operand for NaN and for -0 (not greater): both 0.
+    x = np.array([np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0, -1.0, -1e-40, 1e-40, 1e-20, 3e38,
+                  1.5, 2.0 ** 64], np.float32)
+    y = orc.relu2(x)
+    zero = [0, 1, 3, 4, 5, 6, 7, 8]              # NaN, -inf, +-0, negatives, 1e-40^2 underflow
+    assert (bits(y[zero]) == 0).all()            # all +0
+    assert y[2] == np.inf and y[10] == np.inf and y[12] == np.inf   # inf, 3e38^2, 2^128
+    assert y[11] == np.float32(2.25)
+    # 1e-20^2 = 1e-40 is an f32 subnormal: RNE of the exact square
+    assert y[9] == np.float32(np.float64(np.float32(1e-20)) ** 2) and y[9] > 0
+
+
+def test_relu2_is_the_exact_square_rounded_once(orc):
+    # the product of two f32 is exact in f64 (48 significant bits), so f32(f64(r)^2)
+    # is the single RNE rounding of r*r; subnormal and overflow ranges included
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal(20000) * 10.0 ** rng.integers(-25, 22, 20000)).astype(np.float32)
+    y = orc.relu2(x)
+    r = np.where(x > 0, x, 0).astype(np.float64)
+    with np.errstate(over="ignore"):
+        want = (r * r).astype(np.float32)
+    assert (bits(y) == bits(want)).all()
+
+
 # --- build_i8_weight ----------------------------------------------------------
 
 @pytest.mark.parametrize("n_in", [64, 256 + 32, 1024])
