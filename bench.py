@@ -47,7 +47,7 @@ def log(msg: str) -> None:
 class LinearPath:
     """Every int8 projection of the encoder over M packed rows, on device buffers."""
 
-    def __init__(self, nxg, M: int, fuse: bool = True, weights=None, seed: int = 0):
+    def __init__(self, nxg, M: int, fuse: bool = True, weights=None, seed: int = 0, fuse_mlp: bool = True):
         import torch
         import nexterabert_cpp_amd.model as model
         self.nxg, self.torch, self.M = nxg, torch, M
@@ -60,20 +60,33 @@ class LinearPath:
         rows_block = (M + model.HRA_BLOCK - 1) // model.HRA_BLOCK
         self.residual = torch.randn(M, model.N_EMBD, device="cuda", generator=gen)
         self.ops = 0
-        self.gemm_bytes = 0
+        self.gemm_bytes = 0       # fp32-output GEMMs
+        self.relu2_bytes = 0      # c_fc -> relu^2 -> int8 GEMMs
         self.quant_bytes = 0
+        self.ops_fp32 = self.ops_relu2 = 0
         for l, kind in enumerate(model.BLOCK_TYPES):
             steps = []
             seen = set()
+            made = set()          # qact keys produced by a GEMM of this layer (relu^2 -> int8)
             for g in model.layer_groups(l, kind, fuse):
                 rows = rows_block if g.block_rows else M
                 key = (g.input, g.n_in, rows)
-                if key not in self.inputs:
-                    self.inputs[key] = torch.randn(rows, g.n_in, device="cuda", generator=gen)
+                if key not in self.qacts:
                     self.qacts[key] = nxg.qact_alloc(rows, g.n_in)
+                if key not in made and key not in self.inputs:
+                    self.inputs[key] = torch.randn(rows, g.n_in, device="cuda", generator=gen)
                 okey = (g.n_out, rows)
                 if okey not in self.outs:
                     self.outs[okey] = torch.empty(rows, g.n_out, device="cuda")
+                gkind = "fp32"
+                if g.relu2_into:
+                    # c_fc: its output only feeds relu^2 into the next linear's qact
+                    gkind = "relu2" if fuse_mlp else "relu2_unfused"
+                    rkey = (g.relu2_into, g.n_out, rows)
+                    if rkey not in self.qacts:
+                        self.qacts[rkey] = nxg.qact_alloc(rows, g.n_out)
+                    made.add(rkey)
+                    okey = rkey if fuse_mlp else okey
                 wname = g.name if len(g.specs) == 1 else f"blocks.{l}.{g.name}"
                 if wname not in self.dev_weights:
                     parts = []
@@ -86,43 +99,58 @@ class LinearPath:
                                      np.ascontiguousarray(np.concatenate([p.off for p in parts], 1)))
                     self.host_weights[wname] = W
                     self.dev_weights[wname] = nxg.DeviceWeight(W)
-                first = key not in seen
+                first = key not in seen and key not in made
                 seen.add(key)
                 res = g.residual
-                steps.append((key, first, wname, okey, res, g))
-                self.ops += 2 * rows * g.n_in * g.n_out
+                steps.append((key, first, wname, okey, res, g, gkind))
+                ops = 2 * rows * g.n_in * g.n_out
+                self.ops += ops
                 nb = (g.n_in + 255) // 256
-                self.gemm_bytes += (rows * g.n_in + 4 * rows * nb + g.n_out * g.n_in + 4 * g.n_out * nb
-                                    + 4 * rows * g.n_out * (2 if res else 1))
+                nb_out = (g.n_out + 255) // 256
+                w_in = rows * g.n_in + 4 * rows * nb + g.n_out * g.n_in + 4 * g.n_out * nb
+                if gkind == "relu2":
+                    self.ops_relu2 += ops
+                    self.relu2_bytes += w_in + rows * g.n_out + 4 * rows * nb_out
+                else:
+                    self.ops_fp32 += ops
+                    self.gemm_bytes += w_in + 4 * rows * g.n_out * (2 if res else 1)
+                if gkind == "relu2_unfused":      # fp32 rows, then relu^2 + quantize_row
+                    self.quant_bytes += 5 * rows * g.n_out + 4 * rows * nb_out
                 if first:
                     self.quant_bytes += 5 * rows * g.n_in + 4 * rows * nb
             self.layers.append(steps)
         self.n_gemm = sum(len(s) for s in self.layers)
-        self.n_quant = sum(1 for s in self.layers for st in s if st[1])
+        self.n_relu2 = sum(1 for s in self.layers for st in s if st[6] == "relu2")
+        self.n_quant = sum(1 for s in self.layers for st in s if st[1] or st[6] == "relu2_unfused")
+
+    def _timed(self, events, fn, *tag):
+        if events is None:
+            fn()
+            return
+        torch = self.torch
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        events.append((e0, e1) + tag)
 
     def step(self, gemm_events=None, quant_events=None):
-        nxg, torch = self.nxg, self.torch
+        nxg = self.nxg
         for steps in self.layers:
-            for key, first, wname, okey, res, g in steps:
+            for key, first, wname, okey, res, g, gkind in steps:
                 qa = self.qacts[key]
+                w = self.dev_weights[wname]
                 if first:
-                    if quant_events is not None:
-                        e0 = torch.cuda.Event(enable_timing=True)
-                        e0.record()
-                    nxg.quantize_rows(self.inputs[key], out=qa)
-                    if quant_events is not None:
-                        e1 = torch.cuda.Event(enable_timing=True)
-                        e1.record()
-                        quant_events.append((e0, e1))
-                if gemm_events is not None:
-                    e0 = torch.cuda.Event(enable_timing=True)
-                    e0.record()
-                nxg.linear_i8(self.dev_weights[wname], qa, residual=self.residual if res else None,
-                              out=self.outs[okey])
-                if gemm_events is not None:
-                    e1 = torch.cuda.Event(enable_timing=True)
-                    e1.record()
-                    gemm_events.append((e0, e1, g))
+                    self._timed(quant_events, lambda: nxg.quantize_rows(self.inputs[key], out=qa))
+                if gkind == "relu2":
+                    self._timed(gemm_events, lambda: nxg.linear_i8_relu2_q8(w, qa, out=self.qacts[okey]), g, gkind)
+                    continue
+                self._timed(gemm_events, lambda: nxg.linear_i8(w, qa, residual=self.residual if res else None,
+                                                               out=self.outs[okey]), g, gkind)
+                if gkind == "relu2_unfused":
+                    rkey = (g.relu2_into, g.n_out, qa.T)
+                    self._timed(quant_events, lambda: nxg.quantize_rows_relu2(self.outs[okey], out=self.qacts[rkey]))
 
 
 def time_steps(path, steps: int, warmup: int):
@@ -141,9 +169,12 @@ def time_steps(path, steps: int, warmup: int):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     total_ms = s0.elapsed_time(s1)
-    gemm_ms = sum(a.elapsed_time(b) for a, b, _ in gemm_ev)
+    gemm_ms = {}
+    for a, b, g, kind in gemm_ev:
+        k = "relu2" if kind == "relu2" else "fp32"
+        gemm_ms[k] = gemm_ms.get(k, 0.0) + a.elapsed_time(b) / steps
     quant_ms = sum(a.elapsed_time(b) for a, b in quant_ev)
-    return total_ms / steps, wall / steps * 1e3, gemm_ms / steps, quant_ms / steps, gemm_ev
+    return total_ms / steps, wall / steps * 1e3, gemm_ms, quant_ms / steps, gemm_ev
 
 
 def time_graph(path, steps: int, warmup: int):
@@ -152,6 +183,7 @@ def time_graph(path, steps: int, warmup: int):
     path.step()
     torch.cuda.synchronize()
     eager = {k: v.clone() for k, v in path.outs.items()}
+    eager_q = {k: (v.q.clone(), v.sx.view(torch.int32).clone()) for k, v in path.qacts.items()}
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -161,12 +193,18 @@ def time_graph(path, steps: int, warmup: int):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         path.step()
-    for _ in range(max(1, warmup)):
+    # every replay against the eager result, with eager work between the replays
+    for i in range(max(3, warmup)):
         g.replay()
-    torch.cuda.synchronize()
-    for k, v in path.outs.items():
-        if not torch.equal(v.view(torch.int32), eager[k].view(torch.int32)):
-            raise RuntimeError("graph replay differs from eager execution")
+        torch.cuda.synchronize()
+        for k, v in path.outs.items():
+            if not torch.equal(v.view(torch.int32), eager[k].view(torch.int32)):
+                raise RuntimeError(f"graph replay {i} differs from eager execution (fp32 rows {k})")
+        for k, v in path.qacts.items():
+            if not (torch.equal(v.q, eager_q[k][0]) and torch.equal(v.sx.view(torch.int32), eager_q[k][1])):
+                raise RuntimeError(f"graph replay {i} differs from eager execution (activations {k})")
+        path.step()
+        torch.cuda.synchronize()
     s0 = torch.cuda.Event(enable_timing=True)
     s1 = torch.cuda.Event(enable_timing=True)
     s0.record()
@@ -195,10 +233,10 @@ def cpu_baseline(path, rows: int, reps: int):
     rb = (rows + 3) // 4
     xs = {}
     for steps in path.layers:
-        for key, first, wname, okey, res, g in steps:
+        for key, first, wname, okey, res, g, gkind in steps:
             r = rb if g.block_rows else rows
             k = (key[0], key[1], r)
-            if k not in xs:
+            if first and k not in xs:
                 xs[k] = rng.standard_normal((r, key[1])).astype(np.float32)
     resid = rng.standard_normal((rows, model.N_EMBD)).astype(np.float32)
     ops = 0
@@ -208,14 +246,16 @@ def cpu_baseline(path, rows: int, reps: int):
         ops = 0
         for steps in path.layers:
             q = {}
-            for key, first, wname, okey, res, g in steps:
+            for key, first, wname, okey, res, g, gkind in steps:
                 r = rb if g.block_rows else rows
                 k = (key[0], key[1], r)
                 if k not in q:
                     q[k] = orc.quantize_rows(xs[k], simd=True, n_threads=n_threads)
                 W = path.host_weights[wname]
-                orc.linear(W.w, W.scale, W.off, q[k][0], q[k][1], res=resid if res else None,
-                           simd=True, n_threads=n_threads)
+                y = orc.linear(W.w, W.scale, W.off, q[k][0], q[k][1], res=resid if res else None,
+                               simd=True, n_threads=n_threads)
+                if g.relu2_into:      # op_relu_sqr quantized for the next linear
+                    q[(g.relu2_into, g.n_out, r)] = orc.quantize_rows(orc.relu2(y), simd=True, n_threads=n_threads)
                 ops += 2 * r * g.n_in * g.n_out
 
     one_pass()
@@ -230,7 +270,8 @@ def cpu_baseline(path, rows: int, reps: int):
         "unit": "TOPS",
         "cores": n_threads,
         "kind": "port",
-        "sample": (f"all 140 encoder int8 linears as 92 GEMMs + activation quantization at {rows} rows "
+        "sample": (f"all 140 encoder int8 linears as 92 GEMMs + activation quantization (relu^2 between "
+                   f"c_fc and c_proj) at {rows} rows "
                    f"(HRA q/k/v at {rb}), CPU oracle on {orc.vnni_flavour()}, median of {reps} passes "
                    f"after 1 warm-up, {med:.2f} s per pass"),
         "tokens_per_s": round(rows / med, 1),
@@ -248,13 +289,15 @@ def pmc_summary(fetch_csv: str, write_csv: str, calib_mib: int, out_path: Path) 
     import csv
 
     def per_kernel(path, counter):
-        vals = {"gemm": [], "quant": [], "copy": []}
+        vals = {"gemm_fp32": [], "gemm_relu2": [], "quant": [], "copy": []}
         for row in csv.DictReader(open(path)):
             if row["Counter_Name"] != counter:
                 continue
             name, v = row["Kernel_Name"], float(row["Counter_Value"])
-            if "gemm_kernel" in name:
-                vals["gemm"].append(v)
+            if "gemm_relu2_q8" in name:
+                vals["gemm_relu2"].append(v)
+            elif "gemm_k256" in name or "gemm_kernel" in name:
+                vals["gemm_fp32"].append(v)
             elif "quantize_kernel" in name:
                 vals["quant"].append(v)
             elif "copy" in name.lower():
@@ -268,7 +311,9 @@ def pmc_summary(fetch_csv: str, write_csv: str, calib_mib: int, out_path: Path) 
     fs, ws = kib / f["copy"], kib / w["copy"]
     res = {"fetch_scale": round(fs, 4), "write_scale": round(ws, 4),
            "calibration": f"plain device copy of {calib_mib} MiB (reads and writes {calib_mib} MiB)"}
-    for k in ("gemm", "quant"):
+    for k in ("gemm_fp32", "gemm_relu2", "quant"):
+        if f[k] is None or w[k] is None:
+            continue
         res[k] = {"fetch_bytes_per_launch": int(f[k] * fs * 1024), "write_bytes_per_launch": int(w[k] * ws * 1024),
                   "hbm_bytes_per_launch": int((f[k] * fs + w[k] * ws) * 1024),
                   "raw_fetch_kib": round(f[k], 1), "raw_write_kib": round(w[k], 1)}
@@ -283,6 +328,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--rows", type=int, default=65536, help="packed rows M of the timed workload")
     ap.add_argument("--no-fuse", action="store_true", help="one GEMM per linear (140) instead of 92")
+    ap.add_argument("--no-fuse-mlp", action="store_true",
+                    help="c_fc writes fp32 rows, then relu^2 + quantize (instead of the int8 epilogue)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=2048)
     ap.add_argument("--cpu-reps", type=int, default=3)
@@ -317,43 +364,58 @@ def main() -> int:
         del a, b
 
     t0 = time.perf_counter()
-    path = LinearPath(nxg, args.rows, fuse=not args.no_fuse)
+    path = LinearPath(nxg, args.rows, fuse=not args.no_fuse, fuse_mlp=not args.no_fuse_mlp)
     torch.cuda.synchronize()
-    log(f"setup {time.perf_counter() - t0:.1f} s: M={args.rows}, {path.n_gemm} GEMMs + {path.n_quant} "
-        f"quantizations per step, {path.ops / 1e12:.3f} T int8 ops")
+    log(f"setup {time.perf_counter() - t0:.1f} s: M={args.rows}, {path.n_gemm} GEMMs ({path.n_relu2} with the "
+        f"relu^2 -> int8 output) + {path.n_quant} quantizations per step, {path.ops / 1e12:.3f} T int8 ops")
 
     ms, wall_ms, gemm_ms, quant_ms, gemm_ev = time_steps(path, args.steps, args.warmup)
-    log(f"timed {args.steps} steps: {ms:.3f} ms/step (wall {wall_ms:.3f}), GEMMs {gemm_ms:.3f} ms, "
-        f"quantize {quant_ms:.3f} ms")
+    gemm_total = sum(gemm_ms.values())
+    log(f"timed {args.steps} steps: {ms:.3f} ms/step (wall {wall_ms:.3f}), GEMMs {gemm_total:.3f} ms "
+        f"({gemm_ms}), quantize {quant_ms:.3f} ms")
 
     value = path.ops / (ms * 1e-3) / 1e12
-    gemm_tops = path.ops / (gemm_ms * 1e-3) / 1e12
-    n_launch = path.n_gemm
-    avg_launch_s = gemm_ms * 1e-3 / n_launch
-    ops_per_launch = path.ops / n_launch
-    bytes_per_launch = path.gemm_bytes / n_launch
-    ai = path.ops / path.gemm_bytes
+    gemm_tops = path.ops / (gemm_total * 1e-3) / 1e12
     ridge = PEAK_INT8_TOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
-    if ai >= ridge:
-        roof = {"bound": "mfma", "achieved": round(ops_per_launch / avg_launch_s / 1e12, 2),
-                "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s"}
-    else:
-        roof = {"bound": "hbm", "achieved": round(bytes_per_launch / avg_launch_s / 1e9, 1),
-                "peak": PEAK_HBM_GBS, "unit": "GB/s"}
-    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    roof["traffic"] = None
+
+    def roofline(n_launch, ops, nbytes, ms_step, kernel):
+        avg_launch_s = ms_step * 1e-3 / n_launch
+        ops_pl, bytes_pl, ai = ops / n_launch, nbytes / n_launch, ops / nbytes
+        if ai >= ridge:
+            r = {"bound": "mfma", "achieved": round(ops_pl / avg_launch_s / 1e12, 2),
+                 "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s"}
+        else:
+            r = {"bound": "hbm", "achieved": round(bytes_pl / avg_launch_s / 1e9, 1),
+                 "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+        r["frac"] = round(r["achieved"] / r["peak"], 4)
+        r["traffic"] = None
+        r["kernel"] = kernel
+        r["per_launch"] = {"algorithmic_ops": int(ops_pl), "algorithmic_bytes": int(bytes_pl),
+                           "avg_us": round(avg_launch_s * 1e6, 2), "arith_intensity": round(ai, 1),
+                           "int8_tops": round(ops_pl / avg_launch_s / 1e12, 2)}
+        return r
+
+    # The dominant kernel: the fp32-output GEMM (most launches and most of the time).
+    n_fp32 = path.n_gemm - path.n_relu2
+    roof = roofline(n_fp32, path.ops_fp32, path.gemm_bytes, gemm_ms["fp32"], "gemm_k256 (nxg_linear_i8)")
     if TRAFFIC_FILE.exists() and args.rows == 65536 and not args.no_fuse:
         tr = json.loads(TRAFFIC_FILE.read_text())
-        roof["traffic"] = tr["gemm"]["hbm_bytes_per_launch"]
-        roof["traffic_source"] = (f"{TRAFFIC_FILE.relative_to(ROOT)}: rocprofv3 FETCH_SIZE x {tr['fetch_scale']} + "
-                                  f"WRITE_SIZE x {tr['write_scale']} per GEMM launch of this workload")
-    roof["kernel"] = "gemm_kernel (nxg_linear_i8)"
-    roof["per_launch"] = {"algorithmic_ops": int(ops_per_launch), "algorithmic_bytes": int(bytes_per_launch),
-                          "avg_us": round(avg_launch_s * 1e6, 2), "arith_intensity": round(ai, 1)}
+        if "gemm_fp32" in tr:
+            roof["traffic"] = tr["gemm_fp32"]["hbm_bytes_per_launch"]
+            roof["traffic_source"] = (f"{TRAFFIC_FILE.relative_to(ROOT)}: rocprofv3 FETCH_SIZE x {tr['fetch_scale']}"
+                                      f" + WRITE_SIZE x {tr['write_scale']} per fp32-output GEMM launch of this workload")
+    roof_relu2 = None
+    if path.n_relu2:
+        roof_relu2 = roofline(path.n_relu2, path.ops_relu2, path.relu2_bytes, gemm_ms["relu2"],
+                              "gemm_relu2_q8 (nxg_linear_i8_relu2_q8)")
+        if TRAFFIC_FILE.exists() and args.rows == 65536 and not args.no_fuse:
+            tr = json.loads(TRAFFIC_FILE.read_text())
+            if "gemm_relu2" in tr:
+                roof_relu2["traffic"] = tr["gemm_relu2"]["hbm_bytes_per_launch"]
 
     enc = None
     if not args.no_encoder1024:
-        p1k = LinearPath(nxg, 1024, fuse=not args.no_fuse, weights=path.dev_weights)
+        p1k = LinearPath(nxg, 1024, fuse=not args.no_fuse, weights=path.dev_weights, fuse_mlp=not args.no_fuse_mlp)
         p1k.host_weights = path.host_weights
         ms1k = time_graph(p1k, max(args.steps, 20), args.warmup)
         enc = {"tokens_per_s": round(1024 / (ms1k * 1e-3), 1), "ms_per_step": round(ms1k, 4),
@@ -383,16 +445,19 @@ def main() -> int:
         "data": "synthetic (N(0,1) activations, N(0,0.02) weights -> Q8_0 -> int8)",
         "config": {"workload": f"all 140 encoder int8 projections, one {args.rows}-token sequence",
                    "rows": args.rows, "gemm_launches": path.n_gemm, "quantize_launches": path.n_quant,
-                   "fused_shared_inputs": not args.no_fuse, "weights": "Q8_0 expanded to int8",
+                   "fused_shared_inputs": not args.no_fuse,
+                   "mlp_relu2_int8_epilogue": path.n_relu2 > 0, "weights": "Q8_0 expanded to int8",
                    "parallelism": "single GPU"},
         "pct_of_mfma_peak": round(100 * value / PEAK_INT8_TOPS, 2),
         "tokens_per_s": round(args.rows / (ms * 1e-3), 1),
         "gemm_only": {"int8_tops": round(gemm_tops, 2), "pct_of_mfma_peak": round(100 * gemm_tops / PEAK_INT8_TOPS, 2),
-                      "ms_per_step": round(gemm_ms, 4)},
+                      "ms_per_step": round(gemm_total, 4),
+                      "ms_per_step_by_output": {k: round(v, 4) for k, v in gemm_ms.items()}},
         "quantize": {"ms_per_step": round(quant_ms, 4),
-                     "gb_per_s": round(path.quant_bytes / (quant_ms * 1e-3) / 1e9, 1)},
+                     "gb_per_s": round(path.quant_bytes / (quant_ms * 1e-3) / 1e9, 1) if quant_ms else None},
         "encoder_1024": enc,
         "roofline": roof,
+        "roofline_relu2_q8": roof_relu2,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

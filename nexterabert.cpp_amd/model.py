@@ -34,6 +34,7 @@ class LinearSpec:
     input: str           # which activation of the layer it reads (linears that share one share its qact)
     residual: bool = False     # + residual stream (c_proj of the mixer and of the MLP)
     block_rows: bool = False   # HRA q/k/v: run on ceil(len/4) block rows per sequence
+    relu2_into: str = ""       # the output only feeds relu^2 into this input (the MLP's c_fc)
 
 
 @dataclass
@@ -58,6 +59,10 @@ class LinearGroup:
     @property
     def block_rows(self) -> bool:
         return self.specs[0].block_rows
+
+    @property
+    def relu2_into(self) -> str:
+        return self.specs[0].relu2_into if len(self.specs) == 1 else ""
 
     @property
     def name(self) -> str:
@@ -99,7 +104,7 @@ def layer_linears(l: int, kind: str) -> List[LinearSpec]:
     else:
         raise ValueError(kind)
     # MLP :1284-1289
-    out += [LinearSpec(blk + "mlp.c_fc.weight", C, N_INTER, "mlp_in"),
+    out += [LinearSpec(blk + "mlp.c_fc.weight", C, N_INTER, "mlp_in", relu2_into="relu_out"),
             LinearSpec(blk + "mlp.c_proj.weight", N_INTER, C, "relu_out", residual=True)]
     return out
 
