@@ -103,7 +103,7 @@ __device__ __forceinline__ int quant1(float x, float inv) {
     return u - (ACT_MAX + 1);
 }
 
-// One workgroup per (16-row group, 256-input block). Wave w quantizes rows
+// One workgroup per (16-row group, 256-input block), the block index fastest. Wave w quantizes rows
 // 4w..4w+3; the 16 lanes of a row read its 256 inputs as 4 contiguous 256-byte
 // pieces, so lane c holds inputs 64i + 4c + e (i, e = 0..3). The int8 results are
 // gathered in LDS in fragment order and each wave stores one 1 KiB fragment.
@@ -114,7 +114,8 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict_
                                                        int n_blk, int8_t * __restrict__ q, float * __restrict__ sx) {
     __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
 
-    const int g = blockIdx.x, B = blockIdx.y;
+    // block index fastest: consecutive workgroups read consecutive 1 KiB pieces of the same rows
+    const int g = (int) (blockIdx.x / (unsigned) n_blk), B = (int) (blockIdx.x % (unsigned) n_blk);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rl = wave * 4 + (lane >> 4);     // row within the 16-row group
     const int t = g * 16 + rl;
@@ -1112,7 +1113,9 @@ static int32_t launch_quantize(const float * x, int32_t T, int32_t n_in, int32_t
     if (!x || !q || !sx) return fail(NXG_EINVAL, "quantize: null buffer");
     int rc = check_device();
     if (rc) return rc;
-    const dim3 grid(d.MP / 16, d.n_blk);
+    const long long n_wg = (long long) (d.MP / 16) * d.n_blk;
+    if (n_wg > INT32_MAX) return fail(NXG_EINVAL, "quantize: T=%d n_in=%d too large", T, n_in);
+    const dim3 grid((unsigned) n_wg);
     hipStream_t s = (hipStream_t) stream;
     if (act_max == 127) {
         if (relu2) quantize_kernel<127, true><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
