@@ -20,7 +20,7 @@ import ctypes
 import os
 from dataclasses import dataclass
 from pathlib import Path
-from typing import Dict, Optional, Sequence
+from typing import Dict, List, Optional, Sequence
 
 import numpy as np
 
@@ -33,6 +33,10 @@ TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_1 = 0, 1, 2, 3
 TYPE_Q5_0, TYPE_Q5_1, TYPE_Q8_0 = 6, 7, 8
 TYPE_Q2_K, TYPE_Q3_K, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 10, 11, 12, 13, 14
 TYPE_BF16 = 30
+
+# GGUF metadata value types, include/nxg_gguf.h
+(GGUF_UINT8, GGUF_INT8, GGUF_UINT16, GGUF_INT16, GGUF_UINT32, GGUF_INT32, GGUF_FLOAT32, GGUF_BOOL,
+ GGUF_STRING, GGUF_ARRAY, GGUF_UINT64, GGUF_INT64, GGUF_FLOAT64) = range(13)
 
 NXG_OK, NXG_EINVAL, NXG_ENOMEM, NXG_EDEVICE = 0, 1, 2, 3
 
@@ -77,6 +81,30 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_linear_i8_block_sums": ([P, P, i32, P, P], i32),
         "nxg_linear_i8_relu2_q8": ([P, P, P, P, i32, i32, P, P, P], i32),
         "nxg_linear_i8_relu2_q8_rows": ([P, P, P, i32, i32, P, P, P], i32),
+        # include/nxg_gguf.h
+        "nxg_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(P)], i32),
+        "nxg_gguf_close": ([P], None),
+        "nxg_gguf_version": ([P], ctypes.c_uint32),
+        "nxg_gguf_data_offset": ([P], ctypes.c_uint64),
+        "nxg_gguf_alignment": ([P], ctypes.c_uint32),
+        "nxg_gguf_n_kv": ([P], i64),
+        "nxg_gguf_find_key": ([P, ctypes.c_char_p], i64),
+        "nxg_gguf_key": ([P, i64], ctypes.c_char_p),
+        "nxg_gguf_kv_type": ([P, i64], i32),
+        "nxg_gguf_get_i64": ([P, i64, ctypes.POINTER(i64)], i32),
+        "nxg_gguf_get_f64": ([P, i64, ctypes.POINTER(ctypes.c_double)], i32),
+        "nxg_gguf_get_str": ([P, i64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_uint64)], i32),
+        "nxg_gguf_arr_info": ([P, i64, ctypes.POINTER(i32), ctypes.POINTER(ctypes.c_uint64)], i32),
+        "nxg_gguf_arr_i64": ([P, i64, ctypes.c_uint64, ctypes.POINTER(i64)], i32),
+        "nxg_gguf_arr_f64": ([P, i64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_double)], i32),
+        "nxg_gguf_arr_str": ([P, i64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_uint64)], i32),
+        "nxg_gguf_n_tensors": ([P], i64),
+        "nxg_gguf_find_tensor": ([P, ctypes.c_char_p], i64),
+        "nxg_gguf_tensor_name": ([P, i64], ctypes.c_char_p),
+        "nxg_gguf_tensor_info": ([P, i64, ctypes.POINTER(i32), ctypes.POINTER(i32), ctypes.POINTER(i64),
+                                  ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], i32),
+        "nxg_gguf_tensor_data": ([P, i64], P),
+        "nxg_gguf_weight_create": ([P, i64, i32, ctypes.POINTER(P)], i32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(L, name)
@@ -186,17 +214,18 @@ def init() -> None:
 class DeviceWeight:
     """An I8Weight uploaded once into MFMA fragment tiles (nxg_weight)."""
 
-    def __init__(self, weight: I8Weight):
+    def __init__(self, weight: Optional[I8Weight], handle: Optional[ctypes.c_void_p] = None):
         L = load_library()
-        w = np.ascontiguousarray(weight.w)
-        s = np.ascontiguousarray(weight.scale)
-        h = ctypes.c_void_p()
-        _check(L.nxg_weight_create(_np_ptr(w), _np_ptr(s), w.shape[1], w.shape[0], ctypes.byref(h)),
-               "weight_create")
-        self._h = h
-        self.n_in, self.n_out = w.shape[1], w.shape[0]
+        if handle is None:
+            w = np.ascontiguousarray(weight.w)
+            s = np.ascontiguousarray(weight.scale)
+            handle = ctypes.c_void_p()
+            _check(L.nxg_weight_create(_np_ptr(w), _np_ptr(s), w.shape[1], w.shape[0], ctypes.byref(handle)),
+                   "weight_create")
+        self._h = handle
+        self.n_in, self.n_out = int(L.nxg_weight_n_in(handle)), int(L.nxg_weight_n_out(handle))
         self.n_blk = (self.n_in + BLOCK - 1) // BLOCK
-        self.device_bytes = int(L.nxg_weight_device_bytes(h))
+        self.device_bytes = int(L.nxg_weight_device_bytes(handle))
 
     @property
     def handle(self) -> ctypes.c_void_p:
@@ -333,6 +362,139 @@ def block_sums(weight: DeviceWeight, qa: QAct, stream=None):
     _check(load_library().nxg_linear_i8_block_sums(weight.handle, qa.q.data_ptr(), qa.T, s.data_ptr(),
                                                    _stream_ptr(stream)), "block_sums")
     return s
+
+
+@dataclass
+class TensorInfo:
+    name: str
+    type: int
+    n_dims: int
+    ne: tuple            # ggml ne[0..3]: ne[0] is the row length
+    offset: int          # from the start of the data section
+    nbytes: int
+
+
+class GGUF:
+    """A GGUF model file (include/nxg_gguf.h): metadata, tensor table, tensor bytes, and
+    the int8 load of the linear weights (the reference's nextera_load,
+    src/nexterabert.cpp:1549-1712, for the tensors its int8 GEMM takes)."""
+
+    def __init__(self, path: os.PathLike):
+        L = load_library()
+        h = ctypes.c_void_p()
+        _check(L.nxg_gguf_open(os.fsencode(path), ctypes.byref(h)), "gguf_open")
+        self._h, self.path = h, str(path)
+        self.version = int(L.nxg_gguf_version(h))
+        self.alignment = int(L.nxg_gguf_alignment(h))
+        self.data_offset = int(L.nxg_gguf_data_offset(h))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) and self._h.value:
+            load_library().nxg_gguf_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # metadata
+    def keys(self) -> List[str]:
+        L = load_library()
+        return [L.nxg_gguf_key(self._h, i).decode() for i in range(L.nxg_gguf_n_kv(self._h))]
+
+    def _str(self, fn, *args) -> str:
+        p, n = ctypes.c_void_p(), ctypes.c_uint64()
+        _check(fn(self._h, *args, ctypes.byref(p), ctypes.byref(n)), "gguf metadata")
+        return ctypes.string_at(p.value, n.value).decode("utf-8", errors="surrogateescape") if n.value else ""
+
+    def get(self, key: str, default=None):
+        """The value of `key` as int, float, bool, str or list; `default` if absent."""
+        L = load_library()
+        i = L.nxg_gguf_find_key(self._h, key.encode())
+        if i < 0:
+            return default
+        t = L.nxg_gguf_kv_type(self._h, i)
+        if t == GGUF_STRING:
+            return self._str(L.nxg_gguf_get_str, i)
+        if t == GGUF_ARRAY:
+            et, n = ctypes.c_int32(), ctypes.c_uint64()
+            _check(L.nxg_gguf_arr_info(self._h, i, ctypes.byref(et), ctypes.byref(n)), "gguf metadata")
+            out = []
+            for j in range(n.value):
+                if et.value == GGUF_STRING:
+                    out.append(self._str(L.nxg_gguf_arr_str, i, j))
+                elif et.value in (GGUF_FLOAT32, GGUF_FLOAT64):
+                    v = ctypes.c_double()
+                    _check(L.nxg_gguf_arr_f64(self._h, i, j, ctypes.byref(v)), "gguf metadata")
+                    out.append(v.value)
+                else:
+                    v = ctypes.c_int64()
+                    _check(L.nxg_gguf_arr_i64(self._h, i, j, ctypes.byref(v)), "gguf metadata")
+                    out.append(bool(v.value) if et.value == GGUF_BOOL else v.value)
+            return out
+        if t in (GGUF_FLOAT32, GGUF_FLOAT64):
+            v = ctypes.c_double()
+            _check(L.nxg_gguf_get_f64(self._h, i, ctypes.byref(v)), "gguf metadata")
+            return v.value
+        v = ctypes.c_int64()
+        _check(L.nxg_gguf_get_i64(self._h, i, ctypes.byref(v)), "gguf metadata")
+        return bool(v.value) if t == GGUF_BOOL else v.value
+
+    def metadata(self) -> Dict[str, object]:
+        return {k: self.get(k) for k in self.keys()}
+
+    # tensors
+    def tensors(self) -> List[TensorInfo]:
+        L = load_library()
+        out = []
+        for i in range(L.nxg_gguf_n_tensors(self._h)):
+            t, nd = ctypes.c_int32(), ctypes.c_int32()
+            ne = (ctypes.c_int64 * 4)()
+            off, nb = ctypes.c_uint64(), ctypes.c_uint64()
+            _check(L.nxg_gguf_tensor_info(self._h, i, ctypes.byref(t), ctypes.byref(nd), ne, ctypes.byref(off),
+                                          ctypes.byref(nb)), "gguf tensor_info")
+            out.append(TensorInfo(L.nxg_gguf_tensor_name(self._h, i).decode(), t.value, nd.value, tuple(ne),
+                                  off.value, nb.value))
+        return out
+
+    def _index(self, name: str) -> int:
+        i = load_library().nxg_gguf_find_tensor(self._h, name.encode())
+        if i < 0:
+            raise KeyError(name)
+        return i
+
+    def tensor_bytes(self, name: str) -> np.ndarray:
+        """A copy of the tensor's bytes as stored in the file."""
+        L = load_library()
+        i = self._index(name)
+        info = self.tensors()[i]
+        ptr = L.nxg_gguf_tensor_data(self._h, i)
+        return np.frombuffer(ctypes.string_at(ptr, info.nbytes), dtype=np.uint8).copy()
+
+    def int8_names(self) -> List[str]:
+        """The tensors the reference runs on its int8 GEMM (src/nexterabert.cpp:1658-1667)."""
+        L = load_library()
+        return [t.name for t in self.tensors()
+                if L.nxg_weight_is_int8(t.name.encode(), t.n_dims, t.type, t.ne[0], t.ne[1], 1)]
+
+    def load_int8_weights(self, names: Optional[Sequence[str]] = None, n_threads: int = 0) -> Dict[str, DeviceWeight]:
+        """Expands and uploads the int8 linear weights (all of them by default)."""
+        L = load_library()
+        out = {}
+        for name in (self.int8_names() if names is None else names):
+            h = ctypes.c_void_p()
+            _check(L.nxg_gguf_weight_create(self._h, self._index(name), n_threads, ctypes.byref(h)),
+                   f"gguf_weight_create({name})")
+            out[name] = DeviceWeight(None, handle=h)
+        return out
 
 
 def cu_offsets_of(lengths: Sequence[int]) -> np.ndarray:

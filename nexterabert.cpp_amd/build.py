@@ -44,10 +44,11 @@ def build(verbose: bool = False) -> Path:
               "-fvisibility=hidden", "-DNXG_BUILD", f"-I{INCLUDE}", f"-I{CSRC}", "-Wall"]
     hip_only = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
     _run(["g++", *common, "-pthread", "-c", CSRC / "nxg_host.cpp", "-o", OBJ / "nxg_host.o"], verbose)
+    _run(["g++", *common, "-c", CSRC / "nxg_gguf.cpp", "-o", OBJ / "nxg_gguf.o"], verbose)
     _run([_hipcc(), *hip_only, *common, "-c", CSRC / "nxg_linear.hip", "-o", OBJ / "nxg_linear.o"], verbose)
     tmp = LIB.with_suffix(".so.tmp")
     _run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread",
-          OBJ / "nxg_linear.o", OBJ / "nxg_host.o", "-o", tmp], verbose)
+          OBJ / "nxg_linear.o", OBJ / "nxg_host.o", OBJ / "nxg_gguf.o", "-o", tmp], verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
-HEADER = ROOT / "include" / "nxg_linear.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def bits(a):
@@ -19,14 +19,15 @@ def bits(a):
 
 
 def declared_symbols():
-    text = HEADER.read_text()
+    text = "".join(h.read_text() for h in HEADERS)
     return sorted(set(re.findall(r"NXG_API\s+[^;(]*?\b(nxg_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_path():
     names = declared_symbols()
     for n in ("nxg_quantize_rows", "nxg_linear_i8", "nxg_weight_create", "nxg_expand_weight",
-              "nxg_weight_is_int8", "nxg_linear_i8_block_sums", "nxg_qact_export"):
+              "nxg_weight_is_int8", "nxg_linear_i8_block_sums", "nxg_qact_export",
+              "nxg_linear_i8_relu2_q8", "nxg_quantize_rows_relu2", "nxg_gguf_open", "nxg_gguf_weight_create"):
         assert n in names
 
 
