@@ -130,6 +130,14 @@ NXG_API int32_t nxg_quantize_rows(const float * x, int32_t T, int32_t n_in, int3
 NXG_API int32_t nxg_quantize_rows_relu2(const float * x, int32_t T, int32_t n_in, int32_t act_max,
                                         int8_t * q, float * sx, void * stream);
 
+/* op_rms_norm with an int8 consumer (src/nexterabert.cpp:463-482, quantized by for_rows,
+ * :414-438; chosen by rms_norm(..., int8_only(...)), e.g. :1285): each row becomes
+ * (x * inv) * gain with inv = 1 / sqrt(dot / n_in + eps), dot = dot_f32(x, x) in the
+ * reference's AVX2 accumulation order (:124-149), then quantize_row as nxg_quantize_rows.
+ *   gain  device float [n_in] (the norm's weight);  eps  the model's rms_norm_epsilon */
+NXG_API int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps, int32_t T, int32_t n_in,
+                                          int32_t act_max, int8_t * q, float * sx, void * stream);
+
 /* The qact buffers in the reference's own format (src/nexterabert.cpp:368-375):
  *   u8  device uint8 [T][n_in], the reference's u8 values (q + act_max + 1)
  *   sx_ref device float, ((T+3)/4)*n_blk*4 floats, [token/4][block][token%4] */

@@ -70,6 +70,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_qact_sx_bytes": ([i32, i32], sz),
         "nxg_quantize_rows": ([P, i32, i32, i32, P, P, P], i32),
         "nxg_quantize_rows_relu2": ([P, i32, i32, i32, P, P, P], i32),
+        "nxg_rmsnorm_quantize_rows": ([P, P, ctypes.c_float, i32, i32, i32, P, P, P], i32),
         "nxg_qact_export": ([P, P, i32, i32, i32, P, P, P], i32),
         "nxg_weight_create": ([P, P, i32, i32, ctypes.POINTER(P)], i32),
         "nxg_weight_destroy": ([P], None),
@@ -284,6 +285,23 @@ def quantize_rows(x, act_max: int = 127, out: Optional[QAct] = None, stream=None
 def quantize_rows_relu2(x, act_max: int = 127, out: Optional[QAct] = None, stream=None) -> QAct:
     """op_relu_sqr quantized for an int8 consumer: quantize_row of relu(x)^2 per row."""
     return _quantize("nxg_quantize_rows_relu2", x, act_max, out, stream)
+
+
+def rmsnorm_quantize_rows(x, gain, eps: float, act_max: int = 127, out: Optional[QAct] = None, stream=None) -> QAct:
+    """op_rms_norm quantized for an int8 consumer: quantize_row of (x * inv) * gain per row,
+    inv = 1 / sqrt(mean(x^2) + eps) with the reference's dot_f32 order."""
+    torch = _torch()
+    if x.dtype != torch.float32 or x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
+        raise ValueError("x must be a contiguous 2-D float32 device tensor")
+    T, n_in = x.shape
+    if gain.dtype != torch.float32 or tuple(gain.shape) != (n_in,) or not gain.is_cuda or not gain.is_contiguous():
+        raise ValueError(f"gain must be a contiguous float32 device tensor of shape ({n_in},)")
+    qa = out if out is not None else qact_alloc(T, n_in, act_max, x.device)
+    qa.T, qa.n_in, qa.act_max = T, n_in, act_max
+    _check(load_library().nxg_rmsnorm_quantize_rows(x.data_ptr(), gain.data_ptr(), float(eps), T, n_in, act_max,
+                                                     qa.q.data_ptr(), qa.sx.data_ptr(), _stream_ptr(stream)),
+           "rmsnorm_quantize_rows")
+    return qa
 
 
 def export_qact(qa: QAct, stream=None):
@@ -536,6 +554,11 @@ class Builder:
             raise KeyError(f"{name} is not an int8 weight")
         qa = x if isinstance(x, QAct) else self.quantized(x)
         return linear_i8(w, qa, residual=residual, cu_offsets=cu_offsets, out=out)
+
+    def rms_norm(self, x, gain, eps: float) -> QAct:
+        """builder::rms_norm with int8 consumers (src/nexterabert.cpp:463-482, e.g. :1285):
+        the normalized rows are quantized where they are made; the f32 rows are not kept."""
+        return rmsnorm_quantize_rows(x, gain, eps, self.act_max)
 
     def mlp(self, fc: str, proj: str, h, x, cu_offsets=None, out=None):
         """x + c_proj(relu(c_fc(h))^2) (src/nexterabert.cpp:1284-1289). With both weights

@@ -103,19 +103,21 @@ __device__ __forceinline__ int quant1(float x, float inv) {
     return u - (ACT_MAX + 1);
 }
 
-// One workgroup per (16-row group, 256-input block), the block index fastest. Wave w quantizes rows
-// 4w..4w+3; the 16 lanes of a row read its 256 inputs as 4 contiguous 256-byte
-// pieces, so lane c holds inputs 64i + 4c + e (i, e = 0..3). The int8 results are
-// gathered in LDS in fragment order and each wave stores one 1 KiB fragment.
-// RELU2: the rows are relu(x)^2 of the input (x > 0 ? x : 0, NaN giving 0, then
-// r * r), the reference's op_relu_sqr with an int8 consumer (src/nexterabert.cpp:484-505).
-template <int ACT_MAX, bool RELU2>
-__global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict__ x, int T, int n_in, int KS,
-                                                       int n_blk, int8_t * __restrict__ q, float * __restrict__ sx) {
-    __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
+// Row transforms applied before quantize_row: none (op_copy and producers that hand over
+// f32 rows), relu^2 (op_relu_sqr, src/nexterabert.cpp:484-505: x > 0 ? x : 0, a NaN
+// giving 0, then r * r) and RMSNorm (op_rms_norm, :463-482: (x * inv) * gain).
+enum qmode { Q_PLAIN = 0, Q_RELU2 = 1, Q_RMSNORM = 2 };
 
-    // block index fastest: consecutive workgroups read consecutive 1 KiB pieces of the same rows
-    const int g = (int) (blockIdx.x / (unsigned) n_blk), B = (int) (blockIdx.x % (unsigned) n_blk);
+// quantize_row of one (16-row group g, 256-input block B) by a workgroup of 4 waves.
+// Wave w quantizes rows 4w..4w+3; the 16 lanes of a row read its 256 inputs as 4
+// contiguous 256-byte pieces, so lane c holds inputs 64i + 4c + e (i, e = 0..3). The
+// int8 results are gathered in LDS in fragment order and each wave stores one 1 KiB
+// fragment. Q_RMSNORM: inv is the row's 1/sqrt(mean(x^2) + eps). Ends with the stage
+// buffer still being read by the stores: callers looping over blocks sync before reuse.
+template <int ACT_MAX, int MODE>
+__device__ __forceinline__ void quantize_block(const float * __restrict__ x, int T, int n_in, int KS, int n_blk,
+                                               int8_t * __restrict__ q, float * __restrict__ sx, int g, int B,
+                                               int * stage, float inv_row, const float * __restrict__ gain) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rl = wave * 4 + (lane >> 4);     // row within the 16-row group
     const int t = g * 16 + rl;
@@ -130,18 +132,22 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict_
         if (present[i]) {
             const v4f f = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(x + (size_t) t * n_in + kb + 64 * i + 4 * c));
             xv[i][0] = f.x; xv[i][1] = f.y; xv[i][2] = f.z; xv[i][3] = f.w;
-            if (RELU2) {
+            if (MODE == Q_RELU2) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float r = xv[i][e] > 0.0f ? xv[i][e] : 0.0f;
                     xv[i][e] = r * r;
                 }
+            } else if (MODE == Q_RMSNORM) {
+                const v4f gv = *reinterpret_cast<const v4f *>(gain + kb + 64 * i + 4 * c);
+                const float gr[4] = { gv.x, gv.y, gv.z, gv.w };
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xv[i][e] = (xv[i][e] * inv_row) * gr[e];
             }
         } else {
             xv[i][0] = xv[i][1] = xv[i][2] = xv[i][3] = 0.0f;
         }
     }
-
     bool any_nan = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -222,6 +228,61 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict_
     if (ks < KS) {
         const int4 v = reinterpret_cast<const int4 *>(stage)[wave * 64 + lane];
         *reinterpret_cast<int4 *>(q + ((size_t) g * KS + ks) * FRAG + lane * 16) = v;
+    }
+}
+
+// One workgroup per (16-row group, 256-input block), the block index fastest, so that
+// consecutive workgroups read consecutive 1 KiB pieces of the same rows.
+template <int ACT_MAX, int MODE>
+__global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict__ x, int T, int n_in, int KS,
+                                                       int n_blk, int8_t * __restrict__ q, float * __restrict__ sx) {
+    __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
+    const int g = (int) (blockIdx.x / (unsigned) n_blk), B = (int) (blockIdx.x % (unsigned) n_blk);
+    quantize_block<ACT_MAX, MODE>(x, T, n_in, KS, n_blk, q, sx, g, B, stage, 1.0f, nullptr);
+}
+
+// op_rms_norm feeding an int8 linear (src/nexterabert.cpp:463-482 through for_rows'
+// quantize_row, :414-438): one workgroup per 16-row group. First each row's
+// dot_f32(x, x) exactly as the reference's AVX2 code orders it (:124-149): 32 FMA
+// chains, chain a taking elements 32m + a (lane c of the row runs chains 2c and 2c+1),
+// then (s0 + s1) + (s2 + s3) lane-wise (chains 8k + j are accumulator s_k, lane j), then
+// hsum256: lanes j and j+4, then 0+2 and 1+3, then those two -- each step a shuffle
+// within the row's 16 lanes (fp32 addition is commutative, so either operand order gives
+// the same bits). inv = 1 / sqrt(dot / C + eps), correctly rounded. Then every block is
+// re-read and quantized as (x * inv) * gain. C % 32 == 0, so the reference's remainder
+// loops never run.
+template <int ACT_MAX>
+__global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(const float * __restrict__ x, const float * __restrict__ gain,
+                                                               float eps, int T, int n_in, int KS, int n_blk,
+                                                               int8_t * __restrict__ q, float * __restrict__ sx) {
+    __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
+    const int g = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = g * 16 + wave * 4 + (lane >> 4);
+    const int c = lane & 15;
+    float a0 = 0.0f, a1 = 0.0f;                // chains 2c and 2c + 1
+    if (t < T) {
+        const float * xr = x + (size_t) t * n_in + 2 * c;
+        for (int m = 0; m < n_in / 32; ++m) {
+            const float2 v = *reinterpret_cast<const float2 *>(xr + 32 * m);
+            a0 = __builtin_fmaf(v.x, v.x, a0);
+            a1 = __builtin_fmaf(v.y, v.y, a1);
+        }
+    }
+    // lane c holds s_k[j], s_k[j+1] with k = c/4, j = 2(c%4)
+    a0 = a0 + __shfl_xor(a0, 4);               // s0 + s1, s2 + s3
+    a1 = a1 + __shfl_xor(a1, 4);
+    a0 = a0 + __shfl_xor(a0, 8);               // v[j] = (s0 + s1) + (s2 + s3)
+    a1 = a1 + __shfl_xor(a1, 8);
+    a0 = a0 + __shfl_xor(a0, 2);               // v[j] + v[j+4]: lanes q and q^2 (q = c%4)
+    a1 = a1 + __shfl_xor(a1, 2);
+    a0 = a0 + __shfl_xor(a0, 1);               // (v0+v4) + (v2+v6), (v1+v5) + (v3+v7)
+    a1 = a1 + __shfl_xor(a1, 1);
+    const float dot = a0 + a1;
+    const float inv = 1.0f / __builtin_sqrtf(dot / (float) n_in + eps);
+    for (int B = 0; B < n_blk; ++B) {
+        quantize_block<ACT_MAX, Q_RMSNORM>(x, T, n_in, KS, n_blk, q, sx, g, B, stage, inv, gain);
+        __syncthreads();                       // the stores have read the stage buffer
     }
 }
 
@@ -1118,11 +1179,11 @@ static int32_t launch_quantize(const float * x, int32_t T, int32_t n_in, int32_t
     const dim3 grid((unsigned) n_wg);
     hipStream_t s = (hipStream_t) stream;
     if (act_max == 127) {
-        if (relu2) quantize_kernel<127, true><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
-        else       quantize_kernel<127, false><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
+        if (relu2) quantize_kernel<127, Q_RELU2><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
+        else       quantize_kernel<127, Q_PLAIN><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
     } else {
-        if (relu2) quantize_kernel<63, true><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
-        else       quantize_kernel<63, false><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
+        if (relu2) quantize_kernel<63, Q_RELU2><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
+        else       quantize_kernel<63, Q_PLAIN><<<grid, 256, 0, s>>>(x, T, n_in, d.KS, d.n_blk, q, sx);
     }
     return launch_check("quantize_kernel");
 }
@@ -1135,6 +1196,22 @@ int32_t nxg_quantize_rows(const float * x, int32_t T, int32_t n_in, int32_t act_
 int32_t nxg_quantize_rows_relu2(const float * x, int32_t T, int32_t n_in, int32_t act_max,
                                 int8_t * q, float * sx, void * stream) {
     return launch_quantize(x, T, n_in, act_max, q, sx, stream, true);
+}
+
+int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps, int32_t T, int32_t n_in,
+                                  int32_t act_max, int8_t * q, float * sx, void * stream) {
+    qact_dims d;
+    if (!qact_dims_of(T, n_in, d)) return fail(NXG_EINVAL, "rmsnorm_quantize: T=%d n_in=%d (n_in must be a positive multiple of 32)", T, n_in);
+    if (act_max != 127 && act_max != 63) return fail(NXG_EINVAL, "rmsnorm_quantize: act_max must be 127 or 63, got %d", act_max);
+    if (T == 0) return NXG_OK;
+    if (!x || !gain || !q || !sx) return fail(NXG_EINVAL, "rmsnorm_quantize: null buffer");
+    int rc = check_device();
+    if (rc) return rc;
+    const dim3 grid((unsigned) (d.MP / 16));
+    hipStream_t s = (hipStream_t) stream;
+    if (act_max == 127) rmsnorm_quantize_kernel<127><<<grid, 256, 0, s>>>(x, gain, eps, T, n_in, d.KS, d.n_blk, q, sx);
+    else                rmsnorm_quantize_kernel<63><<<grid, 256, 0, s>>>(x, gain, eps, T, n_in, d.KS, d.n_blk, q, sx);
+    return launch_check("rmsnorm_quantize_kernel");
 }
 
 int32_t nxg_qact_export(const int8_t * q, const float * sx, int32_t T, int32_t n_in, int32_t act_max,

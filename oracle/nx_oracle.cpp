@@ -182,7 +182,31 @@ int orc_quantize_rows_simd_mt(const float * x, int T, int n_in, int act_max, uin
     return 0;
 }
 
-// build_i8_weight from already dequantized rows (row-major n_out x n_in f32):
+// dot_f32 (src/nexterabert.cpp:133-149) in the AVX2 build's order: four 8-lane FMA
+// accumulators s0..s3 over 32-element chunks (s_k lane j takes element 32m + 8k + j), the
+// 8-element remaining chunks into s0, then hsum256 (src/nexterabert.cpp:124-129) of
+// (s0 + s1) + (s2 + s3): lanes j and j+4, then 0+2 and 1+3, then those two. n % 8 == 0
+// (the scalar tail after the vector part is not used: every qact row has n % 32 == 0).
+static float dot_avx2_order(const float * a, const float * b, int n) {
+    float s[4][8] = {};
+    int i = 0;
+    for (; i + 32 <= n; i += 32) {
+        for (int k = 0; k < 4; ++k) {
+            for (int j = 0; j < 8; ++j) s[k][j] = std::fma(a[i + 8 * k + j], b[i + 8 * k + j], s[k][j]);
+        }
+    }
+    for (; i + 8 <= n; i += 8) {
+        for (int j = 0; j < 8; ++j) s[0][j] = std::fma(a[i + j], b[i + j], s[0][j]);
+    }
+    float v[8];
+    for (int j = 0; j < 8; ++j) v[j] = (s[0][j] + s[1][j]) + (s[2][j] + s[3][j]);
+    float h[4];
+    for (int j = 0; j < 4; ++j) h[j] = v[j] + v[j + 4];
+    const float h0 = h[0] + h[2], h1 = h[1] + h[3];
+    return h0 + h1;
+}
+
+
 // src/nexterabert.cpp:1030-1042. scale/off are [n_blk][n_out].
 void orc_expand_rows(const float * rows, int n_in, int n_out, int act_off,
                      int8_t * w, float * scale, int32_t * off) {
@@ -223,6 +247,17 @@ static float fp16_to_f32(uint16_t h) {
     u |= sign;
     std::memcpy(&v, &u, 4);
     return v;
+}
+
+// op_rms_norm's row (src/nexterabert.cpp:463-482): inv = 1 / sqrt(dot(x, x) / C + eps),
+// out = (x * inv) * gain, with dot in the AVX2 order above. C % 8 == 0.
+void orc_rms_norm_rows(const float * x, const float * gain, float eps, int T, int C, float * out) {
+    for (int t = 0; t < T; ++t) {
+        const float * xr = x + (size_t) t * C;
+        float * o = out + (size_t) t * C;
+        const float inv = 1.0f / std::sqrt(dot_avx2_order(xr, xr, C) / (float) C + eps);
+        for (int i = 0; i < C; ++i) o[i] = (xr[i] * inv) * gain[i];
+    }
 }
 
 void orc_dequant_q8_0(const uint8_t * data, int64_t n, float * out) {

@@ -52,6 +52,8 @@ def lib() -> ctypes.CDLL:
         L.orc_quantize_rows_simd_mt.restype = i32
         L.orc_expand_rows.argtypes = [P, i32, i32, i32, P, P, P]
         L.orc_expand_rows.restype = None
+        L.orc_rms_norm_rows.argtypes = [P, P, ctypes.c_float, i32, i32, P]
+        L.orc_rms_norm_rows.restype = None
         L.orc_dequant_q8_0.argtypes = [P, ctypes.c_int64, P]
         L.orc_dequant_q8_0.restype = None
         L.orc_block_sums.argtypes = [P, P, i32, i32, P, i32, P]
@@ -114,6 +116,19 @@ def relu2(x: np.ndarray) -> np.ndarray:
     with np.errstate(invalid="ignore", over="ignore"):
         r = np.where(x > np.float32(0), x, np.float32(0)).astype(np.float32)
         return (r * r).astype(np.float32)
+
+
+def rms_norm(x: np.ndarray, gain: np.ndarray, eps: float) -> np.ndarray:
+    """op_rms_norm (src/nexterabert.cpp:463-482) as the AVX2 build computes it:
+    inv = 1 / sqrt(dot_f32(x, x) / C + eps) with dot_f32's accumulation order
+    (src/nexterabert.cpp:124-149), out = (x * inv) * gain. C % 8 == 0."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    g = np.ascontiguousarray(gain, dtype=np.float32)
+    T, C = x.shape
+    assert C % 8 == 0 and g.shape == (C,)
+    out = np.empty_like(x)
+    lib().orc_rms_norm_rows(_p(x), _p(g), float(np.float32(eps)), T, C, _p(out))
+    return out
 
 
 def expand_rows(rows: np.ndarray, act_off: int = 128):

@@ -67,6 +67,22 @@ def fma(a: float, b: float, c: float) -> float:
     return round_f32(_q(a) * _q(b) + _q(c))
 
 
+def sqrt(a: float) -> float:
+    """Correctly rounded square root of a finite a >= 0. floor(sqrt(q) * 2^p) is an
+    integer square root; with p = 160 every binary32 rounding midpoint times 2^p is an
+    integer, so a remainder (inexact root) can be represented by adding half a unit."""
+    q = _q(a)
+    if q < 0:
+        raise ValueError("sqrt of a negative value")
+    if q == 0:
+        return float(a)
+    p = 160
+    num, den = q.numerator << (2 * p), q.denominator
+    S = math.isqrt(num // den)
+    exact = S * S * den == num
+    return round_f32(Fraction(S, 2 ** p) if exact else Fraction(2 * S + 1, 2 ** (p + 1)))
+
+
 def rne_int(y: float) -> int:
     """Round to the nearest integer, ties to even (CVTPS2DQ's default mode)."""
     fy = _q(y)

@@ -183,3 +183,28 @@ def test_relu2_q8_bad_shapes_raise(nxg, torch, dev):
         nxg.linear_i8_relu2_q8(dw2, nxg.quantize_rows(x2))
     with pytest.raises(ValueError, match="n_out % 32"):
         nxg.linear_i8_relu2_q8(dw2, nxg.quantize_rows(x2), out=nxg.qact_alloc(64, 128))
+
+
+@pytest.mark.parametrize("T,n_in", [(333, 1024), (100, 2304), (17, 32), (50, 96), (1, 4096)])
+@pytest.mark.parametrize("act_max", [127, 63])
+def test_rmsnorm_quantize_matches_oracle(nxg, orc, torch, dev, T, n_in, act_max):
+    """op_rms_norm feeding an int8 linear: the oracle's RMSNorm (AVX2 dot order), then
+    quantize_row; rows of very different scales, eps 1e-8 and 0, NaN/Inf/zero rows."""
+    say(f"rmsnorm_quantize T={T} n_in={n_in} act_max={act_max}")
+    rng = np.random.default_rng(T + n_in + act_max)
+    x = (rng.standard_normal((T, n_in)) * 10.0 ** rng.integers(-6, 6, (T, 1))).astype(np.float32)
+    g = (1.0 + 0.2 * rng.standard_normal(n_in)).astype(np.float32)
+    if T > 8:
+        x[1] = 0.0                       # eps 0: inv = inf, 0 * inf = NaN everywhere
+        x[2, 5] = np.nan
+        x[3, 7] = np.inf
+        x[4] = 1e-30                     # dot underflows to tiny values
+        x[5, ::3] = -0.0
+    for eps in (1e-8, 0.0):
+        qa = nxg.rmsnorm_quantize_rows(torch.from_numpy(x).cuda(), torch.from_numpy(g).cuda(), eps, act_max)
+        u8, sx = nxg.export_qact(qa)
+        y = orc.rms_norm(x, g, eps)
+        q_ref, sx_ref = orc.quantize_rows(y, act_max)
+        assert (u8.cpu().numpy() == q_ref).all(), f"eps={eps}"
+        s = sx.cpu().numpy()
+        assert ((bits(s) == bits(sx_ref)) | (np.isnan(s) & np.isnan(sx_ref))).all(), f"eps={eps}"

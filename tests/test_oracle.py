@@ -193,6 +193,82 @@ def test_relu2_is_the_exact_square_rounded_once(orc):
     assert (bits(y) == bits(want)).all()
 
 
+# --- op_rms_norm -----------------------------------------------------------------
+
+def _exact_dot_avx2(x):
+    """dot_f32(x, x) in the AVX2 build's order (src/nexterabert.cpp:124-149), every
+    operation rounded once by exact arithmetic."""
+    s = [[0.0] * 8 for _ in range(4)]
+    n = len(x)
+    i = 0
+    while i + 32 <= n:
+        for k in range(4):
+            for j in range(8):
+                e = float(x[i + 8 * k + j])
+                s[k][j] = X.fma(e, e, s[k][j])
+        i += 32
+    while i + 8 <= n:
+        for j in range(8):
+            e = float(x[i + j])
+            s[0][j] = X.fma(e, e, s[0][j])
+        i += 8
+    v = [X.add(X.add(s[0][j], s[1][j]), X.add(s[2][j], s[3][j])) for j in range(8)]
+    h = [X.add(v[j], v[j + 4]) for j in range(4)]
+    return X.add(X.add(h[0], h[2]), X.add(h[1], h[3]))
+
+
+def _exact_rms_norm(x, g, eps):
+    C = len(x)
+    inv = X.div(1.0, X.sqrt(X.add(X.div(_exact_dot_avx2(x), float(C)), float(np.float32(eps)))))
+    return np.array([X.mul(X.mul(float(x[i]), inv), float(g[i])) for i in range(C)], np.float32)
+
+
+@pytest.mark.parametrize("C", [32, 64, 96, 136])
+def test_rms_norm_matches_exact_arithmetic(orc, C):
+    rng = np.random.default_rng(C)
+    x = (rng.standard_normal((3, C)) * 10.0 ** rng.integers(-3, 4, (3, C))).astype(np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    for eps in (1e-8, 1e-5, 0.0):
+        y = orc.rms_norm(x, g, eps)
+        for t in range(3):
+            assert (bits(y[t]) == bits(_exact_rms_norm(x[t], g, eps))).all()
+
+
+def test_rms_norm_follows_the_avx2_accumulation_order(orc):
+    # one large square among small ones: where the small ones are absorbed depends on
+    # which accumulator chain and combine step they meet the large one in
+    C = 64
+    x = np.full(C, np.float32(3e-4), np.float32)
+    x[5] = np.float32(1.0)
+    x[37] = np.float32(-1.0)
+    exact_order = _exact_dot_avx2(x)
+    seq = 0.0
+    for e in x:
+        seq = X.fma(float(e), float(e), seq)
+    assert exact_order != seq            # the check below can tell the two orders apart
+    g = np.ones(C, np.float32)
+    y = orc.rms_norm(x[None, :], g, 0.0)[0]
+    assert (bits(y) == bits(_exact_rms_norm(x, g, 0.0))).all()
+
+
+def test_rms_norm_closed_forms(orc):
+    C = 64
+    g = np.full(C, np.float32(2.0), np.float32)
+    # zero row, eps 0: inv = 1/0 = inf, 0 * inf = NaN
+    assert np.isnan(orc.rms_norm(np.zeros((1, C), np.float32), g, 0.0)).all()
+    # zero row, eps > 0: 0
+    assert (orc.rms_norm(np.zeros((1, C), np.float32), g, 1e-8) == 0).all()
+    # constant row a = 2: dot = 256 exactly, mean 4, inv 0.5, out (2 * 0.5) * 2 = 2
+    assert (orc.rms_norm(np.full((1, C), np.float32(2.0)), g, 0.0) == 2.0).all()
+    # a NaN or an Inf anywhere makes inv NaN or 0
+    x = np.ones((2, C), np.float32)
+    x[0, 7] = np.nan
+    x[1, 9] = np.inf
+    y = orc.rms_norm(x, g, 0.0)
+    assert np.isnan(y[0]).all()
+    assert np.isnan(y[1, 9]) and (y[1, np.arange(C) != 9] == 0).all()
+
+
 # --- build_i8_weight ----------------------------------------------------------
 
 @pytest.mark.parametrize("n_in", [64, 256 + 32, 1024])
