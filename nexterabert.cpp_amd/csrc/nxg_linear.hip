@@ -845,6 +845,236 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
 }
 
 // ---------------------------------------------------------------------------
+// GEMMs for few rows: latency-bound, so operands go straight to registers
+// ---------------------------------------------------------------------------
+
+constexpr int SDT = 2;                     // activation fragments (16 tokens each) per wave
+#ifndef NXG_SMALL_DEPTH4
+#define NXG_SMALL_DEPTH4 4                 // k-steps in flight per wave of the 32 x 64 pieces
+#endif
+// k-steps in flight per wave: two 256-input blocks for 32 x 32 pieces, one for 32 x 64
+// pieces (whose 6 fragments per k-step would otherwise need more than 256 registers)
+template <int FN> constexpr int small_depth() { return FN == 2 ? 8 : NXG_SMALL_DEPTH4; }
+constexpr int SNB_MAX = 16;                // 256-input blocks (n_in <= 4096): sw kept in LDS
+#ifndef NXG_SMALL_MAX_WAVES_PER_CU
+#define NXG_SMALL_MAX_WAVES_PER_CU 4       // gemm_small while its waves number at most this many per CU
+#endif
+#ifndef NXG_RELU2_SMALL_MAX_WAVES_PER_CU
+#define NXG_RELU2_SMALL_MAX_WAVES_PER_CU 6 // gemm_relu2_small likewise
+#endif
+#ifndef NXG_SMALL_FN
+#define NXG_SMALL_FN 0                     // weight fragments per wave of gemm_small (0: chosen per launch)
+#endif
+
+// sw of blocks 0 .. n_blk - 1 for the nw features n0 .. n0 + nw - 1 into LDS, sl[B * nw + c].
+// nw divides 256 and n0 is a multiple of nw, so the rows exist (NP is a multiple of 256).
+template <int NW>
+__device__ __forceinline__ void small_sw_fill(const gemm_params & p, int n0, float * sl) {
+    for (int i = threadIdx.x; i < p.n_blk * (NW / 4); i += blockDim.x) {
+        const int B = i / (NW / 4), c = (i - B * (NW / 4)) * 4;
+        *reinterpret_cast<v4f *>(sl + B * NW + c) = *reinterpret_cast<const v4f *>(p.sw + (size_t) B * p.NP + n0 + c);
+    }
+}
+
+// One wave's 32 x 16FN piece: tokens of fragment rows fr0, fr0 + 1, features of weight
+// fragment rows nr0 .. nr0 + FN - 1. Per k-step the wave loads its 2 + FN fragments
+// (1 KiB each, one dwordx4 per lane, already in MFMA operand order) from global memory
+// straight into registers, D k-steps ahead, so that it keeps that many k-steps of
+// loads in flight however little it computes per k-step. The MFMA operands, the lane
+// layout of the accumulators and the per-block epilogue f = fma((float) s * sx[t], sw[n], f)
+// are those of gemm_kernel: f[j][i][r] is token 16(fr0 + j) + lane % 16, feature
+// 16(nr0 + i) + 4(lane / 16) + r. sx is loaded one block ahead; sw comes from LDS,
+// swl[B * PITCH + 16 i + 4(lane / 16)], written by fill() once the first k-steps' loads
+// are in flight (so that its wait for its own loads costs no extra round trip) and
+// published by the workgroup barrier that follows it here. last() runs at the start of
+// the last block (the caller's residual loads then overlap its MFMAs). With K256
+// (n_in % 256 == 0) no k-step is loaded twice; otherwise the last block has fewer than
+// 4 k-steps and refills past the last k-step re-read it.
+template <int FN, bool K256, int PITCH, typename Fill, typename Last>
+__device__ __forceinline__ void small_piece(const gemm_params & p, int fr0, int nr0, const float * swl,
+                                            float (&f)[SDT][FN][4], Fill fill, Last last) {
+    constexpr int NF = SDT + FN;           // fragments per k-step
+    constexpr int D = small_depth<FN>();
+    static_assert(D == 4 || D == 8, "k-steps in flight: one or two blocks");
+    const int lane = threadIdx.x & 63;
+    const int nb = p.n_blk;
+    const size_t frow = (size_t) p.KS * FRAG;
+
+    // Fragment rows past the activation's last re-read its last one (their outputs are
+    // not stored). Weight rows are padded to a multiple of 256: rows nr0 .. nr0 + FN - 1
+    // exist when 16 nr0 < N and nr0 is a multiple of FN.
+    int fr[SDT];
+    const int8_t * base[NF];               // fragment rows, uniform
+#pragma unroll
+    for (int j = 0; j < SDT; ++j) {
+        fr[j] = min(fr0 + j, p.MF - 1);
+        base[j] = p.a + fr[j] * frow;
+    }
+#pragma unroll
+    for (int i = 0; i < FN; ++i) base[SDT + i] = p.w + (nr0 + i) * frow;
+    const uint32_t lane16 = (uint32_t) lane * 16;
+
+    v4i buf[D][NF];
+    // k-step ks (< KS) into d. The scheduling barrier keeps each k-step's loads where
+    // they are issued: the compiler would otherwise sink them towards their first use
+    // and shorten the prefetch.
+    auto load = [&](v4i (&d)[NF], int ks) {
+        const size_t ko = (size_t) ks * FRAG;
+#pragma unroll
+        for (int u = 0; u < NF; ++u) d[u] = *reinterpret_cast<const v4i *>(base[u] + ko + lane16);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    float sxs[2][SDT];
+    auto load_sx = [&](float (&d)[SDT], int B) {
+#pragma unroll
+        for (int j = 0; j < SDT; ++j) {
+            const int t = fr[j] * 16 + (lane & 15);
+            d[j] = p.sx[((size_t) (t >> 2) * nb + B) * 4 + (t & 3)];
+        }
+    };
+
+    load_sx(sxs[0], 0);
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        if (s < p.KS) load(buf[s], s);
+    }
+    fill();
+    lds_barrier();
+
+    v4i acc[SDT][FN];
+#pragma unroll
+    for (int j = 0; j < SDT; ++j)
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) f[j][i][r] = 0.0f;   // the reference's f = 0 before block 0
+
+    // Block b (H = b % 2): k-step 4b + ks lives in buf[(4H + ks) % D]; each slot, once
+    // multiplied, is refilled with the k-step D later: always (R_FULL), clamped to the
+    // last k-step (R_CLAMP, n_in % 256 != 0 only), or not at all (R_NONE, R_LAST). The
+    // block's sx are in set H; the last block (R_LAST) runs last() instead of loading
+    // the next block's sx. The refill mode is static: a run-time test around the loads
+    // would make the compiler keep both versions of every buffer register.
+    enum { R_FULL, R_CLAMP, R_NONE, R_LAST };
+    auto block = [&](int b, auto h_tag, auto mode_tag) {
+        constexpr int H = decltype(h_tag)::value;
+        constexpr int MODE = decltype(mode_tag)::value;
+        if (MODE == R_LAST) last();
+        else load_sx(sxs[H ^ 1], b + 1);
+        const int nks = K256 ? 4 : min(4, p.KS - 4 * b);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            if (K256 || ks < nks) {
+#pragma unroll
+                for (int j = 0; j < SDT; ++j)
+#pragma unroll
+                    for (int i = 0; i < FN; ++i)
+                        acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            buf[(4 * H + ks) % D][SDT + i], buf[(4 * H + ks) % D][j], ks == 0 ? v4i{0, 0, 0, 0} : acc[j][i], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (MODE == R_FULL) load(buf[(4 * H + ks) % D], 4 * b + ks + D);
+                if (MODE == R_CLAMP) load(buf[(4 * H + ks) % D], min(4 * b + ks + D, p.KS - 1));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            const v4f sw4 = *reinterpret_cast<const v4f *>(swl + b * PITCH + 16 * i + 4 * (lane >> 4));
+            const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
+#pragma unroll
+            for (int j = 0; j < SDT; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float prod = (float) acc[j][i][r] * sxs[H][j];
+                    f[j][i][r] = __builtin_fmaf(prod, swr[r], f[j][i][r]);
+                }
+        }
+    };
+    using H0 = std::integral_constant<int, 0>;
+    using H1 = std::integral_constant<int, 1>;
+    using FULL = std::integral_constant<int, R_FULL>;
+    using CLAMP = std::integral_constant<int, R_CLAMP>;
+    using NONE = std::integral_constant<int, R_NONE>;
+    using LAST = std::integral_constant<int, R_LAST>;
+    int b = 0;
+    if (K256) {
+        // The last D/4 blocks have no k-step left to load; the others refill every slot.
+        const int nfull = nb - D / 4;
+        for (; b + 1 < nfull; b += 2) {
+            block(b, H0{}, FULL{});
+            block(b + 1, H1{}, FULL{});
+        }
+        if (b < nfull) {
+            block(b, H0{}, FULL{});
+            ++b;
+        }
+        // blocks b .. nb - 1 remain: one, or (D == 8) two
+        if (D == 8 && b + 2 == nb) {
+            if (b & 1) { block(b, H1{}, NONE{}); block(b + 1, H0{}, LAST{}); }
+            else       { block(b, H0{}, NONE{}); block(b + 1, H1{}, LAST{}); }
+        } else {
+            if (b & 1) block(b, H1{}, LAST{});
+            else       block(b, H0{}, LAST{});
+        }
+    } else {
+        for (; b + 2 < nb; b += 2) {
+            block(b, H0{}, CLAMP{});
+            block(b + 1, H1{}, CLAMP{});
+        }
+        if (b + 2 == nb) {
+            block(b, H0{}, CLAMP{});
+            block(b + 1, H1{}, LAST{});
+        } else {
+            block(b, H0{}, LAST{});
+        }
+    }
+}
+
+// fp32 rows out of a few-row GEMM: one wave per workgroup and piece (32 tokens x 16FN
+// features), pieces numbered with the feature piece fastest. One-wave workgroups let the
+// dispatcher spread a launch of few pieces over as many CUs as there are pieces; the
+// limit then is the bytes a CU takes in per cycle. Needs N % 4 == 0 (16-byte stores)
+// and n_blk <= SNB_MAX.
+template <int FN, bool RES, bool K256>
+__global__ __launch_bounds__(64) void gemm_small(gemm_params p) {
+    __shared__ __attribute__((aligned(16))) float swl[SNB_MAX * 16 * FN];
+    const int lane = threadIdx.x;
+    const int mt = blockIdx.x / p.n_nt, nt = blockIdx.x - mt * p.n_nt;
+    const int fr0 = mt * SDT, nr0 = nt * FN;
+    float f[SDT][FN][4];
+    // The residual of this lane's outputs, loaded at the start of the last block; rows
+    // and features past the output read row T - 1 / feature N - 4 (never stored).
+    v4f rv[SDT][FN];
+    auto load_res = [&] {
+        if (RES) {
+#pragma unroll
+            for (int j = 0; j < SDT; ++j)
+#pragma unroll
+                for (int i = 0; i < FN; ++i) {
+                    const int t = min((fr0 + j) * 16 + (lane & 15), p.T - 1);
+                    const int n = min((nr0 + i) * 16 + 4 * (lane >> 4), p.N - 4);
+                    rv[j][i] = *reinterpret_cast<const v4f *>(p.res + (size_t) t * p.N + n);
+                }
+        }
+    };
+    small_piece<FN, K256, 16 * FN>(p, fr0, nr0, swl, f, [&] { small_sw_fill<16 * FN>(p, nr0 * 16, swl); }, load_res);
+
+    // out[t][n .. n + 3] = (res +) f: 16 bytes per lane and fragment pair.
+#pragma unroll
+    for (int j = 0; j < SDT; ++j) {
+        const int t = (fr0 + j) * 16 + (lane & 15);
+        if (t >= p.T) continue;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            const int n = (nr0 + i) * 16 + 4 * (lane >> 4);
+            if (n >= p.N) continue;
+            v4f y = { f[j][i][0], f[j][i][1], f[j][i][2], f[j][i][3] };
+            if (RES) y = rv[j][i] + y;
+            *reinterpret_cast<v4f *>(p.out + (size_t) t * p.N + n) = y;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Wide GEMM with the relu^2 -> int8 output: 128 x 256 tiles, n_in % 256 == 0
 // ---------------------------------------------------------------------------
 
@@ -1081,6 +1311,78 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
         }
     }
     wait_vm<0>();
+}
+
+// relu(linear(x))^2 quantized for the next linear, for few rows (the same output as
+// gemm_relu2_q8): workgroups of 4 waves over 32 tokens x 256 features -- one 256-input
+// block of the next linear -- each wave a 32 x 64 piece computed by small_piece. The row
+// amax is reduced over the lanes of a wave (rows_max) and the 4 waves (LDS); relu^2, the
+// quantization, the fragment stores and the scale layout are gemm_relu2_q8's. Needs
+// n_in % 256 == 0 and n_blk <= SNB_MAX.
+template <int ACT_MAX>
+__global__ __launch_bounds__(256) void gemm_relu2_small(gemm_params p) {
+    __shared__ __attribute__((aligned(16))) float swl[SNB_MAX * WBN];
+    __shared__ __attribute__((aligned(16))) float am[SDT * 16 * 4];   // row maxima [row][wave]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int mt = blockIdx.x / p.n_nt, nt = blockIdx.x - mt * p.n_nt;
+    const int fr0 = mt * SDT, nr0 = nt * (WBN / 16) + wave * 4;
+    float f[SDT][4][4];
+    small_piece<4, true, WBN>(p, fr0, nr0, swl + wave * 64, f, [&] { small_sw_fill<WBN>(p, nt * WBN, swl); }, [] {});
+
+    // relu(f)^2 in place: f > 0 ? f : 0 (a NaN gives 0), then r * r.
+#pragma unroll
+    for (int j = 0; j < SDT; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float x = f[j][i][r] > 0.0f ? f[j][i][r] : 0.0f;
+                f[j][i][r] = x * x;
+            }
+    // Row maxima (values >= 0, no NaN: the reference's MAXPS fold is the plain maximum
+    // here): this lane's 16 values, the wave's 4 lanes of the row, then the 4 waves.
+#pragma unroll
+    for (int j = 0; j < SDT; ++j) {
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) m = fmaxf(m, f[j][i][r]);
+        m = rows_max(m);
+        if (lane < 16) am[(j * 16 + lane) * 4 + wave] = m;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < SDT; ++j) {
+        const int t = (fr0 + j) * 16 + (lane & 15);
+        const v4f a4 = *reinterpret_cast<const v4f *>(am + (j * 16 + (lane & 15)) * 4);
+        const bool row_ok = t < p.T;
+        const float amax = row_ok ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
+        const float scale = amax / (float) ACT_MAX;
+        const float inv = amax > 0.0f ? (float) ACT_MAX / amax : 0.0f;
+        // column 16i + 4(lane/16) + r of the wave's 64: byte r of d[i]
+        int d[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int n = (nr0 + i) * 16 + 4 * (lane >> 4);
+            int packed = 0;
+            if (row_ok && n < p.N) {
+                packed = (quant1<ACT_MAX>(f[j][i][0], inv) & 0xff) | ((quant1<ACT_MAX>(f[j][i][1], inv) & 0xff) << 8)
+                       | ((quant1<ACT_MAX>(f[j][i][2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(f[j][i][3], inv) & 0xff) << 24);
+            }
+            d[i] = packed;
+        }
+        // lane c + 16 i now gets columns 16 i + 0..15 of row c: one fragment lane
+        rows_transpose(d);
+        const int rf = fr0 + j, kf = nt * (WBN / 64) + wave;
+        if (rf < p.MF) {
+            if (kf < p.KSo) {
+                *reinterpret_cast<v4i *>(p.qo + ((size_t) rf * p.KSo + kf) * FRAG + lane * 16) = v4i{d[0], d[1], d[2], d[3]};
+            }
+            if (wave == 0 && lane < 16) p.sxo[((size_t) (t >> 2) * p.n_nt + nt) * 4 + (t & 3)] = scale;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1334,6 +1636,15 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
         const long long G = (long long) p.n_mt * p.n_nt;
         if (G > INT32_MAX / 2) return fail(NXG_EINVAL, "linear: T=%d too large", T);
         p.G = (int) G;
+        const long long G_small = (long long) ceil_div(p.MF, SDT) * p.n_nt;   // 4 waves each
+        if (p.n_blk <= SNB_MAX && 4 * G_small <= (long long) NXG_RELU2_SMALL_MAX_WAVES_PER_CU * device_cus()) {
+            p.n_mt = ceil_div(p.MF, SDT);
+            p.G = (int) G_small;
+            const dim3 grid((unsigned) p.G), block(256);
+            if (o.act_max == 127) gemm_relu2_small<127><<<grid, block, 0, s>>>(p);
+            else                  gemm_relu2_small<63><<<grid, block, 0, s>>>(p);
+            return launch_check("gemm_relu2_small");
+        }
         const dim3 grid((unsigned) std::min<long long>(G, device_cus())), block(WTHREADS);
         if (o.act_max == 127) gemm_relu2_q8<127><<<grid, block, 0, s>>>(p);
         else                  gemm_relu2_q8<63><<<grid, block, 0, s>>>(p);
@@ -1343,6 +1654,30 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     const long long G = (long long) p.n_mt * p.n_nt;
     if (G > INT32_MAX / 2) return fail(NXG_EINVAL, "linear: T=%d too large", T);
     p.G = (int) G;
+    // Few rows, one wave per piece: 32 x 32 pieces while they number at most
+    // NXG_SMALL_MAX_WAVES_PER_CU per CU, else 32 x 64 pieces (fewer bytes per output
+    // through each CU) while those do; beyond that the 128 x 128 tiles above, which
+    // read each operand fragment once per tile. (Measured on MI355X at 128..4096 rows.)
+    const long long W2 = (long long) ceil_div(p.MF, SDT) * ceil_div(p.N, 32);
+    const long long W4 = (long long) ceil_div(p.MF, SDT) * ceil_div(p.N, 64);
+    const long long w_max = (long long) NXG_SMALL_MAX_WAVES_PER_CU * device_cus();
+    const int fn = NXG_SMALL_FN ? NXG_SMALL_FN : (W2 <= w_max ? 2 : 4);
+    const long long n_waves = fn == 2 ? W2 : W4;
+    if (!o.sums && p.N % 4 == 0 && p.n_blk <= SNB_MAX && n_waves <= w_max) {
+        p.n_mt = ceil_div(p.MF, SDT);
+        p.n_nt = ceil_div(p.N, 16 * fn);
+        p.G = (int) n_waves;
+        const dim3 grid((unsigned) p.G), block(64);
+        const bool res = o.residual != nullptr;
+        if (fn == 2) {
+            if (res) { if (k256) gemm_small<2, true, true><<<grid, block, 0, s>>>(p); else gemm_small<2, true, false><<<grid, block, 0, s>>>(p); }
+            else     { if (k256) gemm_small<2, false, true><<<grid, block, 0, s>>>(p); else gemm_small<2, false, false><<<grid, block, 0, s>>>(p); }
+        } else {
+            if (res) { if (k256) gemm_small<4, true, true><<<grid, block, 0, s>>>(p); else gemm_small<4, true, false><<<grid, block, 0, s>>>(p); }
+            else     { if (k256) gemm_small<4, false, true><<<grid, block, 0, s>>>(p); else gemm_small<4, false, false><<<grid, block, 0, s>>>(p); }
+        }
+        return launch_check("gemm_small");
+    }
     // K256: persistent workgroups, two per CU (the LDS ring needs 68 KiB of the 160);
     // otherwise one workgroup per tile.
     const int n_wg = (k256 && NXG_WG_PER_CU > 0) ? (int) std::min<long long>(G, (long long) NXG_WG_PER_CU * device_cus())
