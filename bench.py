@@ -44,113 +44,11 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-class LinearPath:
-    """Every int8 projection of the encoder over M packed rows, on device buffers."""
-
-    def __init__(self, nxg, M: int, fuse: bool = True, weights=None, seed: int = 0, fuse_mlp: bool = True):
-        import torch
-        import nexterabert_cpp_amd.model as model
-        self.nxg, self.torch, self.M = nxg, torch, M
-        rng = np.random.default_rng(seed)
-        gen = torch.Generator(device="cuda").manual_seed(seed)
-        self.layers = []
-        self.host_weights = {}
-        self.dev_weights = {} if weights is None else weights
-        self.inputs, self.qacts, self.outs = {}, {}, {}
-        rows_block = (M + model.HRA_BLOCK - 1) // model.HRA_BLOCK
-        self.residual = torch.randn(M, model.N_EMBD, device="cuda", generator=gen)
-        self.ops = 0
-        self.gemm_bytes = 0       # fp32-output GEMMs
-        self.relu2_bytes = 0      # c_fc -> relu^2 -> int8 GEMMs
-        self.quant_bytes = 0
-        self.ops_fp32 = self.ops_relu2 = 0
-        for l, kind in enumerate(model.BLOCK_TYPES):
-            steps = []
-            seen = set()
-            made = set()          # qact keys produced by a GEMM of this layer (relu^2 -> int8)
-            for g in model.layer_groups(l, kind, fuse):
-                rows = rows_block if g.block_rows else M
-                key = (g.input, g.n_in, rows)
-                if key not in self.qacts:
-                    self.qacts[key] = nxg.qact_alloc(rows, g.n_in)
-                if key not in made and key not in self.inputs:
-                    self.inputs[key] = torch.randn(rows, g.n_in, device="cuda", generator=gen)
-                okey = (g.n_out, rows)
-                if okey not in self.outs:
-                    self.outs[okey] = torch.empty(rows, g.n_out, device="cuda")
-                gkind = "fp32"
-                if g.relu2_into:
-                    # c_fc: its output only feeds relu^2 into the next linear's qact
-                    gkind = "relu2" if fuse_mlp else "relu2_unfused"
-                    rkey = (g.relu2_into, g.n_out, rows)
-                    if rkey not in self.qacts:
-                        self.qacts[rkey] = nxg.qact_alloc(rows, g.n_out)
-                    made.add(rkey)
-                    okey = rkey if fuse_mlp else okey
-                wname = g.name if len(g.specs) == 1 else f"blocks.{l}.{g.name}"
-                if wname not in self.dev_weights:
-                    parts = []
-                    for s in g.specs:
-                        rows_f = (0.02 * rng.standard_normal((s.n_out, s.n_in))).astype(np.float32)
-                        data = nxg.quantize_weight(nxg.TYPE_Q8_0, rows_f)
-                        parts.append(nxg.expand_weight(nxg.TYPE_Q8_0, data, s.n_in, s.n_out))
-                    W = nxg.I8Weight(np.concatenate([p.w for p in parts]),
-                                     np.ascontiguousarray(np.concatenate([p.scale for p in parts], 1)),
-                                     np.ascontiguousarray(np.concatenate([p.off for p in parts], 1)))
-                    self.host_weights[wname] = W
-                    self.dev_weights[wname] = nxg.DeviceWeight(W)
-                first = key not in seen and key not in made
-                seen.add(key)
-                res = g.residual
-                steps.append((key, first, wname, okey, res, g, gkind))
-                ops = 2 * rows * g.n_in * g.n_out
-                self.ops += ops
-                nb = (g.n_in + 255) // 256
-                nb_out = (g.n_out + 255) // 256
-                w_in = rows * g.n_in + 4 * rows * nb + g.n_out * g.n_in + 4 * g.n_out * nb
-                if gkind == "relu2":
-                    self.ops_relu2 += ops
-                    self.relu2_bytes += w_in + rows * g.n_out + 4 * rows * nb_out
-                else:
-                    self.ops_fp32 += ops
-                    self.gemm_bytes += w_in + 4 * rows * g.n_out * (2 if res else 1)
-                if gkind == "relu2_unfused":      # fp32 rows, then relu^2 + quantize_row
-                    self.quant_bytes += 5 * rows * g.n_out + 4 * rows * nb_out
-                if first:
-                    self.quant_bytes += 5 * rows * g.n_in + 4 * rows * nb
-            self.layers.append(steps)
-        self.n_gemm = sum(len(s) for s in self.layers)
-        self.n_relu2 = sum(1 for s in self.layers for st in s if st[6] == "relu2")
-        self.n_quant = sum(1 for s in self.layers for st in s if st[1] or st[6] == "relu2_unfused")
-
-    def _timed(self, events, fn, *tag):
-        if events is None:
-            fn()
-            return
-        torch = self.torch
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        fn()
-        e1.record()
-        events.append((e0, e1) + tag)
-
-    def step(self, gemm_events=None, quant_events=None):
-        nxg = self.nxg
-        for steps in self.layers:
-            for key, first, wname, okey, res, g, gkind in steps:
-                qa = self.qacts[key]
-                w = self.dev_weights[wname]
-                if first:
-                    self._timed(quant_events, lambda: nxg.quantize_rows(self.inputs[key], out=qa))
-                if gkind == "relu2":
-                    self._timed(gemm_events, lambda: nxg.linear_i8_relu2_q8(w, qa, out=self.qacts[okey]), g, gkind)
-                    continue
-                self._timed(gemm_events, lambda: nxg.linear_i8(w, qa, residual=self.residual if res else None,
-                                                               out=self.outs[okey]), g, gkind)
-                if gkind == "relu2_unfused":
-                    rkey = (g.relu2_into, g.n_out, qa.T)
-                    self._timed(quant_events, lambda: nxg.quantize_rows_relu2(self.outs[okey], out=self.qacts[rkey]))
+def LinearPath(nxg, M: int, **kw):
+    """The encoder's int8 linear path over one sequence of M rows (the package's
+    EncoderLinearPath)."""
+    from nexterabert_cpp_amd.encoder import EncoderLinearPath
+    return EncoderLinearPath(nxg, [M], **kw)
 
 
 def time_steps(path, steps: int, warmup: int):
@@ -294,9 +192,9 @@ def pmc_summary(fetch_csv: str, write_csv: str, calib_mib: int, out_path: Path) 
             if row["Counter_Name"] != counter:
                 continue
             name, v = row["Kernel_Name"], float(row["Counter_Value"])
-            if "gemm_relu2_q8" in name:
+            if "gemm_relu2_q8" in name or "gemm_relu2_small" in name:
                 vals["gemm_relu2"].append(v)
-            elif "gemm_k256" in name or "gemm_kernel" in name:
+            elif "gemm_k256" in name or "gemm_kernel" in name or "gemm_small" in name:
                 vals["gemm_fp32"].append(v)
             elif "quantize_kernel" in name:
                 vals["quant"].append(v)

@@ -1,0 +1,165 @@
+"""The encoder's int8 linear path over one packed batch, on one GPU.
+
+Every int8 projection of the 18 layers, in the order the reference's graph builder
+emits them (src/nexterabert.cpp:1185-1289). Per layer each distinct activation a linear
+reads is quantized once (builder::linear's qcache, :1121-1143); projections that read the
+same activation run as one GEMM over their weights concatenated along N (exact per output
+column); the MLP's c_fc writes c_proj's int8 activations through the fused relu^2
+epilogue (op_relu_sqr feeding an int8 linear, :484-505, :1284-1289). HRA q/k/v run on
+each sequence's ceil(len / 4) block rows. Rows are the packed batch: every GEMM gets the
+batch's cumulative offsets (prepare_batch, :1341-1354).
+
+The producers of the activations (norms, attention, convolutions, the SnowLily state,
+block means) are not on this path: their outputs are synthetic fp32 rows, N(0, 1), made
+on the GPU once. Weights are random N(0, 0.02) encoded as Q8_0, or read from a GGUF
+file; either way they are expanded on the host as build_i8_weight does (:1010-1049) and
+uploaded once.
+"""
+from __future__ import annotations
+
+from typing import Dict, List, Optional, Sequence
+
+import numpy as np
+
+from . import model
+
+
+class EncoderLinearPath:
+    """Device buffers and the launch sequence of one forward of the linear path.
+
+    lengths   sequence lengths of the packed batch (rows = their sum)
+    fuse      run linears that share an input as one GEMM
+    fuse_mlp  c_fc -> relu^2 -> int8 in one kernel (else fp32 rows, then
+              quantize_rows_relu2)
+    weights   device weights from an earlier path (same fuse setting), reused
+    gguf      an open nxg.GGUF holding the encoder's int8 tensors (else random weights)
+    """
+
+    def __init__(self, nxg, lengths: Sequence[int], fuse: bool = True, weights=None, seed: int = 0,
+                 fuse_mlp: bool = True, gguf=None):
+        import torch
+        lengths = [int(n) for n in lengths]
+        if not lengths or min(lengths) <= 0:
+            raise ValueError("lengths: need at least one sequence, each of at least one token")
+        self.nxg, self.torch = nxg, torch
+        self.lengths = lengths
+        self.M = sum(lengths)
+        block_lengths = [(n + model.HRA_BLOCK - 1) // model.HRA_BLOCK for n in lengths]
+        rows_block = sum(block_lengths)
+        single = len(lengths) == 1
+        self.cu = None if single else nxg.cu_offsets_of(lengths)
+        self.cu_block = None if single else nxg.cu_offsets_of(block_lengths)
+        rng = np.random.default_rng(seed)
+        gen = torch.Generator(device="cuda").manual_seed(seed)
+        types = {t.name: t for t in gguf.tensors()} if gguf is not None else {}
+        self.layers = []
+        self.host_weights: Dict[str, object] = {}
+        self.dev_weights = {} if weights is None else weights
+        self.inputs, self.qacts, self.outs = {}, {}, {}
+        self.residual = torch.randn(self.M, model.N_EMBD, device="cuda", generator=gen)
+        self.ops = 0
+        self.ops_fp32 = self.ops_relu2 = 0
+        self.gemm_bytes = 0       # algorithmic HBM bytes of the fp32-output GEMMs
+        self.relu2_bytes = 0      # ... of the c_fc -> relu^2 -> int8 GEMMs
+        self.quant_bytes = 0      # ... of the standalone quantizations
+        M = self.M
+        for l, kind in enumerate(model.BLOCK_TYPES):
+            steps = []
+            seen = set()
+            made = set()          # qact keys produced by a GEMM of this layer (relu^2 -> int8)
+            for g in model.layer_groups(l, kind, fuse):
+                rows = rows_block if g.block_rows else M
+                key = (g.input, g.n_in, rows)
+                if key not in self.qacts:
+                    self.qacts[key] = nxg.qact_alloc(rows, g.n_in)
+                if key not in made and key not in self.inputs:
+                    self.inputs[key] = torch.randn(rows, g.n_in, device="cuda", generator=gen)
+                okey = (g.n_out, rows)
+                gkind = "fp32"
+                if g.relu2_into:
+                    # c_fc: its output only feeds relu^2 into the next linear's qact
+                    gkind = "relu2" if fuse_mlp else "relu2_unfused"
+                    rkey = (g.relu2_into, g.n_out, rows)
+                    if rkey not in self.qacts:
+                        self.qacts[rkey] = nxg.qact_alloc(rows, g.n_out)
+                    made.add(rkey)
+                    okey = rkey if fuse_mlp else okey
+                if gkind != "relu2" and okey not in self.outs:      # fp32 rows out
+                    self.outs[okey] = torch.empty(rows, g.n_out, device="cuda")
+                wname = g.name if len(g.specs) == 1 else f"blocks.{l}.{g.name}"
+                if wname not in self.dev_weights:
+                    parts = [self._expand(nxg, s, rng, gguf, types) for s in g.specs]
+                    W = parts[0] if len(parts) == 1 else nxg.I8Weight(
+                        np.concatenate([p.w for p in parts]),
+                        np.ascontiguousarray(np.concatenate([p.scale for p in parts], 1)),
+                        np.ascontiguousarray(np.concatenate([p.off for p in parts], 1)))
+                    self.host_weights[wname] = W
+                    self.dev_weights[wname] = nxg.DeviceWeight(W)
+                first = key not in seen and key not in made
+                seen.add(key)
+                res = g.residual
+                steps.append((key, first, wname, okey, res, g, gkind))
+                ops = 2 * rows * g.n_in * g.n_out
+                self.ops += ops
+                nb = (g.n_in + 255) // 256
+                nb_out = (g.n_out + 255) // 256
+                w_in = rows * g.n_in + 4 * rows * nb + g.n_out * g.n_in + 4 * g.n_out * nb
+                if gkind == "relu2":
+                    self.ops_relu2 += ops
+                    self.relu2_bytes += w_in + rows * g.n_out + 4 * rows * nb_out
+                else:
+                    self.ops_fp32 += ops
+                    self.gemm_bytes += w_in + 4 * rows * g.n_out * (2 if res else 1)
+                if gkind == "relu2_unfused":      # fp32 rows, then relu^2 + quantize_row
+                    self.quant_bytes += 5 * rows * g.n_out + 4 * rows * nb_out
+                if first:
+                    self.quant_bytes += 5 * rows * g.n_in + 4 * rows * nb
+            self.layers.append(steps)
+        self.n_gemm = sum(len(s) for s in self.layers)
+        self.n_relu2 = sum(1 for s in self.layers for st in s if st[6] == "relu2")
+        self.n_quant = sum(1 for s in self.layers for st in s if st[1] or st[6] == "relu2_unfused")
+
+    @staticmethod
+    def _expand(nxg, spec, rng, gguf, types):
+        if gguf is None:
+            rows_f = (0.02 * rng.standard_normal((spec.n_out, spec.n_in))).astype(np.float32)
+            return nxg.expand_weight(nxg.TYPE_Q8_0, nxg.quantize_weight(nxg.TYPE_Q8_0, rows_f), spec.n_in, spec.n_out)
+        info = types.get(spec.name)
+        if info is None:
+            raise KeyError(f"{spec.name}: not in the GGUF file")
+        if info.n_dims != 2 or tuple(info.ne[:2]) != (spec.n_in, spec.n_out):
+            raise ValueError(f"{spec.name}: ne {info.ne[:info.n_dims]} in the file, expected ({spec.n_in}, {spec.n_out})")
+        return nxg.expand_weight(info.type, gguf.tensor_bytes(spec.name), spec.n_in, spec.n_out)
+
+    def _timed(self, events, fn, *tag):
+        if events is None:
+            fn()
+            return
+        torch = self.torch
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        events.append((e0, e1) + tag)
+
+    def step(self, gemm_events: Optional[List] = None, quant_events: Optional[List] = None) -> None:
+        """One forward of the path on the current stream. With event lists, every GEMM
+        (tagged with its group and kind) and every quantization is bracketed by HIP events."""
+        nxg = self.nxg
+        for steps in self.layers:
+            for key, first, wname, okey, res, g, gkind in steps:
+                qa = self.qacts[key]
+                w = self.dev_weights[wname]
+                cu = self.cu_block if g.block_rows else self.cu
+                if first:
+                    self._timed(quant_events, lambda: nxg.quantize_rows(self.inputs[key], out=qa))
+                if gkind == "relu2":
+                    self._timed(gemm_events, lambda: nxg.linear_i8_relu2_q8(w, qa, cu_offsets=cu, out=self.qacts[okey]),
+                                g, gkind)
+                    continue
+                self._timed(gemm_events, lambda: nxg.linear_i8(w, qa, residual=self.residual if res else None,
+                                                               cu_offsets=cu, out=self.outs[okey]), g, gkind)
+                if gkind == "relu2_unfused":
+                    rkey = (g.relu2_into, g.n_out, qa.T)
+                    self._timed(quant_events, lambda: nxg.quantize_rows_relu2(self.outs[okey], out=self.qacts[rkey]))
