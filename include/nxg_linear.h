@@ -138,6 +138,47 @@ NXG_API int32_t nxg_quantize_rows_relu2(const float * x, int32_t T, int32_t n_in
 NXG_API int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps, int32_t T, int32_t n_in,
                                           int32_t act_max, int8_t * q, float * sx, void * stream);
 
+/* The mixers' producers with an int8 consumer: each computes its rows as the
+ * reference's AVX2 build does (n_in % 32 == 0, so its scalar tails never run) and
+ * quantizes them as nxg_quantize_rows (for_rows' quantize branch, :414-438). All
+ * arrays are device arrays, rows of n_in floats. Unlike nxg_linear_i8, the packed
+ * layout here is on the device: cu_offsets (and cu_blocks) hold n_seqs + 1 int32,
+ * strictly increasing from 0 (the reference's layout::start plus total, :231-244,
+ * :1341-1354); other offsets give unspecified rows but never an out-of-bounds access. */
+
+/* op_gate (src/nexterabert.cpp:507-522), the input of every gated mixer's c_proj
+ * (gated_out, :1208-1213): out = sigmoid(g) * y, sigmoid(g) = 1 / (1 + exp(0 - g))
+ * with exp as exp256 computes it (:81-100, :119-122). g, y: [T][n_in]. */
+NXG_API int32_t nxg_gate_quantize_rows(const float * g, const float * y, int32_t T, int32_t n_in, int32_t act_max,
+                                       int8_t * q, float * sx, void * stream);
+
+/* op_dwconv (src/nexterabert.cpp:524-543), SnowLily's input of ltc_conv.out_proj
+ * (:1233-1236): out[t] = r[t] (or 0 if r is null), then for j = 0 .. k-1 with
+ * t + j - k/2 inside t's document, out[t] = fma(taps[j], x[t + j - k/2], out[t]).
+ * x, r: [T][n_in]; taps: [k][n_in] (the layout conv_params hands over, :1152-1159). */
+NXG_API int32_t nxg_dwconv_quantize_rows(const float * x, const float * r, const float * taps, int32_t k,
+                                         const int32_t * cu_offsets, int32_t n_seqs, int32_t T, int32_t n_in,
+                                         int32_t act_max, int8_t * q, float * sx, void * stream);
+
+/* op_lily_state (src/nexterabert.cpp:545-578), the input of SnowLily's c_proj
+ * (:1239-1243): acc = 0, then for the taps j with t + j - k/2 inside t's document,
+ * acc = fma(taps[j], a[t+j-k/2] * x[t+j-k/2], acc); out[t] = acc * b[t].
+ * a, x, b: [T][n_in]; taps: [k][n_in]. */
+NXG_API int32_t nxg_lily_state_quantize_rows(const float * a, const float * x, const float * b, const float * taps,
+                                             int32_t k, const int32_t * cu_offsets, int32_t n_seqs, int32_t T,
+                                             int32_t n_in, int32_t act_max, int8_t * q, float * sx, void * stream);
+
+/* op_block_mean (src/nexterabert.cpp:638-659), the input of HRA's c_q / c_k / c_v
+ * (:1253-1256): block row b of document d is the mean of its (up to block) tokens,
+ * out = 0, out = fma(h, g, out) per token in order (out + h without g), then
+ * out * (1 / n). h, g (nullable): [T][n_in] tokens; cu_blocks: the block rows'
+ * layout, ceil(len_d / block) rows per document, n_blocks = cu_blocks[n_seqs];
+ * q, sx: a qact of n_blocks rows. */
+NXG_API int32_t nxg_block_mean_quantize_rows(const float * h, const float * g, const int32_t * cu_offsets,
+                                             const int32_t * cu_blocks, int32_t n_seqs, int32_t T, int32_t n_blocks,
+                                             int32_t block, int32_t n_in, int32_t act_max, int8_t * q, float * sx,
+                                             void * stream);
+
 /* The qact buffers in the reference's own format (src/nexterabert.cpp:368-375):
  *   u8  device uint8 [T][n_in], the reference's u8 values (q + act_max + 1)
  *   sx_ref device float, ((T+3)/4)*n_blk*4 floats, [token/4][block][token%4] */

@@ -71,6 +71,10 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_quantize_rows": ([P, i32, i32, i32, P, P, P], i32),
         "nxg_quantize_rows_relu2": ([P, i32, i32, i32, P, P, P], i32),
         "nxg_rmsnorm_quantize_rows": ([P, P, ctypes.c_float, i32, i32, i32, P, P, P], i32),
+        "nxg_gate_quantize_rows": ([P, P, i32, i32, i32, P, P, P], i32),
+        "nxg_dwconv_quantize_rows": ([P, P, P, i32, P, i32, i32, i32, i32, P, P, P], i32),
+        "nxg_lily_state_quantize_rows": ([P, P, P, P, i32, P, i32, i32, i32, i32, P, P, P], i32),
+        "nxg_block_mean_quantize_rows": ([P, P, P, P, i32, i32, i32, i32, i32, i32, P, P, P], i32),
         "nxg_qact_export": ([P, P, i32, i32, i32, P, P, P], i32),
         "nxg_weight_create": ([P, P, i32, i32, ctypes.POINTER(P)], i32),
         "nxg_weight_destroy": ([P], None),
@@ -301,6 +305,113 @@ def rmsnorm_quantize_rows(x, gain, eps: float, act_max: int = 127, out: Optional
     _check(load_library().nxg_rmsnorm_quantize_rows(x.data_ptr(), gain.data_ptr(), float(eps), T, n_in, act_max,
                                                      qa.q.data_ptr(), qa.sx.data_ptr(), _stream_ptr(stream)),
            "rmsnorm_quantize_rows")
+    return qa
+
+
+def _rows_arg(t, name, shape=None):
+    torch = _torch()
+    if t.dtype != torch.float32 or t.dim() != 2 or not t.is_cuda or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous 2-D float32 device tensor")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    return t
+
+
+def _device_offsets(cu_offsets, device):
+    """cu_offsets (host sequence or device int32 tensor) as a device int32 tensor."""
+    torch = _torch()
+    if isinstance(cu_offsets, torch.Tensor):
+        t = cu_offsets.to(device=device, dtype=torch.int32).contiguous()
+    else:
+        t = torch.tensor(np.ascontiguousarray(cu_offsets, dtype=np.int32), device=device)
+    if t.dim() != 1 or t.numel() < 2:
+        raise ValueError("cu_offsets: need n_seqs + 1 >= 2 offsets")
+    return t
+
+
+def _produce_out(T, n_in, act_max, out, device):
+    qa = out if out is not None else qact_alloc(T, n_in, act_max, device)
+    qa.T, qa.n_in, qa.act_max = T, n_in, act_max
+    return qa
+
+
+def gate_quantize_rows(g, y, act_max: int = 127, out: Optional[QAct] = None, stream=None) -> QAct:
+    """op_gate quantized for an int8 consumer: quantize_row of sigmoid(g) * y per row
+    (the reference's exp256-based sigmoid)."""
+    _rows_arg(g, "g")
+    T, n_in = g.shape
+    _rows_arg(y, "y", (T, n_in))
+    qa = _produce_out(T, n_in, act_max, out, g.device)
+    _check(load_library().nxg_gate_quantize_rows(g.data_ptr(), y.data_ptr(), T, n_in, act_max, qa.q.data_ptr(),
+                                                 qa.sx.data_ptr(), _stream_ptr(stream)), "gate_quantize_rows")
+    return qa
+
+
+def dwconv_quantize_rows(x, taps, cu_offsets, r=None, act_max: int = 127, out: Optional[QAct] = None,
+                         stream=None) -> QAct:
+    """op_dwconv quantized for an int8 consumer: r + the depthwise convolution of x with
+    taps [k][n_in] inside each document of the packed batch (cu_offsets)."""
+    _rows_arg(x, "x")
+    T, n_in = x.shape
+    _rows_arg(taps, "taps")
+    if taps.shape[1] != n_in:
+        raise ValueError(f"taps must be [k][{n_in}]")
+    if r is not None:
+        _rows_arg(r, "r", (T, n_in))
+    cu = _device_offsets(cu_offsets, x.device)
+    qa = _produce_out(T, n_in, act_max, out, x.device)
+    _check(load_library().nxg_dwconv_quantize_rows(x.data_ptr(), r.data_ptr() if r is not None else None,
+                                                   taps.data_ptr(), taps.shape[0], cu.data_ptr(), cu.numel() - 1,
+                                                   T, n_in, act_max, qa.q.data_ptr(), qa.sx.data_ptr(),
+                                                   _stream_ptr(stream)), "dwconv_quantize_rows")
+    return qa
+
+
+def lily_state_quantize_rows(a, x, b, taps, cu_offsets, act_max: int = 127, out: Optional[QAct] = None,
+                             stream=None) -> QAct:
+    """op_lily_state quantized for an int8 consumer: b * the depthwise convolution of a * x
+    with taps [k][n_in] inside each document (cu_offsets)."""
+    _rows_arg(x, "x")
+    T, n_in = x.shape
+    _rows_arg(a, "a", (T, n_in))
+    _rows_arg(b, "b", (T, n_in))
+    _rows_arg(taps, "taps")
+    if taps.shape[1] != n_in:
+        raise ValueError(f"taps must be [k][{n_in}]")
+    cu = _device_offsets(cu_offsets, x.device)
+    qa = _produce_out(T, n_in, act_max, out, x.device)
+    _check(load_library().nxg_lily_state_quantize_rows(a.data_ptr(), x.data_ptr(), b.data_ptr(), taps.data_ptr(),
+                                                       taps.shape[0], cu.data_ptr(), cu.numel() - 1, T, n_in,
+                                                       act_max, qa.q.data_ptr(), qa.sx.data_ptr(),
+                                                       _stream_ptr(stream)), "lily_state_quantize_rows")
+    return qa
+
+
+def block_offsets(cu_offsets: Sequence[int], block: int) -> np.ndarray:
+    """The block rows' layout of a packed batch: ceil(len_d / block) rows per document."""
+    cu = np.asarray(cu_offsets, dtype=np.int64)
+    return cu_offsets_of([(int(n) + block - 1) // block for n in np.diff(cu)])
+
+
+def block_mean_quantize_rows(h, cu_offsets: Sequence[int], block: int, g=None, act_max: int = 127,
+                             out: Optional[QAct] = None, stream=None) -> QAct:
+    """op_block_mean quantized for an int8 consumer: per document, the mean of each run of
+    `block` tokens of h (* g), one row per run. cu_offsets: host offsets of the tokens."""
+    _rows_arg(h, "h")
+    T, n_in = h.shape
+    if g is not None:
+        _rows_arg(g, "g", (T, n_in))
+    cu_host = np.ascontiguousarray(cu_offsets, dtype=np.int32)
+    if cu_host.size < 2 or int(cu_host[-1]) != T:
+        raise ValueError(f"cu_offsets must end at T={T}")
+    cub_host = block_offsets(cu_host, block)
+    n_blocks = int(cub_host[-1])
+    cu, cub = _device_offsets(cu_host, h.device), _device_offsets(cub_host, h.device)
+    qa = _produce_out(n_blocks, n_in, act_max, out, h.device)
+    _check(load_library().nxg_block_mean_quantize_rows(h.data_ptr(), g.data_ptr() if g is not None else None,
+                                                       cu.data_ptr(), cub.data_ptr(), cu.numel() - 1, T, n_blocks,
+                                                       block, n_in, act_max, qa.q.data_ptr(), qa.sx.data_ptr(),
+                                                       _stream_ptr(stream)), "block_mean_quantize_rows")
     return qa
 
 

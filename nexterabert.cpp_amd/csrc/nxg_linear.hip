@@ -103,21 +103,64 @@ __device__ __forceinline__ int quant1(float x, float inv) {
     return u - (ACT_MAX + 1);
 }
 
-// Row transforms applied before quantize_row: none (op_copy and producers that hand over
-// f32 rows), relu^2 (op_relu_sqr, src/nexterabert.cpp:484-505: x > 0 ? x : 0, a NaN
-// giving 0, then r * r) and RMSNorm (op_rms_norm, :463-482: (x * inv) * gain).
-enum qmode { Q_PLAIN = 0, Q_RELU2 = 1, Q_RMSNORM = 2 };
+// Row sources of quantize_row: what a producer hands to for_rows' quantize branch
+// (src/nexterabert.cpp:414-438). A source has a per-row state row(t) (computed once per
+// row and lane) and load(rs, t, col, v): the 4 f32 values of row t at inputs col..col+3
+// (t < T, col + 3 < n_in), computed with the producer's own operations in its order.
+
+struct no_row {};
+
+// op_copy (:453-461) and any f32 rows handed over as they are.
+struct src_rows {
+    const float * x;
+    int n;
+    __device__ no_row row(int) const { return {}; }
+    __device__ void load(no_row, int t, int col, float (&v)[4]) const {
+        const v4f f = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(x + (size_t) t * n + col));
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+    }
+};
+
+// op_relu_sqr (:484-505): r = x > 0 ? x : 0 (MAXPS with zero second: a NaN gives 0), r * r.
+struct src_relu2 {
+    src_rows in;
+    __device__ no_row row(int) const { return {}; }
+    __device__ void load(no_row, int t, int col, float (&v)[4]) const {
+        in.load({}, t, col, v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float r = v[e] > 0.0f ? v[e] : 0.0f;
+            v[e] = r * r;
+        }
+    }
+};
+
+// op_rms_norm (:463-482) once the row's inv = 1 / sqrt(mean(x^2) + eps) is known:
+// (x * inv) * gain.
+struct src_rms {
+    src_rows in;
+    const float * gain;
+    float inv;
+    __device__ no_row row(int) const { return {}; }
+    __device__ void load(no_row, int t, int col, float (&v)[4]) const {
+        in.load({}, t, col, v);
+        const v4f gv = *reinterpret_cast<const v4f *>(gain + col);
+        const float gr[4] = { gv.x, gv.y, gv.z, gv.w };
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (v[e] * inv) * gr[e];
+    }
+};
 
 // quantize_row of one (16-row group g, 256-input block B) by a workgroup of 4 waves.
 // Wave w quantizes rows 4w..4w+3; the 16 lanes of a row read its 256 inputs as 4
 // contiguous 256-byte pieces, so lane c holds inputs 64i + 4c + e (i, e = 0..3). The
 // int8 results are gathered in LDS in fragment order and each wave stores one 1 KiB
-// fragment. Q_RMSNORM: inv is the row's 1/sqrt(mean(x^2) + eps). Ends with the stage
-// buffer still being read by the stores: callers looping over blocks sync before reuse.
-template <int ACT_MAX, int MODE>
-__device__ __forceinline__ void quantize_block(const float * __restrict__ x, int T, int n_in, int KS, int n_blk,
+// fragment. Ends with the stage buffer still being read by the stores: callers looping
+// over blocks sync before reuse.
+template <int ACT_MAX, typename Src>
+__device__ __forceinline__ void quantize_block(const Src & src, int T, int n_in, int KS, int n_blk,
                                                int8_t * __restrict__ q, float * __restrict__ sx, int g, int B,
-                                               int * stage, float inv_row, const float * __restrict__ gain) {
+                                               int * stage) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rl = wave * 4 + (lane >> 4);     // row within the 16-row group
     const int t = g * 16 + rl;
@@ -126,24 +169,12 @@ __device__ __forceinline__ void quantize_block(const float * __restrict__ x, int
 
     float xv[4][4];                            // [i][e]: input kb + 64i + 4c + e
     bool present[4];
+    const auto rs = src.row(min(t, T - 1));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         present[i] = t < T && kb + 64 * i + 4 * c < n_in;
         if (present[i]) {
-            const v4f f = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(x + (size_t) t * n_in + kb + 64 * i + 4 * c));
-            xv[i][0] = f.x; xv[i][1] = f.y; xv[i][2] = f.z; xv[i][3] = f.w;
-            if (MODE == Q_RELU2) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float r = xv[i][e] > 0.0f ? xv[i][e] : 0.0f;
-                    xv[i][e] = r * r;
-                }
-            } else if (MODE == Q_RMSNORM) {
-                const v4f gv = *reinterpret_cast<const v4f *>(gain + kb + 64 * i + 4 * c);
-                const float gr[4] = { gv.x, gv.y, gv.z, gv.w };
-#pragma unroll
-                for (int e = 0; e < 4; ++e) xv[i][e] = (xv[i][e] * inv_row) * gr[e];
-            }
+            src.load(rs, t, kb + 64 * i + 4 * c, xv[i]);
         } else {
             xv[i][0] = xv[i][1] = xv[i][2] = xv[i][3] = 0.0f;
         }
@@ -233,12 +264,15 @@ __device__ __forceinline__ void quantize_block(const float * __restrict__ x, int
 
 // One workgroup per (16-row group, 256-input block), the block index fastest, so that
 // consecutive workgroups read consecutive 1 KiB pieces of the same rows.
+enum qmode { Q_PLAIN = 0, Q_RELU2 = 1 };
 template <int ACT_MAX, int MODE>
 __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict__ x, int T, int n_in, int KS,
                                                        int n_blk, int8_t * __restrict__ q, float * __restrict__ sx) {
     __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
     const int g = (int) (blockIdx.x / (unsigned) n_blk), B = (int) (blockIdx.x % (unsigned) n_blk);
-    quantize_block<ACT_MAX, MODE>(x, T, n_in, KS, n_blk, q, sx, g, B, stage, 1.0f, nullptr);
+    const src_rows in{x, n_in};
+    if (MODE == Q_RELU2) quantize_block<ACT_MAX>(src_relu2{in}, T, n_in, KS, n_blk, q, sx, g, B, stage);
+    else                 quantize_block<ACT_MAX>(in, T, n_in, KS, n_blk, q, sx, g, B, stage);
 }
 
 // op_rms_norm feeding an int8 linear (src/nexterabert.cpp:463-482 through for_rows'
@@ -281,9 +315,186 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(const float * __r
     const float dot = a0 + a1;
     const float inv = 1.0f / __builtin_sqrtf(dot / (float) n_in + eps);
     for (int B = 0; B < n_blk; ++B) {
-        quantize_block<ACT_MAX, Q_RMSNORM>(x, T, n_in, KS, n_blk, q, sx, g, B, stage, inv, gain);
+        quantize_block<ACT_MAX>(src_rms{src_rows{x, n_in}, gain, inv}, T, n_in, KS, n_blk, q, sx, g, B, stage);
         __syncthreads();                       // the stores have read the stage buffer
     }
+}
+
+// ---------------------------------------------------------------------------
+// Mixer producers quantizing for an int8 consumer (row_op(..., int8_only(...)))
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float minps1(float a, float b) { return a < b ? a : b; }
+
+// exp(x) as the reference's exp256 computes it (src/nexterabert.cpp:81-100), lane by
+// lane: clamp to [-87.3, 88.3762626647949] with MINPS/MAXPS semantics (a NaN becomes the
+// upper bound); n = x * log2(e) rounded to the nearest integer (ties to even); the
+// argument reduced in two fused steps, r = x - n * 0.693359375 - n * (-2.12194440e-4);
+// the degree-5 Cephes polynomial in r by fused Horner steps, completed as p * r^2 + (r + 1);
+// scaled by 2^n built in the exponent field ((n + 127) << 23).
+__device__ __forceinline__ float exp_cephes(float x) {
+    constexpr float P[6] = { 1.9875691500e-4f, 1.3981999507e-3f, 8.3334519073e-3f,
+                             4.1665795894e-2f, 1.6666665459e-1f, 5.0000001201e-1f };
+    x = minps1(x, 88.3762626647949f);
+    x = maxps1(x, -87.3f);
+    const float n = __builtin_rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(-n, 0.693359375f, x);
+    r = __builtin_fmaf(-n, -2.12194440e-4f, r);
+    const float r2 = r * r;
+    float p = P[0];
+#pragma unroll
+    for (int i = 1; i < 6; ++i) p = __builtin_fmaf(p, r, P[i]);
+    p = __builtin_fmaf(p, r2, r + 1.0f);
+    const uint32_t e = (uint32_t) ((int) n + 127) << 23;
+    return p * __uint_as_float(e);
+}
+
+// op_gate (src/nexterabert.cpp:507-522, AVX2 path; C % 8 == 0): sigmoid(g) * y with
+// sigmoid(g) = 1 / (1 + exp(0 - g)), the division correctly rounded.
+struct src_gate {
+    const float * g;
+    const float * y;
+    int C;
+    __device__ no_row row(int) const { return {}; }
+    __device__ void load(no_row, int t, int col, float (&v)[4]) const {
+        const size_t o = (size_t) t * C + col;
+        const v4f gv = *reinterpret_cast<const v4f *>(g + o);
+        const v4f yv = *reinterpret_cast<const v4f *>(y + o);
+        const float gr[4] = { gv.x, gv.y, gv.z, gv.w }, yr[4] = { yv.x, yv.y, yv.z, yv.w };
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (1.0f / (1.0f + exp_cephes(0.0f - gr[e]))) * yr[e];
+    }
+};
+
+// The document of row t in a packed layout given by its cumulative offsets cu[0..n]
+// (device): the largest d with cu[d] <= t, and its rows [lo, hi) clamped to [0, T)
+// so that any offsets give in-bounds rows.
+struct doc_rows {
+    int lo, hi, d;
+};
+__device__ __forceinline__ doc_rows doc_of(const int32_t * cu, int n, int t, int T) {
+    int a = 0, b = n - 1;                      // search d in [0, n)
+    while (a < b) {
+        const int m = (a + b + 1) >> 1;
+        if (cu[m] <= t) a = m; else b = m - 1;
+    }
+    doc_rows r;
+    r.d = a;
+    r.lo = min(max(cu[a], 0), T);
+    r.hi = min(max(cu[a + 1], r.lo), T);
+    return r;
+}
+
+// op_dwconv (src/nexterabert.cpp:524-543): out = r (or 0), then for every tap j whose
+// row t + j - k/2 lies in t's document, out = fma(taps[j], x[t + j - k/2], out) in order
+// of j (addmul_f32, :166-176). taps [k][C].
+struct src_dwconv {
+    const float * x;
+    const float * r;                           // may be null
+    const float * taps;
+    const int32_t * cu;
+    int n_seqs, T, C, k;
+    __device__ doc_rows row(int t) const { return doc_of(cu, n_seqs, t, T); }
+    __device__ void load(const doc_rows & dr, int t, int col, float (&v)[4]) const {
+        if (r) {
+            const v4f rv = *reinterpret_cast<const v4f *>(r + (size_t) t * C + col);
+            v[0] = rv.x; v[1] = rv.y; v[2] = rv.z; v[3] = rv.w;
+        } else {
+            v[0] = v[1] = v[2] = v[3] = 0.0f;
+        }
+        for (int j = 0; j < k; ++j) {
+            const int tt = t + j - k / 2;
+            if (tt < dr.lo || tt >= dr.hi) continue;
+            const v4f w = *reinterpret_cast<const v4f *>(taps + (size_t) j * C + col);
+            const v4f xv = *reinterpret_cast<const v4f *>(x + (size_t) tt * C + col);
+            v[0] = __builtin_fmaf(w.x, xv.x, v[0]);
+            v[1] = __builtin_fmaf(w.y, xv.y, v[1]);
+            v[2] = __builtin_fmaf(w.z, xv.z, v[2]);
+            v[3] = __builtin_fmaf(w.w, xv.w, v[3]);
+        }
+    }
+};
+
+// op_lily_state (src/nexterabert.cpp:545-578, AVX2 path): acc = 0; for the taps j whose
+// row t + j - k/2 lies in t's document, acc = fma(taps[j], a[tt] * x[tt], acc); out =
+// acc * b[t].
+struct src_lily_state {
+    const float * a;
+    const float * x;
+    const float * b;
+    const float * taps;
+    const int32_t * cu;
+    int n_seqs, T, C, k;
+    __device__ doc_rows row(int t) const { return doc_of(cu, n_seqs, t, T); }
+    __device__ void load(const doc_rows & dr, int t, int col, float (&v)[4]) const {
+        const int j0 = max(0, dr.lo - (t - k / 2)), j1 = min(k, dr.hi - (t - k / 2));
+        float acc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+        for (int j = j0; j < j1; ++j) {
+            const size_t o = (size_t) (t + j - k / 2) * C + col;
+            const v4f w = *reinterpret_cast<const v4f *>(taps + (size_t) j * C + col);
+            const v4f av = *reinterpret_cast<const v4f *>(a + o);
+            const v4f xv = *reinterpret_cast<const v4f *>(x + o);
+            acc[0] = __builtin_fmaf(w.x, av.x * xv.x, acc[0]);
+            acc[1] = __builtin_fmaf(w.y, av.y * xv.y, acc[1]);
+            acc[2] = __builtin_fmaf(w.z, av.z * xv.z, acc[2]);
+            acc[3] = __builtin_fmaf(w.w, av.w * xv.w, acc[3]);
+        }
+        const v4f bv = *reinterpret_cast<const v4f *>(b + (size_t) t * C + col);
+        v[0] = acc[0] * bv.x; v[1] = acc[1] * bv.y; v[2] = acc[2] * bv.z; v[3] = acc[3] * bv.w;
+    }
+};
+
+// op_block_mean (src/nexterabert.cpp:638-659): block row b of document d covers tokens
+// ts .. ts + n - 1 (ts = cu[d] + block * (b - cub[d]), n = min(block, len_d - that));
+// out = 0, then out = fma(h, g, out) per token in order (addmul_f32; with no g,
+// axpy_f32 with weight 1: out + h), then out * (1 / n).
+struct block_rows {
+    int ts, n;
+    float inv;
+};
+struct src_block_mean {
+    const float * h;
+    const float * g;                           // may be null
+    const int32_t * cu;                        // token offsets, n_seqs + 1
+    const int32_t * cub;                       // block-row offsets, n_seqs + 1
+    int n_seqs, T_tok, n_rows, C, block;
+    __device__ block_rows row(int b) const {
+        const doc_rows d = doc_of(cub, n_seqs, b, n_rows);
+        const int tok_lo = min(max(cu[d.d], 0), T_tok), tok_hi = min(max(cu[d.d + 1], tok_lo), T_tok);
+        block_rows r;
+        r.ts = min(max(tok_lo + block * (b - d.lo), tok_lo), tok_hi);
+        r.n = max(0, min(block, tok_hi - r.ts));
+        r.inv = 1.0f / (float) r.n;
+        return r;
+    }
+    __device__ void load(const block_rows & br, int, int col, float (&v)[4]) const {
+        v[0] = v[1] = v[2] = v[3] = 0.0f;
+        for (int i = 0; i < br.n; ++i) {
+            const size_t o = (size_t) (br.ts + i) * C + col;
+            const v4f hv = *reinterpret_cast<const v4f *>(h + o);
+            if (g) {
+                const v4f gv = *reinterpret_cast<const v4f *>(g + o);
+                v[0] = __builtin_fmaf(hv.x, gv.x, v[0]);
+                v[1] = __builtin_fmaf(hv.y, gv.y, v[1]);
+                v[2] = __builtin_fmaf(hv.z, gv.z, v[2]);
+                v[3] = __builtin_fmaf(hv.w, gv.w, v[3]);
+            } else {
+                v[0] = v[0] + hv.x; v[1] = v[1] + hv.y; v[2] = v[2] + hv.z; v[3] = v[3] + hv.w;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v[e] * br.inv;
+    }
+};
+
+// quantize_row over the rows a source produces: one workgroup per (16-row group,
+// 256-input block), as quantize_kernel.
+template <int ACT_MAX, typename Src>
+__global__ __launch_bounds__(256) void produce_quantize_kernel(Src src, int T, int n_in, int KS, int n_blk,
+                                                               int8_t * __restrict__ q, float * __restrict__ sx) {
+    __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
+    const int g = (int) (blockIdx.x / (unsigned) n_blk), B = (int) (blockIdx.x % (unsigned) n_blk);
+    quantize_block<ACT_MAX>(src, T, n_in, KS, n_blk, q, sx, g, B, stage);
 }
 
 // int8 tiles -> the reference's u8 rows (q + act_off); one thread per 16 bytes.
@@ -1453,6 +1664,26 @@ struct nxg_weight {
     size_t   bytes = 0;
 };
 
+// A producer's rows quantized for an int8 consumer: shared checks and launch.
+template <typename Src>
+static int32_t launch_produce(const char * what, const Src & src, int32_t T, int32_t n_in, int32_t act_max,
+                              int8_t * q, float * sx, void * stream) {
+    qact_dims d;
+    if (!qact_dims_of(T, n_in, d)) return fail(NXG_EINVAL, "%s: T=%d n_in=%d (n_in must be a positive multiple of 32)", what, T, n_in);
+    if (act_max != 127 && act_max != 63) return fail(NXG_EINVAL, "%s: act_max must be 127 or 63, got %d", what, act_max);
+    if (T == 0) return NXG_OK;
+    if (!q || !sx) return fail(NXG_EINVAL, "%s: null output", what);
+    int rc = check_device();
+    if (rc) return rc;
+    const long long n_wg = (long long) (d.MP / 16) * d.n_blk;
+    if (n_wg > INT32_MAX) return fail(NXG_EINVAL, "%s: T=%d n_in=%d too large", what, T, n_in);
+    const dim3 grid((unsigned) n_wg);
+    hipStream_t s = (hipStream_t) stream;
+    if (act_max == 127) produce_quantize_kernel<127, Src><<<grid, 256, 0, s>>>(src, T, n_in, d.KS, d.n_blk, q, sx);
+    else                produce_quantize_kernel<63, Src><<<grid, 256, 0, s>>>(src, T, n_in, d.KS, d.n_blk, q, sx);
+    return launch_check(what);
+}
+
 extern "C" {
 
 int32_t nxg_init(void) { return check_device(); }
@@ -1514,6 +1745,42 @@ int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps
     if (act_max == 127) rmsnorm_quantize_kernel<127><<<grid, 256, 0, s>>>(x, gain, eps, T, n_in, d.KS, d.n_blk, q, sx);
     else                rmsnorm_quantize_kernel<63><<<grid, 256, 0, s>>>(x, gain, eps, T, n_in, d.KS, d.n_blk, q, sx);
     return launch_check("rmsnorm_quantize_kernel");
+}
+
+int32_t nxg_gate_quantize_rows(const float * g, const float * y, int32_t T, int32_t n_in, int32_t act_max,
+                               int8_t * q, float * sx, void * stream) {
+    if (T > 0 && (!g || !y)) return fail(NXG_EINVAL, "gate_quantize: null input");
+    return launch_produce("gate_quantize", src_gate{g, y, n_in}, T, n_in, act_max, q, sx, stream);
+}
+
+int32_t nxg_dwconv_quantize_rows(const float * x, const float * r, const float * taps, int32_t k,
+                                 const int32_t * cu_offsets, int32_t n_seqs, int32_t T, int32_t n_in,
+                                 int32_t act_max, int8_t * q, float * sx, void * stream) {
+    if (T > 0 && (!x || !taps || !cu_offsets)) return fail(NXG_EINVAL, "dwconv_quantize: null input");
+    if (k < 1 || n_seqs < 1) return fail(NXG_EINVAL, "dwconv_quantize: k=%d n_seqs=%d (both must be >= 1)", k, n_seqs);
+    return launch_produce("dwconv_quantize", src_dwconv{x, r, taps, cu_offsets, n_seqs, T, n_in, k},
+                          T, n_in, act_max, q, sx, stream);
+}
+
+int32_t nxg_lily_state_quantize_rows(const float * a, const float * x, const float * b, const float * taps, int32_t k,
+                                     const int32_t * cu_offsets, int32_t n_seqs, int32_t T, int32_t n_in,
+                                     int32_t act_max, int8_t * q, float * sx, void * stream) {
+    if (T > 0 && (!a || !x || !b || !taps || !cu_offsets)) return fail(NXG_EINVAL, "lily_state_quantize: null input");
+    if (k < 1 || n_seqs < 1) return fail(NXG_EINVAL, "lily_state_quantize: k=%d n_seqs=%d (both must be >= 1)", k, n_seqs);
+    return launch_produce("lily_state_quantize", src_lily_state{a, x, b, taps, cu_offsets, n_seqs, T, n_in, k},
+                          T, n_in, act_max, q, sx, stream);
+}
+
+int32_t nxg_block_mean_quantize_rows(const float * h, const float * g, const int32_t * cu_offsets,
+                                     const int32_t * cu_blocks, int32_t n_seqs, int32_t T, int32_t n_blocks,
+                                     int32_t block, int32_t n_in, int32_t act_max, int8_t * q, float * sx,
+                                     void * stream) {
+    if (n_blocks > 0 && (!h || !cu_offsets || !cu_blocks)) return fail(NXG_EINVAL, "block_mean_quantize: null input");
+    if (block < 1 || n_seqs < 1 || T < 0) {
+        return fail(NXG_EINVAL, "block_mean_quantize: block=%d n_seqs=%d T=%d (block, n_seqs >= 1)", block, n_seqs, T);
+    }
+    return launch_produce("block_mean_quantize", src_block_mean{h, g, cu_offsets, cu_blocks, n_seqs, T, n_blocks, n_in, block},
+                          n_blocks, n_in, act_max, q, sx, stream);
 }
 
 int32_t nxg_qact_export(const int8_t * q, const float * sx, int32_t T, int32_t n_in, int32_t act_max,

@@ -25,6 +25,11 @@
 //
 // ACT_MAX is 127 on VNNI builds of the reference and 63 on AVX2-only builds
 // (src/nexterabert.cpp:53-70); every function takes it as an argument.
+//
+// The producers that hand rows to quantize_row are restated too (their AVX2 paths, the
+// ones every row of 32k inputs takes): relu^2 (in oracle.py), op_rms_norm with dot_f32's
+// accumulation order, exp256 / op_gate (with an AVX2 + FMA version of exp256 to check the
+// scalar statement against), op_dwconv, op_lily_state and op_block_mean.
 
 #include <algorithm>
 #include <atomic>
@@ -260,6 +265,107 @@ void orc_rms_norm_rows(const float * x, const float * gain, float eps, int T, in
     }
 }
 
+// exp256 (src/nexterabert.cpp:81-100) for one lane: clamp with MINPS/MAXPS semantics
+// (the second operand when either is NaN, so a NaN becomes the upper bound), n = x * log2 e
+// rounded to an integer with ties to even (ROUNDPS, nearest), r = x - n c1 - n c2 as two
+// fused steps (FNMADD), the degree-5 polynomial by fused Horner steps, p r^2 + (r + 1)
+// fused, times 2^n assembled in the exponent field (CVTPS2DQ, + 127, << 23).
+static const float EXP_P[6] = { 1.9875691500e-4f, 1.3981999507e-3f, 8.3334519073e-3f,
+                                4.1665795894e-2f, 1.6666665459e-1f, 5.0000001201e-1f };
+
+float orc_exp_cephes(float x) {
+    x = x < 88.3762626647949f ? x : 88.3762626647949f;
+    x = x > -87.3f ? x : -87.3f;
+    const float n = std::nearbyint(x * 1.44269504088896341f);
+    float r = std::fma(-n, 0.693359375f, x);
+    r = std::fma(-n, -2.12194440e-4f, r);
+    const float r2 = r * r;
+    float p = EXP_P[0];
+    for (int i = 1; i < 6; ++i) p = std::fma(p, r, EXP_P[i]);
+    p = std::fma(p, r2, r + 1.0f);
+    const uint32_t bits = (uint32_t) ((int32_t) n + 127) << 23;
+    float scale;
+    std::memcpy(&scale, &bits, 4);
+    return p * scale;
+}
+
+void orc_exp_cephes_rows(const float * x, int64_t n, float * out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_exp_cephes(x[i]);
+}
+
+// op_gate's row (src/nexterabert.cpp:507-522, AVX2 path): sigmoid(g) * y with
+// sigmoid256 (:119-122) = 1 / (1 + exp256(0 - g)).
+void orc_gate_rows(const float * g, const float * y, int T, int C, float * out) {
+    for (size_t i = 0; i < (size_t) T * C; ++i) out[i] = (1.0f / (1.0f + orc_exp_cephes(0.0f - g[i]))) * y[i];
+}
+
+// op_dwconv (src/nexterabert.cpp:524-543) over a packed batch: out = r (or 0), then
+// out = fma(taps[j], x[t + j - k/2], out) for j ascending, skipping rows outside t's
+// document. taps [k][C], cu: n_seqs + 1 offsets.
+void orc_dwconv_rows(const float * x, const float * r, const float * taps, int k, const int32_t * cu, int n_seqs,
+                     int C, float * out) {
+    for (int d = 0; d < n_seqs; ++d) {
+        const int lo = cu[d], hi = cu[d + 1];
+        for (int t = lo; t < hi; ++t) {
+            float * o = out + (size_t) t * C;
+            for (int i = 0; i < C; ++i) o[i] = r ? r[(size_t) t * C + i] : 0.0f;
+            for (int j = 0; j < k; ++j) {
+                const int tt = t + j - k / 2;
+                if (tt < lo || tt >= hi) continue;
+                for (int i = 0; i < C; ++i) o[i] = std::fma(taps[(size_t) j * C + i], x[(size_t) tt * C + i], o[i]);
+            }
+        }
+    }
+}
+
+// op_lily_state (src/nexterabert.cpp:545-578, AVX2 path): acc = 0, acc = fma(taps[j],
+// a[tt] * x[tt], acc) for the taps j whose row tt = t + j - k/2 is in t's document,
+// out = acc * b[t].
+void orc_lily_state_rows(const float * a, const float * x, const float * b, const float * taps, int k,
+                         const int32_t * cu, int n_seqs, int C, float * out) {
+    for (int d = 0; d < n_seqs; ++d) {
+        const int lo = cu[d], hi = cu[d + 1];
+        for (int t = lo; t < hi; ++t) {
+            const int j0 = std::max(0, lo - (t - k / 2)), j1 = std::min(k, hi - (t - k / 2));
+            for (int i = 0; i < C; ++i) {
+                float acc = 0.0f;
+                for (int j = j0; j < j1; ++j) {
+                    const size_t o = (size_t) (t + j - k / 2) * C + i;
+                    acc = std::fma(taps[(size_t) j * C + i], a[o] * x[o], acc);
+                }
+                out[(size_t) t * C + i] = acc * b[(size_t) t * C + i];
+            }
+        }
+    }
+}
+
+// op_block_mean (src/nexterabert.cpp:638-659): per document, runs of `block` tokens
+// (the last one shorter), out = 0, out = fma(h, g, out) per token (out + h without g),
+// then out * (1 / n). Output rows: ceil(len / block) per document, in order.
+void orc_block_mean_rows(const float * h, const float * g, const int32_t * cu, int n_seqs, int block, int C,
+                         float * out) {
+    size_t row = 0;
+    for (int d = 0; d < n_seqs; ++d) {
+        const int lo = cu[d], len = cu[d + 1] - cu[d];
+        for (int bi = 0; bi * block < len; ++bi, ++row) {
+            const int ts = lo + bi * block, n = std::min(block, len - bi * block);
+            float * o = out + row * C;
+            for (int i = 0; i < C; ++i) o[i] = 0.0f;
+            for (int u = 0; u < n; ++u) {
+                const float * hr = h + (size_t) (ts + u) * C;
+                if (g) {
+                    const float * gr = g + (size_t) (ts + u) * C;
+                    for (int i = 0; i < C; ++i) o[i] = std::fma(hr[i], gr[i], o[i]);
+                } else {
+                    for (int i = 0; i < C; ++i) o[i] = o[i] + hr[i];
+                }
+            }
+            const float inv = 1.0f / (float) n;
+            for (int i = 0; i < C; ++i) o[i] *= inv;
+        }
+    }
+}
+
 void orc_dequant_q8_0(const uint8_t * data, int64_t n, float * out) {
     for (int64_t b = 0; b < n / 32; ++b) {
         const uint8_t * blk = data + b * 34;
@@ -452,3 +558,34 @@ int orc_linear_simd(const int8_t * w, const float * scale, const int32_t * off, 
 }
 
 } // extern "C"
+
+namespace {
+
+// exp256 on the instructions the reference uses (AVX2 + FMA), to check the scalar
+// statement orc_exp_cephes against the hardware semantics of ROUNDPS, FNMADD, CVTPS2DQ.
+__attribute__((target("avx2,fma")))
+void exp_cephes_avx2(const float * x, int64_t n, float * out) {
+    for (int64_t i = 0; i + 8 <= n; i += 8) {
+        __m256 v = _mm256_loadu_ps(x + i);
+        v = _mm256_min_ps(v, _mm256_set1_ps(88.3762626647949f));
+        v = _mm256_max_ps(v, _mm256_set1_ps(-87.3f));
+        const __m256 fn = _mm256_round_ps(_mm256_mul_ps(v, _mm256_set1_ps(1.44269504088896341f)),
+                                          _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+        v = _mm256_fnmadd_ps(fn, _mm256_set1_ps(0.693359375f), v);
+        v = _mm256_fnmadd_ps(fn, _mm256_set1_ps(-2.12194440e-4f), v);
+        const __m256 v2 = _mm256_mul_ps(v, v);
+        __m256 p = _mm256_set1_ps(EXP_P[0]);
+        for (int k = 1; k < 6; ++k) p = _mm256_fmadd_ps(p, v, _mm256_set1_ps(EXP_P[k]));
+        p = _mm256_fmadd_ps(p, v2, _mm256_add_ps(v, _mm256_set1_ps(1.0f)));
+        const __m256i e = _mm256_slli_epi32(_mm256_add_epi32(_mm256_cvtps_epi32(fn), _mm256_set1_epi32(127)), 23);
+        _mm256_storeu_ps(out + i, _mm256_mul_ps(p, _mm256_castsi256_ps(e)));
+    }
+}
+
+} // namespace
+
+extern "C" int orc_exp_cephes_simd(const float * x, int64_t n, float * out) {
+    if (n % 8 != 0 || !__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma")) return -1;
+    exp_cephes_avx2(x, n, out);
+    return 0;
+}

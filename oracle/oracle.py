@@ -54,6 +54,13 @@ def lib() -> ctypes.CDLL:
         L.orc_expand_rows.restype = None
         L.orc_rms_norm_rows.argtypes = [P, P, ctypes.c_float, i32, i32, P]
         L.orc_rms_norm_rows.restype = None
+        i64 = ctypes.c_int64
+        L.orc_exp_cephes_rows.argtypes, L.orc_exp_cephes_rows.restype = [P, i64, P], None
+        L.orc_exp_cephes_simd.argtypes, L.orc_exp_cephes_simd.restype = [P, i64, P], i32
+        L.orc_gate_rows.argtypes, L.orc_gate_rows.restype = [P, P, i32, i32, P], None
+        L.orc_dwconv_rows.argtypes, L.orc_dwconv_rows.restype = [P, P, P, i32, P, i32, i32, P], None
+        L.orc_lily_state_rows.argtypes, L.orc_lily_state_rows.restype = [P, P, P, P, i32, P, i32, i32, P], None
+        L.orc_block_mean_rows.argtypes, L.orc_block_mean_rows.restype = [P, P, P, i32, i32, i32, P], None
         L.orc_dequant_q8_0.argtypes = [P, ctypes.c_int64, P]
         L.orc_dequant_q8_0.restype = None
         L.orc_block_sums.argtypes = [P, P, i32, i32, P, i32, P]
@@ -128,6 +135,73 @@ def rms_norm(x: np.ndarray, gain: np.ndarray, eps: float) -> np.ndarray:
     assert C % 8 == 0 and g.shape == (C,)
     out = np.empty_like(x)
     lib().orc_rms_norm_rows(_p(x), _p(g), float(np.float32(eps)), T, C, _p(out))
+    return out
+
+
+def exp_cephes(x: np.ndarray, simd: bool = False) -> np.ndarray:
+    """exp256 (src/nexterabert.cpp:81-100) element by element; simd: on AVX2 + FMA
+    themselves (size % 8 == 0)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    if simd:
+        if lib().orc_exp_cephes_simd(_p(x), x.size, _p(out)) != 0:
+            raise RuntimeError("AVX2/FMA not available or size % 8 != 0")
+    else:
+        lib().orc_exp_cephes_rows(_p(x), x.size, _p(out))
+    return out
+
+
+def _f32_rows(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def gate(g: np.ndarray, y: np.ndarray) -> np.ndarray:
+    """op_gate (src/nexterabert.cpp:507-522): sigmoid256(g) * y."""
+    g, y = _f32_rows(g), _f32_rows(y)
+    assert g.shape == y.shape and g.ndim == 2
+    out = np.empty_like(g)
+    lib().orc_gate_rows(_p(g), _p(y), g.shape[0], g.shape[1], _p(out))
+    return out
+
+
+def _cu(cu_offsets):
+    return np.ascontiguousarray(cu_offsets, dtype=np.int32)
+
+
+def dwconv(x: np.ndarray, taps: np.ndarray, cu_offsets, r: np.ndarray = None) -> np.ndarray:
+    """op_dwconv (src/nexterabert.cpp:524-543) over a packed batch; taps [k][C]."""
+    x, taps, cu = _f32_rows(x), _f32_rows(taps), _cu(cu_offsets)
+    T, C = x.shape
+    assert taps.shape[1] == C and cu[-1] == T
+    if r is not None:
+        r = _f32_rows(r)
+        assert r.shape == x.shape
+    out = np.empty_like(x)
+    lib().orc_dwconv_rows(_p(x), _p(r), _p(taps), taps.shape[0], _p(cu), cu.size - 1, C, _p(out))
+    return out
+
+
+def lily_state(a: np.ndarray, x: np.ndarray, b: np.ndarray, taps: np.ndarray, cu_offsets) -> np.ndarray:
+    """op_lily_state (src/nexterabert.cpp:545-578) over a packed batch; taps [k][C]."""
+    a, x, b, taps, cu = _f32_rows(a), _f32_rows(x), _f32_rows(b), _f32_rows(taps), _cu(cu_offsets)
+    T, C = x.shape
+    assert a.shape == x.shape == b.shape and taps.shape[1] == C and cu[-1] == T
+    out = np.empty_like(x)
+    lib().orc_lily_state_rows(_p(a), _p(x), _p(b), _p(taps), taps.shape[0], _p(cu), cu.size - 1, C, _p(out))
+    return out
+
+
+def block_mean(h: np.ndarray, cu_offsets, block: int, g: np.ndarray = None) -> np.ndarray:
+    """op_block_mean (src/nexterabert.cpp:638-659): ceil(len / block) rows per document."""
+    h, cu = _f32_rows(h), _cu(cu_offsets)
+    T, C = h.shape
+    assert cu[-1] == T
+    if g is not None:
+        g = _f32_rows(g)
+        assert g.shape == h.shape
+    n_rows = int(sum((int(n) + block - 1) // block for n in np.diff(cu)))
+    out = np.empty((n_rows, C), np.float32)
+    lib().orc_block_mean_rows(_p(h), _p(g), _p(cu), cu.size - 1, block, C, _p(out))
     return out
 
 
