@@ -27,6 +27,7 @@ CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 OBJ = PKG / "_build"
 LIB = PKG / "libnxg.so"
+CLI = PKG / "nxg-cli"
 ARCH = "gfx950"
 
 
@@ -90,6 +91,11 @@ def build(verbose: bool = False) -> Path:
     _run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread",
           OBJ / "nxg_linear.o", OBJ / "nxg_host.o", OBJ / "nxg_gguf.o", "-o", tmp], verbose)
     os.replace(tmp, LIB)
+    # the C++ driver over the C ABI (nxg-cli: --info, --bench), linked against libnxg.so
+    rocm = Path(_hipcc()).resolve().parent.parent
+    _run(["g++", "-O2", "-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}", f"-I{rocm / 'include'}",
+          CSRC / "nxg_cli.cpp", "-o", CLI, f"-L{PKG}", "-lnxg", f"-L{rocm / 'lib'}", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{rocm / 'lib'}"], verbose)
     return LIB
 
 

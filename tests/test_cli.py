@@ -49,3 +49,25 @@ def test_info_on_a_gguf_file(cli, nxg, tmp_path, capsys):
     out = capsys.readouterr().out
     assert "libnxg.so" in out
     assert "GGUF v3, Q4_K_M, architecture nexterabert, 2 tensors, 1 int8 linears" in out
+
+
+# --- the C++ driver (nexterabert.cpp_amd/nxg-cli) ----------------------------------
+
+CXX_CLI = ROOT / "nexterabert.cpp_amd" / "nxg-cli"
+
+
+def test_cxx_cli_help_and_info(nxg, tmp_path):
+    import subprocess
+    import numpy as np
+    assert CXX_CLI.exists(), "nxg-cli is built by nexterabert.cpp_amd/build.py"
+    r = subprocess.run([str(CXX_CLI), "--help"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and "--bench T" in r.stderr
+    r = subprocess.run([str(CXX_CLI), "--bench", "8", "--nonsense"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1
+    rows = (0.02 * np.random.default_rng(1).standard_normal((8, 64))).astype(np.float32)
+    tensors = [("blocks.0.attn.c_q.weight", nxg.TYPE_Q8_0, (64, 8), nxg.quantize_weight(nxg.TYPE_Q8_0, rows).tobytes())]
+    path = tmp_path / "m.gguf"
+    W.write_gguf(path, [("general.file_type", W.UINT32, 7)], tensors)
+    r = subprocess.run([str(CXX_CLI), "--info", "-m", str(path)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    assert "model: GGUF v3, Q8_0, 1 tensors" in r.stdout

@@ -130,3 +130,19 @@ def test_cli_bench(nxg, enc, capsys, extra):
     assert "T=64  batch=3" in line and "median" in line and "tokens/s" in line
     if "--profile" in extra:
         assert "quantize" in out and "GEMM fp32 out" in out and "GEMM relu^2 -> int8" in out
+
+
+@pytest.mark.parametrize("extra", [[], ["--graph", "--profile"]])
+def test_cxx_cli_bench(nxg, extra):
+    """The C++ driver (nxg-cli) runs the same pass through the C ABI alone."""
+    import subprocess
+    cli = ROOT / "nexterabert.cpp_amd" / "nxg-cli"
+    say(f"nxg-cli --bench 64 --batch 3 --reps 3 {' '.join(extra)}")
+    r = subprocess.run([str(cli), "--bench", "64", "--batch", "3", "--reps", "3"] + extra,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    line = next(l for l in r.stdout.splitlines() if l.startswith("bench: "))
+    assert "T=64  batch=3" in line and "tokens/s" in line
+    assert "92 GEMMs (18 relu^2 -> int8) + 74 quantizations" in r.stdout
+    if "--profile" in extra:
+        assert "GEMM fp32 out" in r.stdout and "quantize" in r.stdout
