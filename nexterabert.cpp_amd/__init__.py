@@ -685,6 +685,38 @@ class Builder:
             r = quantize_rows_relu2(linear_i8(w_fc, qa, cu_offsets=cu_offsets), self.act_max)
         return linear_i8(w_proj, r, residual=x, cu_offsets=cu_offsets, out=out)
 
+    def gated_out(self, pre: str, y, z, x, cu_offsets=None, out=None):
+        """x + c_proj(sigmoid(c_gate(y)) * z) (gated_out, src/nexterabert.cpp:1208-1213): y is
+        quantized once (op_copy), c_gate runs in fp32 rows, and op_gate quantizes its rows for
+        the int8 c_proj where it makes them."""
+        gl = self.linear(pre + "c_gate.weight", y, cu_offsets=cu_offsets)
+        gz = gate_quantize_rows(gl, z, self.act_max)
+        return self.linear(pre + "c_proj.weight", gz, residual=x, cu_offsets=cu_offsets, out=out)
+
+    def lily(self, pre: str, h, x, ltc_taps, state_taps, cu_offsets, out=None):
+        """SnowLily's linears and their producers (mix_lily after its norm, src/nexterabert.cpp:
+        1231-1243): z = in_proj(h), r = A(h), lr = dwconv(z; ltc taps) + r quantized for
+        out_proj, a = out_proj(lr), xp = x_proj(h), b = B_proj(h), st = lily_state(a, xp, b)
+        quantized for c_proj, x + c_proj(st). h: the norm's quantized rows (or f32 rows);
+        taps [k][channels] as conv_params hands them over."""
+        cu = cu_offsets if cu_offsets is not None else [0, (h.T if isinstance(h, QAct) else h.shape[0])]
+        z = self.linear(pre + "ltc_conv.in_proj.weight", h, cu_offsets=cu)
+        r = self.linear(pre + "ltc_conv.A.weight", h, cu_offsets=cu)
+        lr = dwconv_quantize_rows(z, ltc_taps, cu, r=r, act_max=self.act_max)
+        a = self.linear(pre + "ltc_conv.out_proj.weight", lr, cu_offsets=cu)
+        xp = self.linear(pre + "x_proj.weight", h, cu_offsets=cu)
+        b = self.linear(pre + "B_proj.weight", h, cu_offsets=cu)
+        st = lily_state_quantize_rows(a, xp, b, state_taps, cu, act_max=self.act_max)
+        return self.linear(pre + "c_proj.weight", st, residual=x, cu_offsets=cu, out=out)
+
+    def hra_block_qkv(self, pre: str, ci, gt, cu_offsets, block: int = 4):
+        """HRA's block attention inputs (mix_hra, src/nexterabert.cpp:1251-1256): the block
+        means of ci * gt (op_block_mean, quantized for the int8 c_q / c_k / c_v, which share
+        it) and the three projections on the block rows. Returns (q, k, v) fp32 rows."""
+        hb = block_mean_quantize_rows(ci, cu_offsets, block, g=gt, act_max=self.act_max)
+        cub = block_offsets(cu_offsets, block)
+        return tuple(self.linear(pre + n, hb, cu_offsets=cub) for n in ("c_q.weight", "c_k.weight", "c_v.weight"))
+
     def reset(self) -> None:
         """Drops the quantized copies (the reference rebuilds its graph per forward)."""
         self.qcache.clear()

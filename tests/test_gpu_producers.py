@@ -157,3 +157,79 @@ def test_producers_bad_arguments(nxg, torch, dev):
         nxg.block_mean_quantize_rows(x, [0, 3], 4)                 # offsets must end at T
     with pytest.raises(ValueError):
         nxg.gate_quantize_rows(torch.zeros(4, 48, device="cuda"), torch.zeros(4, 48, device="cuda"))  # n_in % 32
+
+
+# --- the reference builder's int8 chains through the producers ------------------------
+
+def _weights(nxg, rng, shapes):
+    host, dev = {}, {}
+    for name, (n_in, n_out) in shapes.items():
+        rows = (0.05 * rng.standard_normal((n_out, n_in))).astype(np.float32)
+        W = nxg.expand_weight(nxg.TYPE_Q8_0, nxg.quantize_weight(nxg.TYPE_Q8_0, rows), n_in, n_out)
+        host[name], dev[name] = W, nxg.DeviceWeight(W)
+    return host, dev
+
+
+def _lin(orc, W, x, res=None):
+    q, sx = orc.quantize_rows(x)
+    simd = bool(orc.vnni_flavour()) and W.w.shape[1] % 32 == 0
+    return orc.linear(W.w, W.scale, W.off, q, sx, res=res, simd=simd, n_threads=orc.default_threads())
+
+
+def test_builder_gated_out(nxg, orc, torch, dev):
+    """x + c_proj(sigmoid(c_gate(y)) * z) (src/nexterabert.cpp:1208-1213) against the oracle chain."""
+    say("Builder.gated_out")
+    rng = np.random.default_rng(41)
+    C, pre = 256, "blocks.0.attn."
+    host, devw = _weights(nxg, rng, {pre + "c_gate.weight": (C, C), pre + "c_proj.weight": (C, C)})
+    cu = nxg.cu_offsets_of([100, 50])
+    y, z, x = (rng.standard_normal((150, C)).astype(np.float32) for _ in range(3))
+    b = nxg.Builder(devw)
+    out = b.gated_out(pre, cuda(torch, y), cuda(torch, z), cuda(torch, x), cu_offsets=cu).cpu().numpy()
+    gl = _lin(orc, host[pre + "c_gate.weight"], y)
+    ref = _lin(orc, host[pre + "c_proj.weight"], orc.gate(gl, z), res=x)
+    assert (bits(out) == bits(ref)).all()
+
+
+def test_builder_lily(nxg, orc, torch, dev):
+    """SnowLily's linears and producers (src/nexterabert.cpp:1231-1243) against the oracle chain."""
+    say("Builder.lily")
+    rng = np.random.default_rng(42)
+    C, R, pre = 256, 64, "blocks.0.attn."
+    shapes = {pre + "ltc_conv.in_proj.weight": (C, R), pre + "ltc_conv.A.weight": (C, R),
+              pre + "ltc_conv.out_proj.weight": (R, C), pre + "x_proj.weight": (C, C),
+              pre + "B_proj.weight": (C, C), pre + "c_proj.weight": (C, C)}
+    host, devw = _weights(nxg, rng, shapes)
+    lengths = [100, 3, 47]
+    cu = nxg.cu_offsets_of(lengths)
+    T = int(cu[-1])
+    h, x = (rng.standard_normal((T, C)).astype(np.float32) for _ in range(2))
+    ltc = rng.standard_normal((5, R)).astype(np.float32)
+    st_taps = rng.standard_normal((3, C)).astype(np.float32)
+    b = nxg.Builder(devw)
+    out = b.lily(pre, cuda(torch, h), cuda(torch, x), cuda(torch, ltc), cuda(torch, st_taps), cu).cpu().numpy()
+    W = lambda n: host[pre + n]
+    z, r = _lin(orc, W("ltc_conv.in_proj.weight"), h), _lin(orc, W("ltc_conv.A.weight"), h)
+    a = _lin(orc, W("ltc_conv.out_proj.weight"), orc.dwconv(z, ltc, cu, r))
+    xp, bb = _lin(orc, W("x_proj.weight"), h), _lin(orc, W("B_proj.weight"), h)
+    ref = _lin(orc, W("c_proj.weight"), orc.lily_state(a, xp, bb, st_taps, cu), res=x)
+    assert (bits(out) == bits(ref)).all()
+
+
+def test_builder_hra_block_qkv(nxg, orc, torch, dev):
+    """HRA's block means -> c_q / c_k / c_v on block rows (src/nexterabert.cpp:1251-1256)."""
+    say("Builder.hra_block_qkv")
+    rng = np.random.default_rng(43)
+    C, pre = 256, "blocks.0.attn."
+    host, devw = _weights(nxg, rng, {pre + "c_q.weight": (C, C), pre + "c_k.weight": (C, 128),
+                                     pre + "c_v.weight": (C, 128)})
+    lengths = [9, 1, 30]
+    cu = nxg.cu_offsets_of(lengths)
+    T = int(cu[-1])
+    ci, gt = (rng.standard_normal((T, C)).astype(np.float32) for _ in range(2))
+    b = nxg.Builder(devw)
+    q, k, v = (t.cpu().numpy() for t in b.hra_block_qkv(pre, cuda(torch, ci), cuda(torch, gt), cu, 4))
+    hb = orc.block_mean(ci, cu, 4, gt)
+    assert q.shape == (hb.shape[0], C) and hb.shape[0] == 3 + 1 + 8
+    for got, n in ((q, "c_q.weight"), (k, "c_k.weight"), (v, "c_v.weight")):
+        assert (bits(got) == bits(_lin(orc, host[pre + n], hb))).all(), n
