@@ -179,6 +179,30 @@ NXG_API int32_t nxg_block_mean_quantize_rows(const float * h, const float * g, c
                                              int32_t block, int32_t n_in, int32_t act_max, int8_t * q, float * sx,
                                              void * stream);
 
+/* op_attention with head_dim 64 (src/nexterabert.cpp:704-852): grouped-query attention
+ * inside each document of a packed layout, with the reference's AVX2 arithmetic (the
+ * scores' 8-lane FMA chains and their two summation trees, softmax_exp with exp256 and the
+ * C library's expf for the last n % 8 keys, the value sums in key order).
+ *   q         device float [T][n_head * 64], row-major (after qk_prep)
+ *   k, v      device float [n_kv_head][T][64], head-major
+ *   cu_offsets, n_seqs  the packed layout on the device (as the producers take it)
+ *   scale     device float [n_seqs]: the per-document scale (nxg_attention_scales)
+ *   half      -1: every key of the document; >= 0: the band |i - j| <= half (swa)
+ *   max_keys  an upper bound of keys per query, <= 16384 (a document longer than it gets
+ *             NaN outputs); sizes the kernel's LDS
+ *   out       device float [T][n_head * 64] */
+NXG_API int32_t nxg_attention(const float * q, const float * k, const float * v, const int32_t * cu_offsets,
+                              int32_t n_seqs, const float * scale, int32_t T, int32_t n_head, int32_t n_kv_head,
+                              int32_t half, int32_t max_keys, float * out, void * stream);
+
+/* The per-document scales op_attention uses (src/nexterabert.cpp:1196-1201, :1174-1181),
+ * on the host with the C library's logf: base = 1 / sqrt(head_dim); mode 0 (ssmax "none"
+ * or an swa layer): base; 1 ("ssmax"): base * (s * ln n); 2 ("sssmax"): base *
+ * (s * ln n + ssmax_base + max(b, 0)); n = max(document length, 1).
+ *   cu_offsets  host int32, n_seqs + 1;  out  host float [n_seqs] */
+NXG_API int32_t nxg_attention_scales(const int32_t * cu_offsets, int32_t n_seqs, int32_t head_dim, int32_t mode,
+                                     float s, float b, float ssmax_base, float * out);
+
 /* The qact buffers in the reference's own format (src/nexterabert.cpp:368-375):
  *   u8  device uint8 [T][n_in], the reference's u8 values (q + act_max + 1)
  *   sx_ref device float, ((T+3)/4)*n_blk*4 floats, [token/4][block][token%4] */

@@ -75,6 +75,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_dwconv_quantize_rows": ([P, P, P, i32, P, i32, i32, i32, i32, P, P, P], i32),
         "nxg_lily_state_quantize_rows": ([P, P, P, P, i32, P, i32, i32, i32, i32, P, P, P], i32),
         "nxg_block_mean_quantize_rows": ([P, P, P, P, i32, i32, i32, i32, i32, i32, P, P, P], i32),
+        "nxg_attention": ([P, P, P, P, i32, P, i32, i32, i32, i32, i32, P, P], i32),
+        "nxg_attention_scales": ([P, i32, i32, i32, ctypes.c_float, ctypes.c_float, ctypes.c_float, P], i32),
         "nxg_qact_export": ([P, P, i32, i32, i32, P, P, P], i32),
         "nxg_weight_create": ([P, P, i32, i32, ctypes.POINTER(P)], i32),
         "nxg_weight_destroy": ([P], None),
@@ -413,6 +415,48 @@ def block_mean_quantize_rows(h, cu_offsets: Sequence[int], block: int, g=None, a
                                                        block, n_in, act_max, qa.q.data_ptr(), qa.sx.data_ptr(),
                                                        _stream_ptr(stream)), "block_mean_quantize_rows")
     return qa
+
+
+SSMAX_NONE, SSMAX_SSMAX, SSMAX_SSSMAX = 0, 1, 2   # nxg_attention_scales modes
+
+
+def attention_scales(cu_offsets: Sequence[int], head_dim: int = 64, mode: int = SSMAX_NONE, s: float = 1.0,
+                     b: float = 0.0, ssmax_base: float = 0.1) -> np.ndarray:
+    """The per-document attention scales of src/nexterabert.cpp:1196-1201 (host, the C
+    library's logf): 1/sqrt(head_dim) times 1, s ln n, or s ln n + ssmax_base + max(b, 0)."""
+    cu = np.ascontiguousarray(cu_offsets, dtype=np.int32)
+    out = np.empty(cu.size - 1, np.float32)
+    _check(load_library().nxg_attention_scales(_np_ptr(cu), cu.size - 1, head_dim, mode, float(s), float(b),
+                                                 float(ssmax_base), _np_ptr(out)), "attention_scales")
+    return out
+
+
+def attention(q, k, v, cu_offsets: Sequence[int], scale, n_head: int, n_kv_head: int, half: int = -1,
+              out=None, stream=None):
+    """op_attention with head_dim 64 inside each document: q [T][n_head*64], k / v
+    [n_kv_head][T][64] head-major, scale per document (host or device floats)."""
+    torch = _torch()
+    _rows_arg(q, "q")
+    T = q.shape[0]
+    if q.shape[1] != n_head * 64:
+        raise ValueError(f"q must be [T][{n_head * 64}]")
+    for name, t in (("k", k), ("v", v)):
+        if t.dtype != torch.float32 or tuple(t.shape) != (n_kv_head, T, 64) or not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 device tensor [{n_kv_head}][{T}][64]")
+    cu_host = np.ascontiguousarray(cu_offsets, dtype=np.int32)
+    if cu_host.size < 2 or int(cu_host[-1]) != T:
+        raise ValueError(f"cu_offsets must end at T={T}")
+    lens = np.diff(cu_host)
+    max_keys = int(lens.max()) if half < 0 else int(min(lens.max(), 2 * half + 1))
+    cu = _device_offsets(cu_host, q.device)
+    sc = scale if isinstance(scale, torch.Tensor) else torch.tensor(np.asarray(scale, np.float32), device=q.device)
+    sc = sc.to(device=q.device, dtype=torch.float32).contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    _check(load_library().nxg_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), cu.data_ptr(), cu.numel() - 1,
+                                        sc.data_ptr(), T, n_head, n_kv_head, half, max(1, max_keys), out.data_ptr(),
+                                        _stream_ptr(stream)), "attention")
+    return out
 
 
 def export_qact(qa: QAct, stream=None):

@@ -523,4 +523,25 @@ int32_t nxg_quantize_weight(int32_t type, const float * x, int64_t n_in, int64_t
     return NXG_OK;
 }
 
+int32_t nxg_attention_scales(const int32_t * cu_offsets, int32_t n_seqs, int32_t head_dim, int32_t mode,
+                             float s, float b, float ssmax_base, float * out) {
+    if (!cu_offsets || !out || n_seqs < 1 || head_dim < 1 || mode < 0 || mode > 2) {
+        return host_fail(NXG_EINVAL, "attention_scales: bad arguments");
+    }
+    // src/nexterabert.cpp:1196-1201 with ssmax_scale, :1174-1181 (std::log on a float: logf).
+    // The reference is built with -O3 -march=native and GCC's default floating-point
+    // contraction, which fuses s * ln + ssmax_base into one fma (CMakeLists.txt:6-7,77-78).
+    const float base = 1.0f / std::sqrt((float) head_dim);
+    for (int32_t d = 0; d < n_seqs; ++d) {
+        const int n = cu_offsets[d + 1] - cu_offsets[d];
+        float f = 1.0f;
+        if (mode != 0) {
+            const float ln = std::log((float) std::max(n, 1));
+            f = mode == 1 ? s * ln : std::fma(s, ln, ssmax_base) + std::max(b, 0.0f);
+        }
+        out[d] = base * f;
+    }
+    return NXG_OK;
+}
+
 } // extern "C"

@@ -40,6 +40,7 @@ constexpr int NTHREADS = 256;    // 4 waves, 2 x 2, each 64 x 64
 constexpr int WBN = 256;         // relu^2 -> int8 GEMM tile columns: one 256-input block of the next linear
 constexpr int WTHREADS = 512;    // relu^2 -> int8 GEMM: 8 waves, 2 x 4, each 64 x 64
 constexpr int N_XCD = 8;         // MI355X: 8 XCDs, workgroups dispatched round-robin
+#define NXG_ATTN_MAX_KEYS 16384          // keys per query the attention's LDS holds (64 KiB)
 #ifndef NXG_WG_PER_CU
 #define NXG_WG_PER_CU 2          // persistent GEMM workgroups per CU (0: one workgroup per tile)
 #endif
@@ -495,6 +496,153 @@ __global__ __launch_bounds__(256) void produce_quantize_kernel(Src src, int T, i
     __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
     const int g = (int) (blockIdx.x / (unsigned) n_blk), B = (int) (blockIdx.x % (unsigned) n_blk);
     quantize_block<ACT_MAX>(src, T, n_in, KS, n_blk, q, sx, g, B, stage);
+}
+
+// ---------------------------------------------------------------------------
+// Attention (head_dim 64) inside each document of a packed layout
+// ---------------------------------------------------------------------------
+
+// expf as the reference's C library computes it (glibc 2.35 on x86-64 with FMA; the
+// published ARM optimized-routines method): x / ln2 * 32 rounded to an integer k by the
+// 1.5 * 2^52 shift, r = x * 32/ln2 - k (both fused), 2^(k/32) from a 32-entry table with
+// k's high part added to the exponent bits, a degree-3 polynomial in r, all in double,
+// then rounded to float once; |x| >= 88 handled as the library's special cases. Equal to
+// the host library's expf for every float input (checked exhaustively on the host).
+__device__ __forceinline__ float expf_libm(float x) {
+    constexpr uint64_t TAB[32] = {
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull };
+    const uint32_t ux = __float_as_uint(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ff;
+    if (abstop >= 0x42b) {                                       // |x| >= 88, or NaN / Inf
+        if (ux == 0xff800000u) return 0.0f;                      // -Inf
+        if (abstop >= 0x7f8) return x + x;                       // NaN, +Inf
+        if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double xd = (double) x;
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);
+    const uint64_t ki = (uint64_t) __double_as_longlong(kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    const uint64_t t = TAB[ki % 32] + (ki << 47);
+    const double s = __longlong_as_double((long long) t);
+    const double z = __builtin_fma(0x1.c6af84b912394p-5 / 32 / 32 / 32, r, 0x1.ebfce50fac4f3p-3 / 32 / 32);
+    const double r2 = r * r;
+    double y = __builtin_fma(0x1.62e42ff0c52d6p-1 / 32, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    return (float) (y * s);
+}
+
+// One wave per (query t, head h), the head outermost so that neighbouring workgroups read
+// one head's keys. Keys [lo, hi) of t's document (the band |t - j| <= half when half >= 0);
+// their scores and exponentials live in this workgroup's LDS (max_keys floats).
+//  - scores (scores_d64, src/nexterabert.cpp:704-731): 8 keys at a time, lane 8 kk + l
+//    holding key kk's lane-l partial of the 64-term chain (l-th elements of the 8 chunks:
+//    one multiply, then 7 fused steps); the keys of whole groups of 8 summed as HADDPS and
+//    VPERM2F128 order them ((l0+l1)+(l2+l3)) + ((l4+l5)+(l6+l7)) (shuffles xor 1, 2, 4), the
+//    remaining keys as hsum256 does ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) (xor 4, 2, 1);
+//  - softmax_exp (:177-197): m the running maximum from the first score (a NaN first
+//    score makes it NaN; later NaNs never replace it); exp256 for the whole groups of 8,
+//    summed into 8 lane sums in order and reduced by hsum256; the library's expf for
+//    the rest, added one by one;
+//  - values (values_d64, :733-756): lane e accumulates fma(w_j * inv, v_j[e], acc) in key
+//    order, inv = 1 / sum correctly rounded.
+// A document with more keys than max_keys gets NaN outputs (the caller's bound was wrong).
+struct attn_params {
+    const float * q;       // [T][H * 64]
+    const float * k;       // [G][T][64]
+    const float * v;       // [G][T][64]
+    const int32_t * cu;    // n_seqs + 1 offsets (device)
+    const float * scale;   // [n_seqs] (device)
+    float * out;           // [T][H * 64]
+    int n_seqs, T, H, G, half, max_keys;
+};
+
+__global__ __launch_bounds__(64) void attention_kernel(attn_params p) {
+    extern __shared__ float sc[];
+    const int lane = threadIdx.x;
+    const int h = blockIdx.x / p.T, t = blockIdx.x - h * p.T;
+    const int g = h / (p.H / p.G);
+    const doc_rows dr = doc_of(p.cu, p.n_seqs, t, p.T);
+    int lo = dr.lo, hi = dr.hi;
+    if (p.half >= 0) {
+        lo = max(lo, t - p.half);
+        hi = min(hi, t + p.half + 1);
+    }
+    const int n = hi - lo;
+    float * o = p.out + (size_t) t * p.H * 64 + (size_t) h * 64;
+    if (n <= 0 || n > p.max_keys) {
+        o[lane] = __uint_as_float(0x7fc00000u);
+        return;
+    }
+    const float scale = p.scale[dr.d];
+    const float * qr = p.q + (size_t) t * p.H * 64 + (size_t) h * 64;
+    const float * kh = p.k + ((size_t) g * p.T + lo) * 64;
+    const float * vh = p.v + ((size_t) g * p.T + lo) * 64;
+
+    // scores
+    const int kk = lane >> 3, l = lane & 7;
+    float qv[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) qv[c] = qr[8 * c + l];
+    auto partial = [&](int j) {
+        const float * kp = kh + (size_t) j * 64 + l;
+        float a = qv[0] * kp[0];
+#pragma unroll
+        for (int c = 1; c < 8; ++c) a = __builtin_fmaf(qv[c], kp[8 * c], a);
+        return a;
+    };
+    const int ng = n & ~7;
+    for (int j0 = 0; j0 < ng; j0 += 8) {
+        float a = partial(j0 + kk);
+        a = a + __shfl_xor(a, 1);
+        a = a + __shfl_xor(a, 2);
+        a = a + __shfl_xor(a, 4);
+        if (l == 0) sc[j0 + kk] = a * scale;
+    }
+    if (ng < n) {
+        const int j = min(ng + kk, n - 1);                      // lanes past the last key repeat it
+        float a = partial(j);
+        a = a + __shfl_xor(a, 4);
+        a = a + __shfl_xor(a, 2);
+        a = a + __shfl_xor(a, 1);
+        if (l == 0 && ng + kk < n) sc[j] = scale * a;
+    }
+    __syncthreads();
+
+    // m: NaN if the first score is NaN, else the largest score that is not NaN
+    float mx = -__builtin_inff();
+    for (int j = lane; j < n; j += 64) mx = fmaxf(mx, sc[j]);
+#pragma unroll
+    for (int sft = 32; sft >= 1; sft >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sft));
+    const float m = __builtin_isnan(sc[0]) ? sc[0] : mx;
+    __syncthreads();
+    for (int j = lane; j < n; j += 64) sc[j] = j < ng ? exp_cephes(sc[j] - m) : expf_libm(sc[j] - m);
+    __syncthreads();
+    // lane sums of the whole groups (lane l < 8 takes elements 8i + l in order), hsum256
+    float ls = 0.0f;
+    if (lane < 8) {
+        for (int j = lane; j < ng; j += 8) ls = ls + sc[j];
+    }
+    ls = ls + __shfl_xor(ls, 4);
+    ls = ls + __shfl_xor(ls, 2);
+    ls = ls + __shfl_xor(ls, 1);
+    float sum = __shfl(ls, 0);
+    for (int j = ng; j < n; ++j) sum = sum + sc[j];
+    const float inv = 1.0f / sum;
+
+    // values, key by key
+    float acc = 0.0f;
+    for (int j = 0; j < n; ++j) acc = __builtin_fmaf(sc[j] * inv, vh[(size_t) j * 64 + lane], acc);
+    o[lane] = acc;
 }
 
 // int8 tiles -> the reference's u8 rows (q + act_off); one thread per 16 bytes.
@@ -1781,6 +1929,26 @@ int32_t nxg_block_mean_quantize_rows(const float * h, const float * g, const int
     }
     return launch_produce("block_mean_quantize", src_block_mean{h, g, cu_offsets, cu_blocks, n_seqs, T, n_blocks, n_in, block},
                           n_blocks, n_in, act_max, q, sx, stream);
+}
+
+int32_t nxg_attention(const float * q, const float * k, const float * v, const int32_t * cu_offsets,
+                      int32_t n_seqs, const float * scale, int32_t T, int32_t n_head, int32_t n_kv_head,
+                      int32_t half, int32_t max_keys, float * out, void * stream) {
+    if (T < 0 || n_seqs < 1 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head != 0) {
+        return fail(NXG_EINVAL, "attention: T=%d n_seqs=%d n_head=%d n_kv_head=%d", T, n_seqs, n_head, n_kv_head);
+    }
+    if (max_keys < 1 || max_keys > NXG_ATTN_MAX_KEYS) {
+        return fail(NXG_EINVAL, "attention: max_keys=%d (1..%d)", max_keys, NXG_ATTN_MAX_KEYS);
+    }
+    if (T == 0) return NXG_OK;
+    if (!q || !k || !v || !cu_offsets || !scale || !out) return fail(NXG_EINVAL, "attention: null buffer");
+    const long long n_wg = (long long) T * n_head;
+    if (n_wg > INT32_MAX) return fail(NXG_EINVAL, "attention: T=%d n_head=%d too large", T, n_head);
+    int rc = check_device();
+    if (rc) return rc;
+    attn_params p{q, k, v, cu_offsets, scale, out, n_seqs, T, n_head, n_kv_head, half < 0 ? -1 : half, max_keys};
+    attention_kernel<<<dim3((unsigned) n_wg), dim3(64), (size_t) max_keys * sizeof(float), (hipStream_t) stream>>>(p);
+    return launch_check("attention_kernel");
 }
 
 int32_t nxg_qact_export(const int8_t * q, const float * sx, int32_t T, int32_t n_in, int32_t act_max,

@@ -366,6 +366,156 @@ void orc_block_mean_rows(const float * h, const float * g, const int32_t * cu, i
     }
 }
 
+// ---------------------------------------------------------------------------
+// op_attention, head_dim 64 (src/nexterabert.cpp:704-852), lane by lane.
+// ---------------------------------------------------------------------------
+
+// One key's 8 lane partials of the NEXTERA_DOT64 chain: lane l = q[l] * k[l], then
+// fma(q[8c + l], k[8c + l], .) for c = 1..7.
+static void dot64_lanes(const float * q, const float * k, float p[8]) {
+    for (int l = 0; l < 8; ++l) {
+        float a = q[l] * k[l];
+        for (int c = 1; c < 8; ++c) a = std::fma(q[8 * c + l], k[8 * c + l], a);
+        p[l] = a;
+    }
+}
+
+// scores_d64 (:704-731): keys in groups of 8 from the first, each total reduced by the
+// HADDPS / VPERM2F128 tree ((l0+l1)+(l2+l3)) + ((l4+l5)+(l6+l7)); the remaining keys by
+// hsum256 ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)); then * scale.
+static void scores_d64_lanes(const float * q, const float * k, int n, float scale, float * sc) {
+    float p[8];
+    const int n_groups = n & ~7;
+    int j = 0;
+    for (; j < n_groups; ++j) {
+        dot64_lanes(q, k + (size_t) j * 64, p);
+        sc[j] = (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]))) * scale;
+    }
+    for (; j < n; ++j) {
+        dot64_lanes(q, k + (size_t) j * 64, p);
+        sc[j] = scale * (((p[0] + p[4]) + (p[2] + p[6])) + ((p[1] + p[5]) + (p[3] + p[7])));
+    }
+}
+
+// softmax_exp (:177-197): m = the running std::max from s[0]; for the whole 8-groups
+// e = exp256(s - m) added into 8 lane sums, reduced by hsum256; then the remaining
+// elements with the C library's expf, added one by one. Returns the sum.
+static float softmax_exp_lanes(float * s, int n) {
+    float m = s[0];
+    for (int i = 1; i < n; ++i) m = m < s[i] ? s[i] : m;
+    float v[8] = { 0, 0, 0, 0, 0, 0, 0, 0 };
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+        for (int l = 0; l < 8; ++l) {
+            s[i + l] = orc_exp_cephes(s[i + l] - m);
+            v[l] = v[l] + s[i + l];
+        }
+    }
+    float sum = ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
+    for (; i < n; ++i) {
+        s[i] = std::exp(s[i] - m);
+        sum += s[i];
+    }
+    return sum;
+}
+
+// Grouped-query attention inside each document (optionally the band |i - j| <= half):
+// q [T][H*64] row-major, k / v [G][T][64] head-major, out [T][H*64]; scale per document.
+// attend (:758-774): scores, inv = 1 / sum, out = fma(w_j * inv, v_j, out) over j in order.
+void orc_attention(const float * q, const float * k, const float * v, const int32_t * cu, int n_seqs,
+                   const float * scale, int T, int H, int G, int half, float * out) {
+    std::vector<float> sc;
+    const int rep = H / G;
+    for (int d = 0; d < n_seqs; ++d) {
+        for (int t = cu[d]; t < cu[d + 1]; ++t) {
+            int lo = cu[d], hi = cu[d + 1];
+            if (half >= 0) {
+                lo = std::max(lo, t - half);
+                hi = std::min(hi, t + half + 1);
+            }
+            const int n = hi - lo;
+            sc.resize(n);
+            for (int h = 0; h < H; ++h) {
+                const size_t go = (size_t) (h / rep) * T * 64;
+                const float * kh = k + go + (size_t) lo * 64, * vh = v + go + (size_t) lo * 64;
+                scores_d64_lanes(q + (size_t) t * H * 64 + (size_t) h * 64, kh, n, scale[d], sc.data());
+                const float inv = 1.0f / softmax_exp_lanes(sc.data(), n);
+                float * o = out + (size_t) t * H * 64 + (size_t) h * 64;
+                for (int e = 0; e < 64; ++e) o[e] = 0.0f;
+                for (int j = 0; j < n; ++j) {
+                    const float c = sc[j] * inv;
+                    for (int e = 0; e < 64; ++e) o[e] = std::fma(c, vh[(size_t) j * 64 + e], o[e]);
+                }
+            }
+        }
+    }
+}
+
+// The C library's expf restated (glibc 2.35's FMA path, the published ARM optimized-routines
+// method): the statement the GPU computes for softmax_exp's tail, checked here against
+// the host's expf.
+static const uint64_t EXPF_TAB[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull };
+
+float orc_expf_restated(float x) {
+    uint32_t ux;
+    std::memcpy(&ux, &x, 4);
+    const uint32_t abstop = (ux >> 20) & 0x7ff;
+    if (abstop >= 0x42b) {
+        if (ux == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8) return x + x;
+        if (x > 0x1.62e42ep6f) return INFINITY;
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double xd = (double) x;
+    double kd = std::fma(inv_ln2_n, xd, shift);
+    uint64_t ki;
+    std::memcpy(&ki, &kd, 8);
+    kd -= shift;
+    const double r = std::fma(inv_ln2_n, xd, -kd);
+    const uint64_t t = EXPF_TAB[ki % 32] + (ki << 47);
+    double s;
+    std::memcpy(&s, &t, 8);
+    const double z = std::fma(0x1.c6af84b912394p-5 / 32 / 32 / 32, r, 0x1.ebfce50fac4f3p-3 / 32 / 32);
+    const double r2 = r * r;
+    double y = std::fma(0x1.62e42ff0c52d6p-1 / 32, r, 1.0);
+    y = std::fma(z, r2, y);
+    return (float) (y * s);
+}
+
+// Floats u = first, first + stride, ... (as bit patterns) where the restatement differs from
+// the host's expf (NaN results compared as NaN); returns the count, the first few in bad.
+int64_t orc_expf_restated_check(uint32_t first, uint32_t stride, uint64_t count, uint32_t * bad, int n_bad) {
+    int64_t n = 0;
+    uint64_t u = first;
+    for (uint64_t i = 0; i < count && u <= 0xffffffffull; ++i, u += stride) {
+        const uint32_t v = (uint32_t) u;
+        float x;
+        std::memcpy(&x, &v, 4);
+        const float a = std::exp(x), b = orc_expf_restated(x);
+        uint32_t ua, ub;
+        std::memcpy(&ua, &a, 4);
+        std::memcpy(&ub, &b, 4);
+        if (ua != ub && !(std::isnan(a) && std::isnan(b))) {
+            if (n < n_bad) bad[n] = v;
+            ++n;
+        }
+    }
+    return n;
+}
+
+void orc_expf_rows(const float * x, int64_t n, float * out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = std::exp(x[i]);
+}
+
 void orc_dequant_q8_0(const uint8_t * data, int64_t n, float * out) {
     for (int64_t b = 0; b < n / 32; ++b) {
         const uint8_t * blk = data + b * 34;
@@ -588,4 +738,49 @@ extern "C" int orc_exp_cephes_simd(const float * x, int64_t n, float * out) {
     if (n % 8 != 0 || !__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma")) return -1;
     exp_cephes_avx2(x, n, out);
     return 0;
+}
+
+namespace {
+
+// scores_d64's reduction of 8 keys on the instructions the reference uses (HADDPS,
+// VPERM2F128), to check the scalar statement's summation trees against them.
+__attribute__((target("avx2,fma")))
+void scores8_avx2(const float * q, const float * k, float scale, float * sc) {
+    __m256 qv[8], a[8];
+    for (int c = 0; c < 8; ++c) qv[c] = _mm256_loadu_ps(q + 8 * c);
+    for (int key = 0; key < 8; ++key) {
+        const float * kp = k + (size_t) key * 64;
+        __m256 acc = _mm256_mul_ps(qv[0], _mm256_loadu_ps(kp));
+        for (int c = 1; c < 8; ++c) acc = _mm256_fmadd_ps(qv[c], _mm256_loadu_ps(kp + 8 * c), acc);
+        a[key] = acc;
+    }
+    const __m256 h0 = _mm256_hadd_ps(_mm256_hadd_ps(a[0], a[1]), _mm256_hadd_ps(a[2], a[3]));
+    const __m256 h1 = _mm256_hadd_ps(_mm256_hadd_ps(a[4], a[5]), _mm256_hadd_ps(a[6], a[7]));
+    const __m256 t = _mm256_add_ps(_mm256_permute2f128_ps(h0, h1, 0x20), _mm256_permute2f128_ps(h0, h1, 0x31));
+    _mm256_storeu_ps(sc, _mm256_mul_ps(t, _mm256_set1_ps(scale)));
+}
+
+__attribute__((target("avx2,fma")))
+float hsum_key_avx2(const float * q, const float * k, float scale) {
+    __m256 acc = _mm256_mul_ps(_mm256_loadu_ps(q), _mm256_loadu_ps(k));
+    for (int c = 1; c < 8; ++c) acc = _mm256_fmadd_ps(_mm256_loadu_ps(q + 8 * c), _mm256_loadu_ps(k + 8 * c), acc);
+    __m128 s = _mm_add_ps(_mm256_castps256_ps128(acc), _mm256_extractf128_ps(acc, 1));
+    s = _mm_add_ps(s, _mm_movehl_ps(s, s));
+    s = _mm_add_ss(s, _mm_movehdup_ps(s));
+    return scale * _mm_cvtss_f32(s);
+}
+
+} // namespace
+
+// The scores of n keys (n % 8 == 0 taken as groups, the rest one by one) on AVX2.
+extern "C" int orc_scores_d64_simd(const float * q, const float * k, int n, float scale, float * sc) {
+    if (!__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma")) return -1;
+    int j = 0;
+    for (; j + 8 <= n; j += 8) scores8_avx2(q, k + (size_t) j * 64, scale, sc + j);
+    for (; j < n; ++j) sc[j] = hsum_key_avx2(q, k + (size_t) j * 64, scale);
+    return 0;
+}
+
+extern "C" void orc_scores_d64(const float * q, const float * k, int n, float scale, float * sc) {
+    scores_d64_lanes(q, k, n, scale, sc);
 }

@@ -61,6 +61,13 @@ def lib() -> ctypes.CDLL:
         L.orc_dwconv_rows.argtypes, L.orc_dwconv_rows.restype = [P, P, P, i32, P, i32, i32, P], None
         L.orc_lily_state_rows.argtypes, L.orc_lily_state_rows.restype = [P, P, P, P, i32, P, i32, i32, P], None
         L.orc_block_mean_rows.argtypes, L.orc_block_mean_rows.restype = [P, P, P, i32, i32, i32, P], None
+        L.orc_attention.argtypes = [P, P, P, P, i32, P, i32, i32, i32, i32, P]
+        L.orc_attention.restype = None
+        L.orc_expf_rows.argtypes, L.orc_expf_rows.restype = [P, i64, P], None
+        L.orc_expf_restated_check.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, P, i32]
+        L.orc_expf_restated_check.restype = i64
+        L.orc_scores_d64.argtypes, L.orc_scores_d64.restype = [P, P, i32, ctypes.c_float, P], None
+        L.orc_scores_d64_simd.argtypes, L.orc_scores_d64_simd.restype = [P, P, i32, ctypes.c_float, P], i32
         L.orc_dequant_q8_0.argtypes = [P, ctypes.c_int64, P]
         L.orc_dequant_q8_0.restype = None
         L.orc_block_sums.argtypes = [P, P, i32, i32, P, i32, P]
@@ -202,6 +209,49 @@ def block_mean(h: np.ndarray, cu_offsets, block: int, g: np.ndarray = None) -> n
     n_rows = int(sum((int(n) + block - 1) // block for n in np.diff(cu)))
     out = np.empty((n_rows, C), np.float32)
     lib().orc_block_mean_rows(_p(h), _p(g), _p(cu), cu.size - 1, block, C, _p(out))
+    return out
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_offsets, scale, n_head: int, n_kv_head: int,
+              half: int = -1) -> np.ndarray:
+    """op_attention with head_dim 64 (src/nexterabert.cpp:704-852): q [T][H*64] row-major,
+    k / v [G][T][64] head-major, scale per document; half >= 0 restricts keys to the band."""
+    q, k, v, cu = _f32_rows(q), np.ascontiguousarray(k, np.float32), np.ascontiguousarray(v, np.float32), _cu(cu_offsets)
+    T = q.shape[0]
+    assert q.shape[1] == n_head * 64 and k.shape == v.shape == (n_kv_head, T, 64) and cu[-1] == T
+    sc = np.ascontiguousarray(scale, np.float32)
+    assert sc.size == cu.size - 1
+    out = np.empty_like(q)
+    lib().orc_attention(_p(q), _p(k), _p(v), _p(cu), cu.size - 1, _p(sc), T, n_head, n_kv_head, half, _p(out))
+    return out
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    """The C library's expf (the reference's std::exp on floats), element by element."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().orc_expf_rows(_p(x), x.size, _p(out))
+    return out
+
+
+def expf_restated_mismatches(first: int, stride: int, count: int):
+    """Inputs (as float bit patterns first, first + stride, ...) where the restated C-library
+    expf differs from the host's expf: (count, first few patterns)."""
+    bad = np.zeros(8, np.uint32)
+    n = lib().orc_expf_restated_check(first, stride, count, _p(bad), bad.size)
+    return int(n), bad[:min(int(n), bad.size)]
+
+
+def scores_d64(q: np.ndarray, k: np.ndarray, scale: float, simd: bool = False) -> np.ndarray:
+    """scores_d64 (src/nexterabert.cpp:704-731) of one query against n keys [n][64]."""
+    q, k = np.ascontiguousarray(q, np.float32), np.ascontiguousarray(k, np.float32)
+    n = k.shape[0]
+    out = np.empty(n, np.float32)
+    if simd:
+        if lib().orc_scores_d64_simd(_p(q), _p(k), n, float(scale), _p(out)) != 0:
+            raise RuntimeError("AVX2/FMA not available")
+    else:
+        lib().orc_scores_d64(_p(q), _p(k), n, float(scale), _p(out))
     return out
 
 

@@ -1,0 +1,104 @@
+"""GPU: op_attention (head_dim 64) bit for bit against the oracle (src/nexterabert.cpp:704-852):
+documents of 1 to 2,500 tokens (key counts off multiples of 8 send the last keys through
+hsum256 and the C library's expf), full and banded (swa) attention, 16 query / 8 KV heads,
+per-document scales, and scores large enough to underflow exp in both its forms."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "no GPU"
+    return t
+
+
+@pytest.fixture(scope="module")
+def dev(torch, nxg):
+    nxg.init()
+    return torch.device("cuda:0")
+
+
+def run(nxg, torch, q, k, v, cu, scale, H, G, half):
+    c = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    return nxg.attention(c(q), c(k), c(v), cu, scale, H, G, half).cpu().numpy()
+
+
+CASES = [
+    ([1, 7, 8, 9, 64, 111], -1),
+    ([1, 7, 8, 9, 64, 111], 5),
+    ([1, 7, 8, 9, 64, 111], 64),
+    ([1024], -1),
+    ([1024], 128),
+    ([300, 2, 45], 0),
+]
+
+
+@pytest.mark.parametrize("lengths,half", CASES)
+def test_attention_matches_oracle(nxg, orc, torch, dev, lengths, half):
+    say(f"attention lengths={lengths} half={half}")
+    rng = np.random.default_rng(sum(lengths) + half)
+    H, G = 16, 8
+    cu = nxg.cu_offsets_of(lengths)
+    T = int(cu[-1])
+    q = rng.standard_normal((T, H * 64)).astype(np.float32)
+    k = rng.standard_normal((G, T, 64)).astype(np.float32)
+    v = rng.standard_normal((G, T, 64)).astype(np.float32)
+    scale = rng.uniform(0.05, 0.3, len(lengths)).astype(np.float32)
+    y = run(nxg, torch, q, k, v, cu, scale, H, G, half)
+    ref = orc.attention(q, k, v, cu, scale, H, G, half)
+    assert (bits(y) == bits(ref)).all()
+
+
+def test_attention_long_document(nxg, orc, torch, dev):
+    say("attention one document of 2,500 tokens")
+    rng = np.random.default_rng(7)
+    H, G = 2, 1
+    cu = nxg.cu_offsets_of([2500])
+    q = rng.standard_normal((2500, H * 64)).astype(np.float32)
+    k, v = (rng.standard_normal((G, 2500, 64)).astype(np.float32) for _ in range(2))
+    scale = np.array([0.125], np.float32)
+    assert (bits(run(nxg, torch, q, k, v, cu, scale, H, G, -1)) == bits(orc.attention(q, k, v, cu, scale, H, G))).all()
+
+
+def test_attention_extreme_scores(nxg, orc, torch, dev):
+    """Scores spread over +-400: most exponentials underflow, in exp256 (clamped at -87.3)
+    and in the C library's expf (to subnormals and to 0)."""
+    say("attention with extreme scores")
+    rng = np.random.default_rng(8)
+    H, G = 4, 2
+    cu = nxg.cu_offsets_of([13, 29, 5])
+    T = int(cu[-1])
+    q = (rng.standard_normal((T, H * 64)) * 6).astype(np.float32)
+    k, v = (rng.standard_normal((G, T, 64)).astype(np.float32) for _ in range(2))
+    scale = np.array([1.0, 0.5, 2.0], np.float32)
+    y = run(nxg, torch, q, k, v, cu, scale, H, G, -1)
+    assert (bits(y) == bits(orc.attention(q, k, v, cu, scale, H, G))).all()
+
+
+def test_attention_document_alone(nxg, torch, dev):
+    say("attention: a document alone and in a batch")
+    rng = np.random.default_rng(9)
+    H, G = 16, 8
+    lengths = [33, 100, 7]
+    cu = nxg.cu_offsets_of(lengths)
+    T = int(cu[-1])
+    q = rng.standard_normal((T, H * 64)).astype(np.float32)
+    k, v = (rng.standard_normal((G, T, 64)).astype(np.float32) for _ in range(2))
+    scale = np.array([0.1, 0.2, 0.3], np.float32)
+    y = run(nxg, torch, q, k, v, cu, scale, H, G, -1)
+    lo, hi = 33, 133
+    alone = run(nxg, torch, q[lo:hi], k[:, lo:hi], v[:, lo:hi], [0, 100], scale[1:2], H, G, -1)
+    assert (bits(alone) == bits(y[lo:hi])).all()

@@ -1,0 +1,139 @@
+"""CPU: pins of the oracle's op_attention (head_dim 64, src/nexterabert.cpp:704-852) and of
+the restated C-library expf that the GPU uses for softmax_exp's last n % 8 keys.
+
+  * expf: the restatement equals the host's expf on every 97th float bit pattern and on
+    the whole range softmax arguments take near 0 and near underflow (the full 2^32 check
+    was run once on the host: 0 mismatches);
+  * scores: the lane-wise statement of scores_d64 equals the same steps on AVX2 + FMA
+    (HADDPS / VPERM2F128 for groups of 8 keys, hsum256 for the rest);
+  * attention: one key gives v itself; equal scores give the exact-arithmetic mean chain;
+    it is attention (a float64 softmax within a few float ulps); GQA heads of one group
+    share their keys; a band at least as wide as the document is the full attention;
+    documents do not see each other; per-document scales apply per document."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import exact_fp32 as X
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def test_expf_restatement_equals_the_c_library(orc):
+    n, bad = orc.expf_restated_mismatches(0, 97, 2 ** 32 // 97 + 1)
+    assert n == 0, [hex(b) for b in bad]
+    # [-104, 0]: softmax's arguments, through the subnormal results to the underflow cut
+    lo, hi = 0x80000000, 0xC2D00000          # -0.0 .. -104.0 as bit patterns
+    n, bad = orc.expf_restated_mismatches(lo, 7, (hi - lo) // 7 + 1)
+    assert n == 0, [hex(b) for b in bad]
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 16, 63, 100])
+def test_scores_lane_statement_equals_avx2(orc, n):
+    rng = np.random.default_rng(n)
+    q = rng.standard_normal(64).astype(np.float32)
+    k = (rng.standard_normal((n, 64)) * np.exp(rng.uniform(-4, 4, (n, 1)))).astype(np.float32)
+    try:
+        s = orc.scores_d64(q, k, 0.125, simd=True)
+    except RuntimeError:
+        pytest.skip("no AVX2/FMA")
+    assert (bits(orc.scores_d64(q, k, 0.125)) == bits(s)).all()
+
+
+def rand_qkv(rng, T, H, G):
+    q = rng.standard_normal((T, H * 64)).astype(np.float32)
+    k = rng.standard_normal((G, T, 64)).astype(np.float32)
+    v = rng.standard_normal((G, T, 64)).astype(np.float32)
+    return q, k, v
+
+
+def attention64(q, k, v, cu, scale, H, G, half=-1):
+    """float64 softmax attention inside each document (no particular order)."""
+    T = q.shape[0]
+    out = np.zeros((T, H * 64))
+    rep = H // G
+    for d in range(len(cu) - 1):
+        for t in range(cu[d], cu[d + 1]):
+            lo, hi = cu[d], cu[d + 1]
+            if half >= 0:
+                lo, hi = max(lo, t - half), min(hi, t + half + 1)
+            for h in range(H):
+                g = h // rep
+                s = k[g, lo:hi].astype(np.float64) @ q[t, h * 64:(h + 1) * 64].astype(np.float64) * scale[d]
+                w = np.exp(s - s.max())
+                out[t, h * 64:(h + 1) * 64] = (w / w.sum()) @ v[g, lo:hi].astype(np.float64)
+    return out
+
+
+def test_attention_is_attention(orc):
+    rng = np.random.default_rng(1)
+    H, G = 4, 2
+    cu = np.array([0, 5, 13, 40], np.int32)
+    q, k, v = rand_qkv(rng, 40, H, G)
+    scale = np.array([0.125, 0.2, 0.09], np.float32)
+    for half in (-1, 3):
+        y = orc.attention(q, k, v, cu, scale, H, G, half)
+        ref = attention64(q, k, v, cu, scale, H, G, half)
+        assert np.max(np.abs(y - ref)) < 2e-6 * max(1.0, np.max(np.abs(ref)))
+
+
+def test_attention_closed_forms(orc):
+    rng = np.random.default_rng(2)
+    H, G = 4, 2
+    cu = np.array([0, 1, 9, 25], np.int32)          # a one-token document, 8 and 16 keys
+    q, k, v = rand_qkv(rng, 25, H, G)
+    scale = np.full(3, 0.125, np.float32)
+    y = orc.attention(q, k, v, cu, scale, H, G)
+    # one key: softmax weight 1 (expf(0) = 1, 1/1), out = fma(1, v, 0) = v
+    for h in range(H):
+        assert (bits(y[0, h * 64:(h + 1) * 64]) == bits(v[h // 2, 0])).all()
+    # equal keys: every weight exp256(0) = 1, sum n, out = fma(1/n, v_j, out) in key order
+    k2 = k.copy()
+    k2[:, 1:9] = k[:, 1:2]
+    y2 = orc.attention(q, k2, v, cu, scale, H, G)
+    inv = X.div(1.0, 8.0)
+    for h in range(H):
+        acc = [0.0] * 64
+        for j in range(1, 9):
+            acc = [X.fma(inv, float(v[h // 2, j, e]), acc[e]) for e in range(64)]
+        assert (bits(y2[1, h * 64:(h + 1) * 64]) == bits(np.array(acc, np.float32))).all()
+    # GQA: heads 0 and 1 share kv head 0 -- with the same query they give the same output
+    q3 = q.copy()
+    q3[:, 64:128] = q3[:, 0:64]
+    y3 = orc.attention(q3, k, v, cu, scale, H, G)
+    assert (bits(y3[:, 0:64]) == bits(y3[:, 64:128])).all()
+    # a band as wide as the longest document is the full attention
+    assert (bits(orc.attention(q, k, v, cu, scale, H, G, half=16)) == bits(y)).all()
+
+
+def test_attention_documents_and_scales(orc):
+    rng = np.random.default_rng(3)
+    H, G = 2, 1
+    cu = np.array([0, 11, 30, 37], np.int32)
+    q, k, v = rand_qkv(rng, 37, H, G)
+    scale = np.array([0.125, 0.3, 0.05], np.float32)
+    y = orc.attention(q, k, v, cu, scale, H, G)
+    lo, hi = 11, 30
+    alone = orc.attention(q[lo:hi], k[:, lo:hi], v[:, lo:hi], [0, hi - lo], scale[1:2], H, G)
+    assert (bits(alone) == bits(y[lo:hi])).all()
+    # the scale is the document's own: another scale changes only that document
+    s2 = scale.copy()
+    s2[1] = 0.7
+    y2 = orc.attention(q, k, v, cu, s2, H, G)
+    assert (bits(y2[:lo]) == bits(y[:lo])).all() and (bits(y2[hi:]) == bits(y[hi:])).all()
+    assert not (bits(y2[lo:hi]) == bits(y[lo:hi])).all()
+
+
+def test_attention_scales_helper(nxg):
+    import math
+    cu = [0, 1, 5, 1029]
+    base = np.float32(1.0) / np.float32(math.sqrt(64.0))
+    assert (nxg.attention_scales(cu, 64, nxg.SSMAX_NONE) == base).all()
+    s = nxg.attention_scales(cu, 64, nxg.SSMAX_SSMAX, s=0.5)
+    ln = np.log(np.array([1, 4, 1024], np.float32))
+    assert np.allclose(s, base * (np.float32(0.5) * ln), rtol=0, atol=1e-7)
+    s3 = nxg.attention_scales(cu, 64, nxg.SSMAX_SSSMAX, s=0.5, b=-1.0, ssmax_base=0.1)
+    assert s3[0] == base * np.float32(0.1)           # ln 1 = 0, max(b, 0) = 0
