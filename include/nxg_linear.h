@@ -195,6 +195,27 @@ NXG_API int32_t nxg_attention(const float * q, const float * k, const float * v,
                               int32_t n_seqs, const float * scale, int32_t T, int32_t n_head, int32_t n_kv_head,
                               int32_t half, int32_t max_keys, float * out, void * stream);
 
+/* op_qk_prep (src/nexterabert.cpp:590-632): the separable DyT (beta * tanh(alpha * x), with
+ * tanh256's arithmetic) then RoPE at each row's position in its document:
+ *   x          device float [T][n_head * head_dim]
+ *   alpha, beta device float [head_dim] (the q_norm / k_norm parameters)
+ *   cos_t, sin_t device float [n_pos][head_dim / 2] (nxg_rope_table), n_pos > the longest document
+ *   out        device float, row-major [T][n_head * head_dim] (head_major 0, queries) or
+ *              head-major [n_head][T][head_dim] (head_major 1, keys) */
+NXG_API int32_t nxg_qk_prep(const float * x, const float * alpha, const float * beta, const float * cos_t,
+                            const float * sin_t, int32_t n_pos, const int32_t * cu_offsets, int32_t n_seqs,
+                            int32_t T, int32_t n_head, int32_t head_dim, int32_t head_major, float * out,
+                            void * stream);
+
+/* op_head_major (src/nexterabert.cpp:620-632): device [T][n_head * head_dim] -> [n_head][T][head_dim]. */
+NXG_API int32_t nxg_head_major(const float * x, int32_t T, int32_t n_head, int32_t head_dim, float * out,
+                               void * stream);
+
+/* build_rope (src/nexterabert.cpp:1322-1338) on the host with the same C library calls:
+ * cos / sin of t * (1 / base^(2i / head_dim)) for t < n_pos, i < head_dim / 2.
+ *   cos_out, sin_out  host float [n_pos][head_dim / 2] */
+NXG_API int32_t nxg_rope_table(int32_t n_pos, float base, int32_t head_dim, float * cos_out, float * sin_out);
+
 /* The per-document scales op_attention uses (src/nexterabert.cpp:1196-1201, :1174-1181),
  * on the host with the C library's logf: base = 1 / sqrt(head_dim); mode 0 (ssmax "none"
  * or an swa layer): base; 1 ("ssmax"): base * (s * ln n); 2 ("sssmax"): base *

@@ -77,6 +77,9 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_block_mean_quantize_rows": ([P, P, P, P, i32, i32, i32, i32, i32, i32, P, P, P], i32),
         "nxg_attention": ([P, P, P, P, i32, P, i32, i32, i32, i32, i32, P, P], i32),
         "nxg_attention_scales": ([P, i32, i32, i32, ctypes.c_float, ctypes.c_float, ctypes.c_float, P], i32),
+        "nxg_qk_prep": ([P, P, P, P, P, i32, P, i32, i32, i32, i32, i32, P, P], i32),
+        "nxg_head_major": ([P, i32, i32, i32, P, P], i32),
+        "nxg_rope_table": ([i32, ctypes.c_float, i32, P, P], i32),
         "nxg_qact_export": ([P, P, i32, i32, i32, P, P, P], i32),
         "nxg_weight_create": ([P, P, i32, i32, ctypes.POINTER(P)], i32),
         "nxg_weight_destroy": ([P], None),
@@ -456,6 +459,53 @@ def attention(q, k, v, cu_offsets: Sequence[int], scale, n_head: int, n_kv_head:
     _check(load_library().nxg_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), cu.data_ptr(), cu.numel() - 1,
                                         sc.data_ptr(), T, n_head, n_kv_head, half, max(1, max_keys), out.data_ptr(),
                                         _stream_ptr(stream)), "attention")
+    return out
+
+
+def rope_table(n_pos: int, base: float, head_dim: int = 64):
+    """build_rope (src/nexterabert.cpp:1322-1338) on the host: (cos, sin) [n_pos][head_dim/2]."""
+    c = np.empty((n_pos, head_dim // 2), np.float32)
+    s = np.empty_like(c)
+    _check(load_library().nxg_rope_table(n_pos, float(base), head_dim, _np_ptr(c), _np_ptr(s)), "rope_table")
+    return c, s
+
+
+def qk_prep(x, alpha, beta, cos_t, sin_t, cu_offsets: Sequence[int], n_head: int, head_major: bool = False,
+            out=None, stream=None):
+    """op_qk_prep: DyT (beta * tanh(alpha * x)) then RoPE at each row's position in its
+    document. x [T][n_head*D]; alpha, beta [D]; cos_t, sin_t [n_pos][D/2] (device tensors).
+    Returns [T][n_head*D] or, head_major, [n_head][T][D]."""
+    torch = _torch()
+    _rows_arg(x, "x")
+    T, width = x.shape
+    D = width // n_head
+    if D * n_head != width or D % 2:
+        raise ValueError(f"x must be [T][n_head * head_dim] with an even head_dim")
+    for name, t, n in (("alpha", alpha, D), ("beta", beta, D)):
+        if t.dtype != torch.float32 or tuple(t.shape) != (n,) or not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 device tensor [{n}]")
+    _rows_arg(cos_t, "cos_t")
+    _rows_arg(sin_t, "sin_t", cos_t.shape)
+    if cos_t.shape[1] != D // 2:
+        raise ValueError(f"cos_t / sin_t must be [n_pos][{D // 2}]")
+    cu = _device_offsets(cu_offsets, x.device)
+    if out is None:
+        out = torch.empty((n_head, T, D) if head_major else (T, width), dtype=torch.float32, device=x.device)
+    _check(load_library().nxg_qk_prep(x.data_ptr(), alpha.data_ptr(), beta.data_ptr(), cos_t.data_ptr(),
+                                      sin_t.data_ptr(), cos_t.shape[0], cu.data_ptr(), cu.numel() - 1, T, n_head, D,
+                                      1 if head_major else 0, out.data_ptr(), _stream_ptr(stream)), "qk_prep")
+    return out
+
+
+def head_major(x, n_head: int, out=None, stream=None):
+    """op_head_major: [T][n_head*D] -> [n_head][T][D]."""
+    torch = _torch()
+    _rows_arg(x, "x")
+    T, width = x.shape
+    D = width // n_head
+    if out is None:
+        out = torch.empty((n_head, T, D), dtype=torch.float32, device=x.device)
+    _check(load_library().nxg_head_major(x.data_ptr(), T, n_head, D, out.data_ptr(), _stream_ptr(stream)), "head_major")
     return out
 
 

@@ -544,4 +544,22 @@ int32_t nxg_attention_scales(const int32_t * cu_offsets, int32_t n_seqs, int32_t
     return NXG_OK;
 }
 
+int32_t nxg_rope_table(int32_t n_pos, float base, int32_t head_dim, float * cos_out, float * sin_out) {
+    if (n_pos < 1 || head_dim < 2 || head_dim % 2 != 0 || !cos_out || !sin_out) {
+        return host_fail(NXG_EINVAL, "rope_table: bad arguments");
+    }
+    // build_rope, src/nexterabert.cpp:1322-1338, with the same C library calls on floats
+    const int half = head_dim / 2;
+    std::vector<float> inv(half);
+    for (int i = 0; i < half; ++i) inv[i] = 1.0f / std::pow(base, (float) (2 * i) / (float) head_dim);
+    for (int t = 0; t < n_pos; ++t) {
+        for (int i = 0; i < half; ++i) {
+            const float a = (float) t * inv[i];
+            cos_out[(size_t) t * half + i] = std::cos(a);
+            sin_out[(size_t) t * half + i] = std::sin(a);
+        }
+    }
+    return NXG_OK;
+}
+
 } // extern "C"

@@ -645,6 +645,60 @@ __global__ __launch_bounds__(64) void attention_kernel(attn_params p) {
     o[lane] = acc;
 }
 
+// tanh256 (src/nexterabert.cpp:103-117) lane by lane: big = (1 - t) / (1 + t) with t =
+// exp256(|x| * -2) and x's sign bit ORed in, small = the fused odd polynomial * x, small
+// where |x| < 0.1 (ordered: a NaN takes big).
+__device__ __forceinline__ float tanh_ref(float x) {
+    const uint32_t ux = __float_as_uint(x);
+    const float ax = __uint_as_float(ux & 0x7fffffffu);
+    const float t = exp_cephes(ax * -2.0f);
+    const float big = __uint_as_float(__float_as_uint((1.0f - t) / (1.0f + t)) | (ux & 0x80000000u));
+    const float x2 = x * x;
+    float p = -17.0f / 315.0f;
+    p = __builtin_fmaf(p, x2, 2.0f / 15.0f);
+    p = __builtin_fmaf(p, x2, -1.0f / 3.0f);
+    p = __builtin_fmaf(p, x2, 1.0f);
+    const float small = p * x;
+    return ax < 0.1f ? small : big;
+}
+
+// op_qk_prep (src/nexterabert.cpp:590-632): separable DyT then RoPE, one thread per (row,
+// head, i < D/2): a = beta[i] tanh(alpha[i] x1[i]), b = beta[D/2+i] tanh(alpha[D/2+i] x2[i]),
+// y1 = fma(a, cos, b sin), y2 = fma(-a, sin, b cos) at the row's position in its document.
+// Output row-major [T][H*D] or head-major [H][T][D].
+__global__ __launch_bounds__(256) void qk_prep_kernel(const float * __restrict__ x, const float * __restrict__ alpha,
+                                                      const float * __restrict__ beta, const float * __restrict__ cos_t,
+                                                      const float * __restrict__ sin_t, const int32_t * __restrict__ cu,
+                                                      int n_seqs, int T, int H, int D, int n_pos, int head_major,
+                                                      float * __restrict__ out) {
+    const int half = D / 2;
+    const size_t idx = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t) T * H * half) return;
+    const int i = (int) (idx % half);
+    const int h = (int) ((idx / half) % H);
+    const int t = (int) (idx / ((size_t) half * H));
+    const doc_rows dr = doc_of(cu, n_seqs, t, T);
+    const int pos = min(max(t - dr.lo, 0), n_pos - 1);
+    const float c = cos_t[(size_t) pos * half + i], s = sin_t[(size_t) pos * half + i];
+    const float * x1 = x + (size_t) t * H * D + (size_t) h * D;
+    const float a = beta[i] * tanh_ref(alpha[i] * x1[i]);
+    const float b = beta[half + i] * tanh_ref(alpha[half + i] * x1[half + i]);
+    float * y = head_major ? out + ((size_t) h * T + t) * D : out + (size_t) t * H * D + (size_t) h * D;
+    y[i] = __builtin_fmaf(a, c, b * s);
+    y[half + i] = __builtin_fmaf(-a, s, b * c);
+}
+
+// op_head_major (src/nexterabert.cpp:620-632): [T][H*D] -> [H][T][D].
+__global__ __launch_bounds__(256) void head_major_kernel(const float * __restrict__ x, int T, int H, int D,
+                                                         float * __restrict__ out) {
+    const size_t idx = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t) T * H * D) return;
+    const int e = (int) (idx % D);
+    const int h = (int) ((idx / D) % H);
+    const int t = (int) (idx / ((size_t) D * H));
+    out[((size_t) h * T + t) * D + e] = x[idx];
+}
+
 // int8 tiles -> the reference's u8 rows (q + act_off); one thread per 16 bytes.
 __global__ void export_kernel(const int8_t * __restrict__ q, int T, int n_in, int KS, int act_off,
                               uint8_t * __restrict__ u8) {
@@ -1949,6 +2003,35 @@ int32_t nxg_attention(const float * q, const float * k, const float * v, const i
     attn_params p{q, k, v, cu_offsets, scale, out, n_seqs, T, n_head, n_kv_head, half < 0 ? -1 : half, max_keys};
     attention_kernel<<<dim3((unsigned) n_wg), dim3(64), (size_t) max_keys * sizeof(float), (hipStream_t) stream>>>(p);
     return launch_check("attention_kernel");
+}
+
+int32_t nxg_qk_prep(const float * x, const float * alpha, const float * beta, const float * cos_t, const float * sin_t,
+                    int32_t n_pos, const int32_t * cu_offsets, int32_t n_seqs, int32_t T, int32_t n_head,
+                    int32_t head_dim, int32_t head_major, float * out, void * stream) {
+    if (T < 0 || n_head < 1 || head_dim < 2 || head_dim % 2 != 0 || n_pos < 1 || n_seqs < 1) {
+        return fail(NXG_EINVAL, "qk_prep: T=%d n_head=%d head_dim=%d n_pos=%d n_seqs=%d", T, n_head, head_dim, n_pos, n_seqs);
+    }
+    if (T == 0) return NXG_OK;
+    if (!x || !alpha || !beta || !cos_t || !sin_t || !cu_offsets || !out) return fail(NXG_EINVAL, "qk_prep: null buffer");
+    const size_t n = (size_t) T * n_head * (head_dim / 2);
+    if (n / 256 + 1 > (size_t) INT32_MAX) return fail(NXG_EINVAL, "qk_prep: too large");
+    int rc = check_device();
+    if (rc) return rc;
+    qk_prep_kernel<<<(unsigned) ((n + 255) / 256), 256, 0, (hipStream_t) stream>>>(
+        x, alpha, beta, cos_t, sin_t, cu_offsets, n_seqs, T, n_head, head_dim, n_pos, head_major ? 1 : 0, out);
+    return launch_check("qk_prep_kernel");
+}
+
+int32_t nxg_head_major(const float * x, int32_t T, int32_t n_head, int32_t head_dim, float * out, void * stream) {
+    if (T < 0 || n_head < 1 || head_dim < 1) return fail(NXG_EINVAL, "head_major: T=%d n_head=%d head_dim=%d", T, n_head, head_dim);
+    if (T == 0) return NXG_OK;
+    if (!x || !out) return fail(NXG_EINVAL, "head_major: null buffer");
+    const size_t n = (size_t) T * n_head * head_dim;
+    if (n / 256 + 1 > (size_t) INT32_MAX) return fail(NXG_EINVAL, "head_major: too large");
+    int rc = check_device();
+    if (rc) return rc;
+    head_major_kernel<<<(unsigned) ((n + 255) / 256), 256, 0, (hipStream_t) stream>>>(x, T, n_head, head_dim, out);
+    return launch_check("head_major_kernel");
 }
 
 int32_t nxg_qact_export(const int8_t * q, const float * sx, int32_t T, int32_t n_in, int32_t act_max,

@@ -512,6 +512,62 @@ int64_t orc_expf_restated_check(uint32_t first, uint32_t stride, uint64_t count,
     return n;
 }
 
+// tanh256 (src/nexterabert.cpp:103-117) for one lane: big = (1 - t) / (1 + t) with
+// t = exp256(|x| * -2) and x's sign bit ORed in; small = (((-17/315 x^2 + 2/15) x^2 - 1/3)
+// x^2 + 1) * x by fused steps; small where |x| < 0.1 (an ordered compare: NaN takes big).
+float orc_tanh_ref(float x) {
+    uint32_t ux;
+    std::memcpy(&ux, &x, 4);
+    const uint32_t sign = ux & 0x80000000u;
+    float ax;
+    const uint32_t uax = ux & 0x7fffffffu;
+    std::memcpy(&ax, &uax, 4);
+    const float t = orc_exp_cephes(ax * -2.0f);
+    float big = (1.0f - t) / (1.0f + t);
+    uint32_t ub;
+    std::memcpy(&ub, &big, 4);
+    ub |= sign;
+    std::memcpy(&big, &ub, 4);
+    const float x2 = x * x;
+    float p = -17.0f / 315.0f;
+    p = std::fma(p, x2, 2.0f / 15.0f);
+    p = std::fma(p, x2, -1.0f / 3.0f);
+    p = std::fma(p, x2, 1.0f);
+    const float small = p * x;
+    return ax < 0.1f ? small : big;
+}
+
+// op_qk_prep (src/nexterabert.cpp:590-632): per row t (position pos = t - its document's
+// start) and head h, with half = D/2: a = beta[i] * tanh(alpha[i] * x1[i]), b = beta[half+i] *
+// tanh(alpha[half+i] * x2[i]); y1 = fma(a, cos, b * sin), y2 = fma(-a, sin, b * cos).
+// x [T][H*D]; alpha, beta [D]; cos, sin [n_pos][half]; out [T][H*D] (head_major 0) or
+// [H][T][D] (head_major 1).
+void orc_qk_prep(const float * x, const float * alpha, const float * beta, const float * cos_t, const float * sin_t,
+                 const int32_t * cu, int n_seqs, int T, int H, int D, int head_major, float * out) {
+    const int half = D / 2;
+    for (int d = 0; d < n_seqs; ++d) {
+        for (int t = cu[d]; t < cu[d + 1]; ++t) {
+            const int pos = t - cu[d];
+            const float * c = cos_t + (size_t) pos * half, * s = sin_t + (size_t) pos * half;
+            for (int h = 0; h < H; ++h) {
+                const float * x1 = x + (size_t) t * H * D + (size_t) h * D, * x2 = x1 + half;
+                float * y1 = head_major ? out + ((size_t) h * T + t) * D : out + (size_t) t * H * D + (size_t) h * D;
+                float * y2 = y1 + half;
+                for (int i = 0; i < half; ++i) {
+                    const float a = beta[i] * orc_tanh_ref(alpha[i] * x1[i]);
+                    const float b = beta[half + i] * orc_tanh_ref(alpha[half + i] * x2[i]);
+                    y1[i] = std::fma(a, c[i], b * s[i]);
+                    y2[i] = std::fma(-a, s[i], b * c[i]);
+                }
+            }
+        }
+    }
+}
+
+void orc_tanh_rows(const float * x, int64_t n, float * out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_tanh_ref(x[i]);
+}
+
 void orc_expf_rows(const float * x, int64_t n, float * out) {
     for (int64_t i = 0; i < n; ++i) out[i] = std::exp(x[i]);
 }
@@ -783,4 +839,50 @@ extern "C" int orc_scores_d64_simd(const float * q, const float * k, int n, floa
 
 extern "C" void orc_scores_d64(const float * q, const float * k, int n, float scale, float * sc) {
     scores_d64_lanes(q, k, n, scale, sc);
+}
+
+namespace {
+
+// tanh256 on AVX2 + FMA, to check orc_tanh_ref's reading of ANDNOT / OR / BLENDV / CMP_LT_OQ.
+__attribute__((target("avx2,fma")))
+__m256 exp256_avx2(__m256 x) {
+    x = _mm256_min_ps(x, _mm256_set1_ps(88.3762626647949f));
+    x = _mm256_max_ps(x, _mm256_set1_ps(-87.3f));
+    const __m256 fn = _mm256_round_ps(_mm256_mul_ps(x, _mm256_set1_ps(1.44269504088896341f)),
+                                      _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+    x = _mm256_fnmadd_ps(fn, _mm256_set1_ps(0.693359375f), x);
+    x = _mm256_fnmadd_ps(fn, _mm256_set1_ps(-2.12194440e-4f), x);
+    const __m256 x2 = _mm256_mul_ps(x, x);
+    __m256 p = _mm256_set1_ps(EXP_P[0]);
+    for (int k = 1; k < 6; ++k) p = _mm256_fmadd_ps(p, x, _mm256_set1_ps(EXP_P[k]));
+    p = _mm256_fmadd_ps(p, x2, _mm256_add_ps(x, _mm256_set1_ps(1.0f)));
+    const __m256i e = _mm256_slli_epi32(_mm256_add_epi32(_mm256_cvtps_epi32(fn), _mm256_set1_epi32(127)), 23);
+    return _mm256_mul_ps(p, _mm256_castsi256_ps(e));
+}
+
+__attribute__((target("avx2,fma")))
+void tanh_avx2(const float * x, int64_t n, float * out) {
+    const __m256 sign = _mm256_set1_ps(-0.0f), one = _mm256_set1_ps(1.0f);
+    for (int64_t i = 0; i + 8 <= n; i += 8) {
+        const __m256 v = _mm256_loadu_ps(x + i);
+        const __m256 ax = _mm256_andnot_ps(sign, v);
+        const __m256 t = exp256_avx2(_mm256_mul_ps(ax, _mm256_set1_ps(-2.0f)));
+        __m256 big = _mm256_div_ps(_mm256_sub_ps(one, t), _mm256_add_ps(one, t));
+        big = _mm256_or_ps(big, _mm256_and_ps(sign, v));
+        const __m256 v2 = _mm256_mul_ps(v, v);
+        __m256 p = _mm256_set1_ps(-17.0f / 315.0f);
+        p = _mm256_fmadd_ps(p, v2, _mm256_set1_ps(2.0f / 15.0f));
+        p = _mm256_fmadd_ps(p, v2, _mm256_set1_ps(-1.0f / 3.0f));
+        p = _mm256_fmadd_ps(p, v2, one);
+        const __m256 small = _mm256_mul_ps(p, v);
+        _mm256_storeu_ps(out + i, _mm256_blendv_ps(big, small, _mm256_cmp_ps(ax, _mm256_set1_ps(0.1f), _CMP_LT_OQ)));
+    }
+}
+
+} // namespace
+
+extern "C" int orc_tanh_simd(const float * x, int64_t n, float * out) {
+    if (n % 8 != 0 || !__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma")) return -1;
+    tanh_avx2(x, n, out);
+    return 0;
 }

@@ -64,6 +64,10 @@ def lib() -> ctypes.CDLL:
         L.orc_attention.argtypes = [P, P, P, P, i32, P, i32, i32, i32, i32, P]
         L.orc_attention.restype = None
         L.orc_expf_rows.argtypes, L.orc_expf_rows.restype = [P, i64, P], None
+        L.orc_tanh_rows.argtypes, L.orc_tanh_rows.restype = [P, i64, P], None
+        L.orc_tanh_simd.argtypes, L.orc_tanh_simd.restype = [P, i64, P], i32
+        L.orc_qk_prep.argtypes = [P, P, P, P, P, P, i32, i32, i32, i32, i32, P]
+        L.orc_qk_prep.restype = None
         L.orc_expf_restated_check.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, P, i32]
         L.orc_expf_restated_check.restype = i64
         L.orc_scores_d64.argtypes, L.orc_scores_d64.restype = [P, P, i32, ctypes.c_float, P], None
@@ -223,6 +227,32 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_offsets, scale, n_
     assert sc.size == cu.size - 1
     out = np.empty_like(q)
     lib().orc_attention(_p(q), _p(k), _p(v), _p(cu), cu.size - 1, _p(sc), T, n_head, n_kv_head, half, _p(out))
+    return out
+
+
+def tanh_ref(x: np.ndarray, simd: bool = False) -> np.ndarray:
+    """tanh256 (src/nexterabert.cpp:103-117) element by element; simd: on AVX2 + FMA (size % 8 == 0)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    if simd:
+        if lib().orc_tanh_simd(_p(x), x.size, _p(out)) != 0:
+            raise RuntimeError("AVX2/FMA not available or size % 8 != 0")
+    else:
+        lib().orc_tanh_rows(_p(x), x.size, _p(out))
+    return out
+
+
+def qk_prep(x, alpha, beta, cos_t, sin_t, cu_offsets, n_head: int, head_major: bool = False) -> np.ndarray:
+    """op_qk_prep (src/nexterabert.cpp:590-632): DyT then RoPE; x [T][H*D]."""
+    x, cu = _f32_rows(x), _cu(cu_offsets)
+    T, width = x.shape
+    D = width // n_head
+    a, b = np.ascontiguousarray(alpha, np.float32), np.ascontiguousarray(beta, np.float32)
+    c, s = _f32_rows(cos_t), _f32_rows(sin_t)
+    assert a.shape == b.shape == (D,) and c.shape[1] == D // 2 and s.shape == c.shape and cu[-1] == T
+    assert int(np.diff(cu).max()) <= c.shape[0]
+    out = np.empty((n_head, T, D) if head_major else (T, width), np.float32)
+    lib().orc_qk_prep(_p(x), _p(a), _p(b), _p(c), _p(s), _p(cu), cu.size - 1, T, n_head, D, int(head_major), _p(out))
     return out
 
 

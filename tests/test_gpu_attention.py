@@ -102,3 +102,28 @@ def test_attention_document_alone(nxg, torch, dev):
     lo, hi = 33, 133
     alone = run(nxg, torch, q[lo:hi], k[:, lo:hi], v[:, lo:hi], [0, 100], scale[1:2], H, G, -1)
     assert (bits(alone) == bits(y[lo:hi])).all()
+
+
+@pytest.mark.parametrize("head_major", [False, True])
+def test_qk_prep_matches_oracle(nxg, orc, torch, dev, head_major):
+    say(f"qk_prep head_major={head_major}")
+    rng = np.random.default_rng(20 + head_major)
+    H, D = 16, 64
+    lengths = [1, 7, 100, 33]
+    cu = nxg.cu_offsets_of(lengths)
+    T = int(cu[-1])
+    x = (rng.standard_normal((T, H * D)) * np.exp(rng.uniform(-6, 3, (T, 1)))).astype(np.float32)
+    x.flat[rng.integers(0, x.size, 50)] = np.array([0.0, -0.0, 0.1, -0.1, 30.0, -1e-30], np.float32)[rng.integers(0, 6, 50)]
+    alpha = rng.uniform(0.2, 2.0, D).astype(np.float32)
+    beta = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    c, s = nxg.rope_table(128, 10000.0, D)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    y = nxg.qk_prep(t(x), t(alpha), t(beta), t(c), t(s), cu, H, head_major=head_major).cpu().numpy()
+    assert (bits(y) == bits(orc.qk_prep(x, alpha, beta, c, s, cu, H, head_major=head_major))).all()
+
+
+def test_head_major(nxg, torch, dev):
+    say("head_major")
+    x = torch.randn(77, 8 * 64, device="cuda")
+    y = nxg.head_major(x, 8)
+    assert torch.equal(y, x.view(77, 8, 64).permute(1, 0, 2).contiguous())

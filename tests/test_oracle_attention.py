@@ -137,3 +137,73 @@ def test_attention_scales_helper(nxg):
     assert np.allclose(s, base * (np.float32(0.5) * ln), rtol=0, atol=1e-7)
     s3 = nxg.attention_scales(cu, 64, nxg.SSMAX_SSSMAX, s=0.5, b=-1.0, ssmax_base=0.1)
     assert s3[0] == base * np.float32(0.1)           # ln 1 = 0, max(b, 0) = 0
+
+
+# --- tanh256 / op_qk_prep / build_rope ---------------------------------------------
+
+def test_tanh_scalar_equals_avx2_and_is_tanh(orc):
+    import math
+    rng = np.random.default_rng(11)
+    specials = [0.0, -0.0, 0.1, -0.1, 0.09999999, -0.09999999, np.nan, np.inf, -np.inf, 20.0, -20.0, 1e-30, 3e38, -3e38]
+    x = np.concatenate([rng.standard_normal(200_000) * 3, specials]).astype(np.float32)
+    x = np.concatenate([x, np.zeros((-x.size) % 8, np.float32)])
+    y = orc.tanh_ref(x)
+    try:
+        ys = orc.tanh_ref(x, simd=True)
+    except RuntimeError:
+        ys = None
+    if ys is not None:
+        nan = np.isnan(y) & np.isnan(ys)
+        assert ((bits(y) == bits(ys)) | nan).all()
+    fin = np.isfinite(x)
+    assert (bits(orc.tanh_ref(-x[fin])) == bits(-y[fin])).all()          # odd, bit for bit
+    t = np.abs(x) < 15
+    ref = np.tanh(x[t].astype(np.float64))
+    assert np.max(np.abs(y[t] - ref) / np.maximum(np.abs(ref), 1e-30)) < 8 * 2.0 ** -24   # (1-t)/(1+t) near 0.1
+    assert bits(orc.tanh_ref(np.array([-0.0], np.float32)))[0] == 0x80000000
+    assert orc.tanh_ref(np.array([20.0], np.float32))[0] == 1.0
+    # MINPS returns its second operand for a NaN, so exp256 clamps NaN to 88.38: t = inf-ish,
+    # (1 - t) / (1 + t) = -1, and the NaN's sign bit is ORed in (NaN is not < 0.1: big is taken)
+    assert orc.tanh_ref(np.array([np.nan], np.float32))[0] == -1.0
+    assert not math.isnan(orc.tanh_ref(np.array([np.nan], np.float32))[0])
+
+
+def test_rope_table(nxg):
+    c, s = nxg.rope_table(300, 10000.0, 64)
+    assert c.shape == s.shape == (300, 32)
+    assert (c[0] == 1.0).all() and (s[0] == 0.0).all()
+    inv = 1.0 / (10000.0 ** (np.arange(32) * 2 / 64.0))
+    a = np.arange(300)[:, None] * inv[None, :]
+    assert np.max(np.abs(c - np.cos(a))) < 1e-4 and np.max(np.abs(s - np.sin(a))) < 1e-4
+
+
+def test_qk_prep_closed_forms(orc, nxg):
+    rng = np.random.default_rng(12)
+    H, D = 4, 64
+    cu = np.array([0, 3, 40], np.int32)
+    x = rng.standard_normal((40, H * D)).astype(np.float32)
+    alpha = rng.uniform(0.2, 2.0, D).astype(np.float32)
+    beta = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    c, s = nxg.rope_table(64, 10000.0, D)
+    y = orc.qk_prep(x, alpha, beta, c, s, cu, H)
+    # DyT terms
+    a = beta[None, :32] * orc.tanh_ref(alpha[None, :32] * x.reshape(40, H, D)[:, :, :32])
+    b = beta[None, 32:] * orc.tanh_ref(alpha[None, 32:] * x.reshape(40, H, D)[:, :, 32:])
+    yr = y.reshape(40, H, D)
+    # position 0 of each document: cos 1, sin 0 -> (a, b) exactly
+    for t in (0, 3):
+        assert (bits(yr[t, :, :32]) == bits(a[t])).all() and (bits(yr[t, :, 32:]) == bits(b[t])).all()
+    # any position: y1 = fma(a, cos, b sin), y2 = fma(-a, sin, b cos), each rounded once
+    t, pos = 17, 14
+    for h in range(H):
+        for i in range(32):
+            ai, bi, ci, si = float(a[t, h, i]), float(b[t, h, i]), float(c[pos, i]), float(s[pos, i])
+            assert bits(np.float32(X.fma(ai, ci, X.mul(bi, si)))) == bits(yr[t, h, i])
+            assert bits(np.float32(X.fma(-ai, si, X.mul(bi, ci)))) == bits(yr[t, h, 32 + i])
+    # a rotation: each pair keeps its length (up to rounding)
+    n0 = a ** 2 + b ** 2
+    n1 = yr[:, :, :32].astype(np.float64) ** 2 + yr[:, :, 32:].astype(np.float64) ** 2
+    assert np.max(np.abs(n1 - n0) / n0) < 1e-5
+    # head-major is the same values, [H][T][D]
+    yh = orc.qk_prep(x, alpha, beta, c, s, cu, H, head_major=True)
+    assert (bits(yh) == bits(yr.transpose(1, 0, 2))).all()
