@@ -211,6 +211,49 @@ NXG_API int32_t nxg_qk_prep(const float * x, const float * alpha, const float * 
 NXG_API int32_t nxg_head_major(const float * x, int32_t T, int32_t n_head, int32_t head_dim, float * out,
                                void * stream);
 
+/* op_dwconv writing fp32 rows (src/nexterabert.cpp:524-543, row_op(..., false): HRA's qkv_conv
+ * and c_o, :1252, :1265): out = r (or 0 with r null), then out = fma(taps[j], x[t + j - k/2], out)
+ * for the taps j whose row lies in t's document, in order of j.
+ *   x, r       device float [T][C] (C % 4 == 0; 16-byte aligned)
+ *   taps       device float [k][C] (the loader's per-tap rows, :1703-1710)
+ *   cu_offsets device int32 [n_seqs + 1]
+ *   out        device float [T][C] */
+NXG_API int32_t nxg_dwconv_rows(const float * x, const float * r, const float * taps, int32_t k,
+                                const int32_t * cu_offsets, int32_t n_seqs, int32_t T, int32_t C, float * out,
+                                void * stream);
+
+/* op_upsample_add (src/nexterabert.cpp:675-690): out[t] = yb[cu_blocks[d] + (t - cu_offsets[d]) / block]
+ * + r[t] for row t of document d.
+ *   yb   device float [n_blocks][C] (one row per block of `block` tokens, per document)
+ *   r    device float [T][C];  cu_offsets, cu_blocks device int32 [n_seqs + 1];  out [T][C] */
+NXG_API int32_t nxg_upsample_add(const float * yb, const float * r, const int32_t * cu_offsets,
+                                 const int32_t * cu_blocks, int32_t n_seqs, int32_t T, int32_t n_blocks,
+                                 int32_t block, int32_t C, float * out, void * stream);
+
+/* The encoder's input rows (src/nexterabert.cpp:1271-1272): ggml_get_rows of the embedding,
+ * plus the segment embedding's row (ggml_add) when type_table is given.
+ *   table       device float [n_vocab][C] (a block-quantized file table decoded once)
+ *   ids         device int32 [T] (checked on the host: an id outside the table is clamped)
+ *   type_table  device float [n_types][C] or null;  types  device int32 [T]
+ *   out         device float [T][C] */
+NXG_API int32_t nxg_embed_rows(const float * table, int32_t n_vocab, const int32_t * ids, const float * type_table,
+                               int32_t n_types, const int32_t * types, int32_t T, int32_t C, float * out,
+                               void * stream);
+
+/* ggml_norm then ggml_mul by w and ggml_add of b (the encoder's out_norm, src/nexterabert.cpp:
+ * 1290-1291; the heads' transform, :1296-1297, has no b). ggml (v0.9.9) is not in the reference's
+ * tree: mean and variance are taken in double as its CPU op publishes them, in a fixed lane order.
+ *   x  device float [T][C];  w, b  device float [C] or null;  out  device float [T][C] */
+NXG_API int32_t nxg_layer_norm(const float * x, const float * w, const float * b, float eps, int32_t T, int32_t C,
+                               float * out, void * stream);
+
+/* nextera_encode's pooled output (src/nexterabert.cpp:1913-1925) and op_doc_mean (:659-672): the
+ * sum of each document's rows in row order, times 1 / n, or with normalize != 0 times
+ * 1 / sqrt(dot_f32(p, p)) (0 for a zero vector; C % 32 == 0, C <= 16384).
+ *   x  device float [T][C];  cu_offsets device int32 [n_seqs + 1];  out  device float [n_seqs][C] */
+NXG_API int32_t nxg_doc_mean(const float * x, const int32_t * cu_offsets, int32_t n_seqs, int32_t T, int32_t C,
+                             int32_t normalize, float * out, void * stream);
+
 /* build_rope (src/nexterabert.cpp:1322-1338) on the host with the same C library calls:
  * cos / sin of t * (1 / base^(2i / head_dim)) for t < n_pos, i < head_dim / 2.
  *   cos_out, sin_out  host float [n_pos][head_dim / 2] */

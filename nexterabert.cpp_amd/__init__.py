@@ -79,6 +79,11 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_attention_scales": ([P, i32, i32, i32, ctypes.c_float, ctypes.c_float, ctypes.c_float, P], i32),
         "nxg_qk_prep": ([P, P, P, P, P, i32, P, i32, i32, i32, i32, i32, P, P], i32),
         "nxg_head_major": ([P, i32, i32, i32, P, P], i32),
+        "nxg_dwconv_rows": ([P, P, P, i32, P, i32, i32, i32, P, P], i32),
+        "nxg_upsample_add": ([P, P, P, P, i32, i32, i32, i32, i32, P, P], i32),
+        "nxg_embed_rows": ([P, i32, P, P, i32, P, i32, i32, P, P], i32),
+        "nxg_layer_norm": ([P, P, P, ctypes.c_float, i32, i32, P, P], i32),
+        "nxg_doc_mean": ([P, P, i32, i32, i32, i32, P, P], i32),
         "nxg_rope_table": ([i32, ctypes.c_float, i32, P, P], i32),
         "nxg_qact_export": ([P, P, i32, i32, i32, P, P, P], i32),
         "nxg_weight_create": ([P, P, i32, i32, ctypes.POINTER(P)], i32),
@@ -506,6 +511,101 @@ def head_major(x, n_head: int, out=None, stream=None):
     if out is None:
         out = torch.empty((n_head, T, D), dtype=torch.float32, device=x.device)
     _check(load_library().nxg_head_major(x.data_ptr(), T, n_head, D, out.data_ptr(), _stream_ptr(stream)), "head_major")
+    return out
+
+
+def dwconv_rows(x, taps, cu_offsets, r=None, out=None, stream=None):
+    """op_dwconv as fp32 rows: r (or 0) + the depthwise convolution of x with taps [k][C]
+    inside each document of the packed batch."""
+    torch = _torch()
+    _rows_arg(x, "x")
+    T, C = x.shape
+    _rows_arg(taps, "taps")
+    if taps.shape[1] != C:
+        raise ValueError(f"taps must be [k][{C}]")
+    if r is not None:
+        _rows_arg(r, "r", (T, C))
+    cu = _device_offsets(cu_offsets, x.device)
+    if out is None:
+        out = torch.empty_like(x)
+    _check(load_library().nxg_dwconv_rows(x.data_ptr(), r.data_ptr() if r is not None else None, taps.data_ptr(),
+                                          taps.shape[0], cu.data_ptr(), cu.numel() - 1, T, C, out.data_ptr(),
+                                          _stream_ptr(stream)), "dwconv_rows")
+    return out
+
+
+def upsample_add(yb, r, cu_offsets, block: int, out=None, stream=None):
+    """op_upsample_add: every token row of r plus its block's row of yb (ceil(len / block)
+    block rows per document, in order)."""
+    torch = _torch()
+    _rows_arg(r, "r")
+    T, C = r.shape
+    _rows_arg(yb, "yb")
+    cu_host = np.ascontiguousarray(cu_offsets, dtype=np.int32)
+    cub_host = block_offsets(cu_host, block)
+    if yb.shape != (int(cub_host[-1]), C):
+        raise ValueError(f"yb must be [{int(cub_host[-1])}][{C}]")
+    cu, cub = _device_offsets(cu_host, r.device), _device_offsets(cub_host, r.device)
+    if out is None:
+        out = torch.empty_like(r)
+    _check(load_library().nxg_upsample_add(yb.data_ptr(), r.data_ptr(), cu.data_ptr(), cub.data_ptr(), cu.numel() - 1,
+                                           T, yb.shape[0], block, C, out.data_ptr(), _stream_ptr(stream)),
+           "upsample_add")
+    return out
+
+
+def embed_rows(table, ids, type_table=None, types=None, out=None, stream=None):
+    """The encoder's input rows: table[ids] (+ type_table[types]). table [n_vocab][C] fp32,
+    ids / types int32 device tensors [T]."""
+    torch = _torch()
+    _rows_arg(table, "table")
+    n_vocab, C = table.shape
+    if ids.dtype != torch.int32 or ids.dim() != 1 or not ids.is_cuda or not ids.is_contiguous():
+        raise ValueError("ids must be a contiguous int32 device tensor [T]")
+    T = ids.numel()
+    n_types = 0
+    if type_table is not None:
+        _rows_arg(type_table, "type_table")
+        n_types = type_table.shape[0]
+        if type_table.shape[1] != C or types is None or types.dtype != torch.int32 or types.numel() != T:
+            raise ValueError("type_table must be [n_types][C] with int32 types [T]")
+    if out is None:
+        out = torch.empty((T, C), dtype=torch.float32, device=table.device)
+    _check(load_library().nxg_embed_rows(table.data_ptr(), n_vocab, ids.data_ptr(),
+                                         type_table.data_ptr() if type_table is not None else None, n_types,
+                                         types.data_ptr() if type_table is not None else None, T, C, out.data_ptr(),
+                                         _stream_ptr(stream)), "embed_rows")
+    return out
+
+
+def layer_norm(x, w=None, b=None, eps: float = 1e-5, out=None, stream=None):
+    """ggml_norm of each row, then * w and + b (either may be None)."""
+    torch = _torch()
+    _rows_arg(x, "x")
+    T, C = x.shape
+    for name, t in (("w", w), ("b", b)):
+        if t is not None and (t.dtype != torch.float32 or tuple(t.shape) != (C,) or not t.is_cuda or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous float32 device tensor [{C}]")
+    if out is None:
+        out = torch.empty_like(x)
+    _check(load_library().nxg_layer_norm(x.data_ptr(), w.data_ptr() if w is not None else None,
+                                         b.data_ptr() if b is not None else None, eps, T, C, out.data_ptr(),
+                                         _stream_ptr(stream)), "layer_norm")
+    return out
+
+
+def doc_mean(x, cu_offsets, normalize: bool = False, out=None, stream=None):
+    """Per-document mean of the rows (normalize: the sum scaled to unit L2 norm), as
+    nextera_encode's pooled output."""
+    torch = _torch()
+    _rows_arg(x, "x")
+    T, C = x.shape
+    cu = _device_offsets(cu_offsets, x.device)
+    n = cu.numel() - 1
+    if out is None:
+        out = torch.empty((n, C), dtype=torch.float32, device=x.device)
+    _check(load_library().nxg_doc_mean(x.data_ptr(), cu.data_ptr(), n, T, C, 1 if normalize else 0, out.data_ptr(),
+                                       _stream_ptr(stream)), "doc_mean")
     return out
 
 

@@ -41,6 +41,7 @@ constexpr int WBN = 256;         // relu^2 -> int8 GEMM tile columns: one 256-in
 constexpr int WTHREADS = 512;    // relu^2 -> int8 GEMM: 8 waves, 2 x 4, each 64 x 64
 constexpr int N_XCD = 8;         // MI355X: 8 XCDs, workgroups dispatched round-robin
 #define NXG_ATTN_MAX_KEYS 16384          // keys per query the attention's LDS holds (64 KiB)
+#define NXG_DOC_MEAN_MAX_C 16384         // columns the normalized document mean keeps in LDS (64 KiB)
 #ifndef NXG_WG_PER_CU
 #define NXG_WG_PER_CU 2          // persistent GEMM workgroups per CU (0: one workgroup per tile)
 #endif
@@ -276,29 +277,18 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict_
     else                 quantize_block<ACT_MAX>(in, T, n_in, KS, n_blk, q, sx, g, B, stage);
 }
 
-// op_rms_norm feeding an int8 linear (src/nexterabert.cpp:463-482 through for_rows'
-// quantize_row, :414-438): one workgroup per 16-row group. First each row's
-// dot_f32(x, x) exactly as the reference's AVX2 code orders it (:124-149): 32 FMA
-// chains, chain a taking elements 32m + a (lane c of the row runs chains 2c and 2c+1),
-// then (s0 + s1) + (s2 + s3) lane-wise (chains 8k + j are accumulator s_k, lane j), then
-// hsum256: lanes j and j+4, then 0+2 and 1+3, then those two -- each step a shuffle
-// within the row's 16 lanes (fp32 addition is commutative, so either operand order gives
-// the same bits). inv = 1 / sqrt(dot / C + eps), correctly rounded. Then every block is
-// re-read and quantized as (x * inv) * gain. C % 32 == 0, so the reference's remainder
-// loops never run.
-template <int ACT_MAX>
-__global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(const float * __restrict__ x, const float * __restrict__ gain,
-                                                               float eps, int T, int n_in, int KS, int n_blk,
-                                                               int8_t * __restrict__ q, float * __restrict__ sx) {
-    __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
-    const int g = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t = g * 16 + wave * 4 + (lane >> 4);
-    const int c = lane & 15;
+// dot_f32(x, x) over a row of n floats (n % 32 == 0) in the reference's AVX2 order
+// (src/nexterabert.cpp:124-149), on the 16 lanes c = 0..15 of a lane group (xr null: the
+// row does not exist, the lanes still join the shuffles). 32 FMA chains, chain a taking
+// elements 32m + a (lane c runs chains 2c and 2c+1); then (s0 + s1) + (s2 + s3) lane-wise
+// (chains 8k + j are accumulator s_k, lane j); then hsum256: lanes j and j+4, then 0+2
+// and 1+3, then those two. fp32 addition is commutative, so both lanes of a shuffle pair
+// get the same bits and every lane of the group returns the dot.
+__device__ __forceinline__ float dot_sq_ref16(const float * xr, int n, int c) {
     float a0 = 0.0f, a1 = 0.0f;                // chains 2c and 2c + 1
-    if (t < T) {
-        const float * xr = x + (size_t) t * n_in + 2 * c;
-        for (int m = 0; m < n_in / 32; ++m) {
+    if (xr) {
+        xr += 2 * c;
+        for (int m = 0; m < n / 32; ++m) {
             const float2 v = *reinterpret_cast<const float2 *>(xr + 32 * m);
             a0 = __builtin_fmaf(v.x, v.x, a0);
             a1 = __builtin_fmaf(v.y, v.y, a1);
@@ -313,7 +303,24 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(const float * __r
     a1 = a1 + __shfl_xor(a1, 2);
     a0 = a0 + __shfl_xor(a0, 1);               // (v0+v4) + (v2+v6), (v1+v5) + (v3+v7)
     a1 = a1 + __shfl_xor(a1, 1);
-    const float dot = a0 + a1;
+    return a0 + a1;
+}
+
+// op_rms_norm feeding an int8 linear (src/nexterabert.cpp:463-482 through for_rows'
+// quantize_row, :414-438): one workgroup per 16-row group, 16 lanes per row. Each row's
+// dot_f32(x, x) in the reference's order (dot_sq_ref16), inv = 1 / sqrt(dot / C + eps)
+// correctly rounded, then every block re-read and quantized as (x * inv) * gain. C % 32
+// == 0, so the reference's remainder loops never run.
+template <int ACT_MAX>
+__global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(const float * __restrict__ x, const float * __restrict__ gain,
+                                                               float eps, int T, int n_in, int KS, int n_blk,
+                                                               int8_t * __restrict__ q, float * __restrict__ sx) {
+    __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
+    const int g = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = g * 16 + wave * 4 + (lane >> 4);
+    const int c = lane & 15;
+    const float dot = dot_sq_ref16(t < T ? x + (size_t) t * n_in : nullptr, n_in, c);
     const float inv = 1.0f / __builtin_sqrtf(dot / (float) n_in + eps);
     for (int B = 0; B < n_blk; ++B) {
         quantize_block<ACT_MAX>(src_rms{src_rows{x, n_in}, gain, inv}, T, n_in, KS, n_blk, q, sx, g, B, stage);
@@ -697,6 +704,136 @@ __global__ __launch_bounds__(256) void head_major_kernel(const float * __restric
     const int h = (int) ((idx / D) % H);
     const int t = (int) (idx / ((size_t) D * H));
     out[((size_t) h * T + t) * D + e] = x[idx];
+}
+
+// ---------------------------------------------------------------------------
+// Row ops writing fp32 rows (consumers that are not int8 linears, and the output)
+// ---------------------------------------------------------------------------
+
+// The rows a source produces as fp32 [T][C] (C % 4 == 0): 2^lg lanes per row, 4 columns
+// per lane per step, 256 >> lg rows per workgroup.
+template <typename Src>
+__global__ __launch_bounds__(256) void produce_rows_kernel(Src src, int T, int C, int lg, float * __restrict__ out) {
+    const int t = (int) blockIdx.x * (256 >> lg) + (int) (threadIdx.x >> lg);
+    const int lane = (int) threadIdx.x & ((1 << lg) - 1);
+    if (t >= T) return;
+    const auto r = src.row(t);
+    for (int col = 4 * lane; col < C; col += 4 << lg) {
+        float v[4];
+        src.load(r, t, col, v);
+        *reinterpret_cast<v4f *>(out + (size_t) t * C + col) = v4f{ v[0], v[1], v[2], v[3] };
+    }
+}
+
+// op_upsample_add (src/nexterabert.cpp:675-690): out[t] = yb[b] + r[t] with b = cub[d] +
+// (t - cu[d]) / block the block row of t in its document d (clamped into the block rows).
+struct src_upsample_add {
+    const float * yb;
+    const float * r;
+    const int32_t * cu;
+    const int32_t * cub;
+    int n_seqs, T, n_blocks, C, block;
+    __device__ int row(int t) const {
+        const doc_rows d = doc_of(cu, n_seqs, t, T);
+        return min(max(cub[d.d] + (t - d.lo) / block, 0), n_blocks - 1);
+    }
+    __device__ void load(int b, int t, int col, float (&v)[4]) const {
+        const v4f y = *reinterpret_cast<const v4f *>(yb + (size_t) b * C + col);
+        const v4f rv = *reinterpret_cast<const v4f *>(r + (size_t) t * C + col);
+        v[0] = y.x + rv.x; v[1] = y.y + rv.y; v[2] = y.z + rv.z; v[3] = y.w + rv.w;
+    }
+};
+
+// ggml_get_rows of the embedding (src/nexterabert.cpp:1271-1272) from a table held in
+// fp32 (a block-quantized table is decoded once at load, the values to_float gives), plus
+// the segment embedding's row where given (ggml_add: one fp32 addition). Ids are clamped
+// into the tables so that any ids read in bounds; the host rejects bad ids first.
+__global__ __launch_bounds__(256) void embed_rows_kernel(const float * __restrict__ table, int n_vocab,
+                                                         const int32_t * __restrict__ ids,
+                                                         const float * __restrict__ type_table, int n_types,
+                                                         const int32_t * __restrict__ types, int T, int C, int lg,
+                                                         float * __restrict__ out) {
+    const int t = (int) blockIdx.x * (256 >> lg) + (int) (threadIdx.x >> lg);
+    const int lane = (int) threadIdx.x & ((1 << lg) - 1);
+    if (t >= T) return;
+    const float * er = table + (size_t) min(max(ids[t], 0), n_vocab - 1) * C;
+    const float * tr = type_table ? type_table + (size_t) min(max(types[t], 0), n_types - 1) * C : nullptr;
+    for (int col = 4 * lane; col < C; col += 4 << lg) {
+        v4f e = *reinterpret_cast<const v4f *>(er + col);
+        if (tr) e = e + *reinterpret_cast<const v4f *>(tr + col);
+        *reinterpret_cast<v4f *>(out + (size_t) t * C + col) = e;
+    }
+}
+
+// ggml_norm (ggml v0.9.9's CPU op; ggml is not in the reference's tree) then ggml_mul by w
+// and ggml_add of b (src/nexterabert.cpp:1290-1291, :1296-1297): mean = (float) sum(x) /
+// C; v = x - mean; variance = (float) (sum((double) (v * v)) / C); y = v * (1 / sqrtf(
+// variance + eps)); out = y * w + b, each operation rounded on its own. The sums are taken
+// in double by one wave per row: lane l adds elements l + 64 j in order of j, then a
+// butterfly over the 64 lanes (the same order in the oracle).
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float * __restrict__ x, const float * __restrict__ w,
+                                                         const float * __restrict__ b, float eps, int T, int C,
+                                                         float * __restrict__ out) {
+    const int t = (int) blockIdx.x * 4 + (int) (threadIdx.x >> 6), lane = (int) threadIdx.x & 63;
+    if (t >= T) return;                        // uniform across the wave
+    const float * xr = x + (size_t) t * C;
+    double s = 0.0;
+    for (int i = lane; i < C; i += 64) s += (double) xr[i];
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+    const float mean = (float) s / (float) C;
+    double s2 = 0.0;
+    for (int i = lane; i < C; i += 64) {
+        const float v = xr[i] - mean;
+        s2 += (double) (v * v);
+    }
+    for (int m = 32; m >= 1; m >>= 1) s2 += __shfl_xor(s2, m);
+    const float variance = (float) (s2 / (double) C);
+    const float scale = 1.0f / __builtin_sqrtf(variance + eps);
+    float * o = out + (size_t) t * C;
+    for (int i = lane; i < C; i += 64) {
+        float y = (xr[i] - mean) * scale;
+        if (w) y = y * w[i];
+        if (b) y = y + b[i];
+        o[i] = y;
+    }
+}
+
+// The pooled vector of nextera_encode (src/nexterabert.cpp:1913-1925) and op_doc_mean
+// (:659-672): the sum of the document's rows in row order (axpy_f32 with weight 1, one
+// rounding per row) times 1 / n -- or, with normalize, times 1 / sqrt(dot_f32(p, p)) (0
+// for a zero vector; dot in the reference's order, C % 32 == 0). One workgroup per
+// document, 4 columns per thread per step; with normalize the sums are kept in LDS
+// (dynamic, C floats) for the dot.
+__global__ __launch_bounds__(256) void doc_mean_kernel(const float * __restrict__ x, const int32_t * __restrict__ cu,
+                                                       int T, int C, int normalize, float * __restrict__ out) {
+    extern __shared__ float pooled[];
+    __shared__ float scale_s;
+    const int d = (int) blockIdx.x;
+    const int lo = min(max(cu[d], 0), T), hi = min(max(cu[d + 1], lo), T);
+    float * o = out + (size_t) d * C;
+    for (int col = 4 * (int) threadIdx.x; col < C; col += 1024) {
+        v4f acc = { 0.0f, 0.0f, 0.0f, 0.0f };
+        for (int t = lo; t < hi; ++t) acc = acc + *reinterpret_cast<const v4f *>(x + (size_t) t * C + col);
+        *reinterpret_cast<v4f *>(o + col) = acc;
+        if (normalize) *reinterpret_cast<v4f *>(pooled + col) = acc;
+    }
+    float scale = 1.0f / (float) (hi - lo);
+    if (normalize) {
+        __syncthreads();
+        if (threadIdx.x < 16) {
+            const float dot = dot_sq_ref16(pooled, C, (int) threadIdx.x);
+            if (threadIdx.x == 0) {
+                const float nrm = __builtin_sqrtf(dot);
+                scale_s = nrm > 0.0f ? 1.0f / nrm : 0.0f;
+            }
+        }
+        __syncthreads();
+        scale = scale_s;
+    }
+    for (int col = 4 * (int) threadIdx.x; col < C; col += 1024) {
+        const v4f a = *reinterpret_cast<const v4f *>(o + col);
+        *reinterpret_cast<v4f *>(o + col) = v4f{ a.x * scale, a.y * scale, a.z * scale, a.w * scale };
+    }
 }
 
 // int8 tiles -> the reference's u8 rows (q + act_off); one thread per 16 bytes.
@@ -1886,6 +2023,30 @@ static int32_t launch_produce(const char * what, const Src & src, int32_t T, int
     return launch_check(what);
 }
 
+// Lanes per row of the fp32 row kernels: the largest power of two <= min(64, C / 4).
+static int row_lanes_log2(int C) {
+    int lg = 0;
+    while (lg < 6 && (4 << (lg + 1)) <= C) ++lg;
+    return lg;
+}
+
+static bool aligned16(const void * p) { return ((uintptr_t) p & 15u) == 0; }
+
+// A producer's rows written as fp32: shared checks and launch.
+template <typename Src>
+static int32_t launch_rows(const char * what, const Src & src, int32_t T, int32_t C, float * out, void * stream) {
+    if (T < 0 || C < 4 || C % 4 != 0) return fail(NXG_EINVAL, "%s: T=%d C=%d (C must be a positive multiple of 4)", what, T, C);
+    if (T == 0) return NXG_OK;
+    if (!out || !aligned16(out)) return fail(NXG_EINVAL, "%s: output null or not 16-byte aligned", what);
+    int rc = check_device();
+    if (rc) return rc;
+    const int lg = row_lanes_log2(C);
+    const int rows_per_wg = 256 >> lg;
+    const unsigned grid = (unsigned) ((T + rows_per_wg - 1) / rows_per_wg);
+    produce_rows_kernel<Src><<<grid, 256, 0, (hipStream_t) stream>>>(src, T, C, lg, out);
+    return launch_check(what);
+}
+
 extern "C" {
 
 int32_t nxg_init(void) { return check_device(); }
@@ -2032,6 +2193,75 @@ int32_t nxg_head_major(const float * x, int32_t T, int32_t n_head, int32_t head_
     if (rc) return rc;
     head_major_kernel<<<(unsigned) ((n + 255) / 256), 256, 0, (hipStream_t) stream>>>(x, T, n_head, head_dim, out);
     return launch_check("head_major_kernel");
+}
+
+int32_t nxg_dwconv_rows(const float * x, const float * r, const float * taps, int32_t k, const int32_t * cu_offsets,
+                        int32_t n_seqs, int32_t T, int32_t C, float * out, void * stream) {
+    if (T > 0 && (!x || !taps || !cu_offsets)) return fail(NXG_EINVAL, "dwconv_rows: null input");
+    if (k < 1 || n_seqs < 1) return fail(NXG_EINVAL, "dwconv_rows: k=%d n_seqs=%d (both must be >= 1)", k, n_seqs);
+    if (T > 0 && (!aligned16(x) || !aligned16(taps) || (r && !aligned16(r)))) {
+        return fail(NXG_EINVAL, "dwconv_rows: inputs must be 16-byte aligned");
+    }
+    return launch_rows("dwconv_rows", src_dwconv{x, r, taps, cu_offsets, n_seqs, T, C, k}, T, C, out, stream);
+}
+
+int32_t nxg_upsample_add(const float * yb, const float * r, const int32_t * cu_offsets, const int32_t * cu_blocks,
+                         int32_t n_seqs, int32_t T, int32_t n_blocks, int32_t block, int32_t C, float * out,
+                         void * stream) {
+    if (block < 1 || n_seqs < 1 || (T > 0 && n_blocks < 1)) {
+        return fail(NXG_EINVAL, "upsample_add: block=%d n_seqs=%d n_blocks=%d", block, n_seqs, n_blocks);
+    }
+    if (T > 0 && (!yb || !r || !cu_offsets || !cu_blocks)) return fail(NXG_EINVAL, "upsample_add: null input");
+    if (T > 0 && (!aligned16(yb) || !aligned16(r))) return fail(NXG_EINVAL, "upsample_add: inputs must be 16-byte aligned");
+    return launch_rows("upsample_add", src_upsample_add{yb, r, cu_offsets, cu_blocks, n_seqs, T, n_blocks, C, block},
+                       T, C, out, stream);
+}
+
+int32_t nxg_embed_rows(const float * table, int32_t n_vocab, const int32_t * ids, const float * type_table,
+                       int32_t n_types, const int32_t * types, int32_t T, int32_t C, float * out, void * stream) {
+    if (T < 0 || C < 4 || C % 4 != 0 || n_vocab < 1 || (type_table && n_types < 1)) {
+        return fail(NXG_EINVAL, "embed_rows: T=%d C=%d n_vocab=%d n_types=%d", T, C, n_vocab, n_types);
+    }
+    if (T == 0) return NXG_OK;
+    if (!table || !ids || !out || (type_table && !types)) return fail(NXG_EINVAL, "embed_rows: null buffer");
+    if (!aligned16(table) || !aligned16(out) || (type_table && !aligned16(type_table))) {
+        return fail(NXG_EINVAL, "embed_rows: tables and output must be 16-byte aligned");
+    }
+    int rc = check_device();
+    if (rc) return rc;
+    const int lg = row_lanes_log2(C);
+    const int rows_per_wg = 256 >> lg;
+    embed_rows_kernel<<<(unsigned) ((T + rows_per_wg - 1) / rows_per_wg), 256, 0, (hipStream_t) stream>>>(
+        table, n_vocab, ids, type_table, n_types, types, T, C, lg, out);
+    return launch_check("embed_rows_kernel");
+}
+
+int32_t nxg_layer_norm(const float * x, const float * w, const float * b, float eps, int32_t T, int32_t C, float * out,
+                       void * stream) {
+    if (T < 0 || C < 1) return fail(NXG_EINVAL, "layer_norm: T=%d C=%d", T, C);
+    if (T == 0) return NXG_OK;
+    if (!x || !out) return fail(NXG_EINVAL, "layer_norm: null buffer");
+    int rc = check_device();
+    if (rc) return rc;
+    layer_norm_kernel<<<(unsigned) ((T + 3) / 4), 256, 0, (hipStream_t) stream>>>(x, w, b, eps, T, C, out);
+    return launch_check("layer_norm_kernel");
+}
+
+int32_t nxg_doc_mean(const float * x, const int32_t * cu_offsets, int32_t n_seqs, int32_t T, int32_t C, int32_t normalize,
+                     float * out, void * stream) {
+    if (n_seqs < 0 || T < 0 || C < 4 || C % 4 != 0) return fail(NXG_EINVAL, "doc_mean: n_seqs=%d T=%d C=%d", n_seqs, T, C);
+    if (normalize && (C % 32 != 0 || C > NXG_DOC_MEAN_MAX_C)) {
+        return fail(NXG_EINVAL, "doc_mean: normalize needs C a multiple of 32 and <= %d, got %d", NXG_DOC_MEAN_MAX_C, C);
+    }
+    if (n_seqs == 0) return NXG_OK;
+    if (!x || !cu_offsets || !out || !aligned16(x) || !aligned16(out)) {
+        return fail(NXG_EINVAL, "doc_mean: null or unaligned buffer");
+    }
+    int rc = check_device();
+    if (rc) return rc;
+    const size_t lds = normalize ? (size_t) C * sizeof(float) : 0;
+    doc_mean_kernel<<<(unsigned) n_seqs, 256, lds, (hipStream_t) stream>>>(x, cu_offsets, T, C, normalize ? 1 : 0, out);
+    return launch_check("doc_mean_kernel");
 }
 
 int32_t nxg_qact_export(const int8_t * q, const float * sx, int32_t T, int32_t n_in, int32_t act_max,

@@ -339,6 +339,80 @@ void orc_lily_state_rows(const float * a, const float * x, const float * b, cons
     }
 }
 
+// op_upsample_add (src/nexterabert.cpp:675-690): row t of document d gets yb[cub[d] + (t -
+// cu[d]) / block] + r[t].
+void orc_upsample_add(const float * yb, const float * r, const int32_t * cu, const int32_t * cub, int n_seqs,
+                      int block, int C, float * out) {
+    for (int d = 0; d < n_seqs; ++d) {
+        for (int t = cu[d]; t < cu[d + 1]; ++t) {
+            const float * y = yb + (size_t) (cub[d] + (t - cu[d]) / block) * C;
+            const float * rr = r + (size_t) t * C;
+            float * o = out + (size_t) t * C;
+            for (int c = 0; c < C; ++c) o[c] = y[c] + rr[c];
+        }
+    }
+}
+
+// ggml_norm (ggml v0.9.9's CPU op, published as: mean = (float) sum / n with the sum in
+// double; v = x - mean; variance = (float) (sum of (double) (v * v) / n); y = v * (1 /
+// sqrtf(variance + eps))) then ggml_mul by w and ggml_add of b (src/nexterabert.cpp:
+// 1290-1291), each rounded on its own. ggml is not in the reference's tree, so the order
+// of the double sums is this build's: 64 partial sums, partial l taking elements l + 64 j
+// in order of j, then combined pairwise l + (l ^ m) for m = 32, 16, ..., 1.
+static double lane_sum64(const double (&p)[64]) {
+    double s[64];
+    for (int l = 0; l < 64; ++l) s[l] = p[l];
+    for (int m = 32; m >= 1; m >>= 1) {
+        double n[64];
+        for (int l = 0; l < 64; ++l) n[l] = s[l] + s[l ^ m];
+        for (int l = 0; l < 64; ++l) s[l] = n[l];
+    }
+    return s[0];
+}
+
+void orc_layer_norm(const float * x, const float * w, const float * b, float eps, int T, int C, float * out) {
+    for (int t = 0; t < T; ++t) {
+        const float * xr = x + (size_t) t * C;
+        double p[64] = {};
+        for (int i = 0; i < C; ++i) p[i % 64] += (double) xr[i];
+        const float mean = (float) lane_sum64(p) / (float) C;
+        double p2[64] = {};
+        for (int i = 0; i < C; ++i) {
+            const float v = xr[i] - mean;
+            p2[i % 64] += (double) (v * v);
+        }
+        const float variance = (float) (lane_sum64(p2) / (double) C);
+        const float scale = 1.0f / std::sqrt(variance + eps);
+        float * o = out + (size_t) t * C;
+        for (int i = 0; i < C; ++i) {
+            float y = (xr[i] - mean) * scale;
+            if (w) y = y * w[i];
+            if (b) y = y + b[i];
+            o[i] = y;
+        }
+    }
+}
+
+// nextera_encode's pooled vectors (src/nexterabert.cpp:1913-1925), op_doc_mean (:659-672):
+// per document the sum of its rows in order, then times 1 / n, or (normalize) times 1 /
+// sqrt(dot_f32(p, p)), 0 for a zero vector.
+void orc_doc_mean(const float * x, const int32_t * cu, int n_seqs, int C, int normalize, float * out) {
+    for (int d = 0; d < n_seqs; ++d) {
+        float * o = out + (size_t) d * C;
+        for (int c = 0; c < C; ++c) o[c] = 0.0f;
+        for (int t = cu[d]; t < cu[d + 1]; ++t) {
+            const float * xr = x + (size_t) t * C;
+            for (int c = 0; c < C; ++c) o[c] = std::fma(1.0f, xr[c], o[c]);
+        }
+        float scale = 1.0f / (float) (cu[d + 1] - cu[d]);
+        if (normalize) {
+            const float nrm = std::sqrt(dot_avx2_order(o, o, C));
+            scale = nrm > 0.0f ? 1.0f / nrm : 0.0f;
+        }
+        for (int c = 0; c < C; ++c) o[c] *= scale;
+    }
+}
+
 // op_block_mean (src/nexterabert.cpp:638-659): per document, runs of `block` tokens
 // (the last one shorter), out = 0, out = fma(h, g, out) per token (out + h without g),
 // then out * (1 / n). Output rows: ceil(len / block) per document, in order.

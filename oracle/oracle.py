@@ -61,6 +61,10 @@ def lib() -> ctypes.CDLL:
         L.orc_dwconv_rows.argtypes, L.orc_dwconv_rows.restype = [P, P, P, i32, P, i32, i32, P], None
         L.orc_lily_state_rows.argtypes, L.orc_lily_state_rows.restype = [P, P, P, P, i32, P, i32, i32, P], None
         L.orc_block_mean_rows.argtypes, L.orc_block_mean_rows.restype = [P, P, P, i32, i32, i32, P], None
+        L.orc_upsample_add.argtypes, L.orc_upsample_add.restype = [P, P, P, P, i32, i32, i32, P], None
+        L.orc_layer_norm.argtypes = [P, P, P, ctypes.c_float, i32, i32, P]
+        L.orc_layer_norm.restype = None
+        L.orc_doc_mean.argtypes, L.orc_doc_mean.restype = [P, P, i32, i32, i32, P], None
         L.orc_attention.argtypes = [P, P, P, P, i32, P, i32, i32, i32, i32, P]
         L.orc_attention.restype = None
         L.orc_expf_rows.argtypes, L.orc_expf_rows.restype = [P, i64, P], None
@@ -213,6 +217,42 @@ def block_mean(h: np.ndarray, cu_offsets, block: int, g: np.ndarray = None) -> n
     n_rows = int(sum((int(n) + block - 1) // block for n in np.diff(cu)))
     out = np.empty((n_rows, C), np.float32)
     lib().orc_block_mean_rows(_p(h), _p(g), _p(cu), cu.size - 1, block, C, _p(out))
+    return out
+
+
+def upsample_add(yb: np.ndarray, r: np.ndarray, cu_offsets, block: int) -> np.ndarray:
+    """op_upsample_add (src/nexterabert.cpp:675-690): each token row gets its block row of yb
+    (ceil(len / block) rows per document, in order) added to r."""
+    yb, r, cu = _f32_rows(yb), _f32_rows(r), _cu(cu_offsets)
+    T, C = r.shape
+    lens = np.diff(cu)
+    cub = np.concatenate([[0], np.cumsum((lens + block - 1) // block)]).astype(np.int32)
+    assert cu[-1] == T and yb.shape == (int(cub[-1]), C)
+    out = np.empty_like(r)
+    lib().orc_upsample_add(_p(yb), _p(r), _p(cu), _p(cub), cu.size - 1, block, C, _p(out))
+    return out
+
+
+def layer_norm(x: np.ndarray, w: np.ndarray = None, b: np.ndarray = None, eps: float = 1e-5) -> np.ndarray:
+    """ggml_norm, then * w and + b (src/nexterabert.cpp:1290-1291); sums in double in a fixed
+    lane order (ggml's own order is not in the reference's tree)."""
+    x = _f32_rows(x)
+    T, C = x.shape
+    w = None if w is None else np.ascontiguousarray(w, np.float32)
+    b = None if b is None else np.ascontiguousarray(b, np.float32)
+    out = np.empty_like(x)
+    lib().orc_layer_norm(_p(x), _p(w), _p(b), eps, T, C, _p(out))
+    return out
+
+
+def doc_mean(x: np.ndarray, cu_offsets, normalize: bool = False) -> np.ndarray:
+    """Per-document mean of the rows (or L2-normalised sum) as nextera_encode pools
+    (src/nexterabert.cpp:1913-1925)."""
+    x, cu = _f32_rows(x), _cu(cu_offsets)
+    T, C = x.shape
+    assert cu[-1] == T
+    out = np.empty((cu.size - 1, C), np.float32)
+    lib().orc_doc_mean(_p(x), _p(cu), cu.size - 1, C, 1 if normalize else 0, _p(out))
     return out
 
 
