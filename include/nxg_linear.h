@@ -97,7 +97,7 @@ NXG_API int32_t nxg_expand_weight(int32_t type, const void * data, int32_t n_in,
                                   int32_t act_off, int32_t n_threads,
                                   int8_t * w, float * scale, int32_t * off);
 
-/* Encodes n_rows rows of n_in f32 values as Q8_0, Q4_K or Q6_K GGUF blocks into
+/* Encodes n_rows rows of n_in f32 values as Q8_0, Q5_0, Q4_K or Q6_K GGUF blocks into
  * nxg_row_bytes(type, n_in) * n_rows bytes at `out`. For synthetic weight files; the
  * reference's own quantizer is ggml's (tools/quantize.cpp:201-213), whose search for
  * K-quant scales this one-pass encoder does not reproduce. */

@@ -47,6 +47,11 @@ class NxgError(RuntimeError):
     pass
 
 
+class EncoderParams(ctypes.Structure):
+    """struct nxg_encoder_params (include/nxg_encoder.h)."""
+    _fields_ = [("act_max", ctypes.c_int32), ("load_threads", ctypes.c_int32), ("verbosity", ctypes.c_int32)]
+
+
 def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     """Loads libnxg.so (built by build.py); raises if it is missing."""
     global _lib
@@ -84,6 +89,17 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_embed_rows": ([P, i32, P, P, i32, P, i32, i32, P, P], i32),
         "nxg_layer_norm": ([P, P, P, ctypes.c_float, i32, i32, P, P], i32),
         "nxg_doc_mean": ([P, P, i32, i32, i32, i32, P, P], i32),
+        "nxg_encoder_load": ([ctypes.c_char_p, ctypes.POINTER(EncoderParams), ctypes.POINTER(P)], i32),
+        "nxg_encoder_free": ([P], None),
+        "nxg_encoder_n_embd": ([P], i32),
+        "nxg_encoder_n_vocab": ([P], i32),
+        "nxg_encoder_n_layer": ([P], i32),
+        "nxg_encoder_n_token_types": ([P], i32),
+        "nxg_encoder_device_bytes": ([P], sz),
+        "nxg_encoder_set_layers": ([P, i32], None),
+        "nxg_encoder_encode": ([P, P, P, P, i32, P, P, i32], i32),
+        "nxg_encoder_forward": ([P, P, P, P, i32, P, P, i32, P], i32),
+        "nxg_encoder_last_ms": ([P], ctypes.c_double),
         "nxg_rope_table": ([i32, ctypes.c_float, i32, P, P], i32),
         "nxg_qact_export": ([P, P, i32, i32, i32, P, P, P], i32),
         "nxg_weight_create": ([P, P, i32, i32, ctypes.POINTER(P)], i32),
@@ -163,7 +179,7 @@ def dequantize_rows(type_: int, data: np.ndarray, n_in: int, n_rows: int) -> np.
 
 
 def quantize_weight(type_: int, x: np.ndarray) -> np.ndarray:
-    """Encodes f32 rows [n_rows][n_in] as GGUF blocks (Q8_0, Q4_K or Q6_K)."""
+    """Encodes f32 rows [n_rows][n_in] as GGUF blocks (Q8_0, Q5_0, Q4_K or Q6_K)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     n_rows, n_in = x.shape
     rb = row_bytes(type_, n_in)
@@ -818,6 +834,105 @@ class GGUF:
                    f"gguf_weight_create({name})")
             out[name] = DeviceWeight(None, handle=h)
         return out
+
+
+class Encoder:
+    """The encoder on the GPU (include/nxg_encoder.h): nextera_load of a GGUF file, then
+    nextera_encode / nextera_encode_segments of packed batches (src/nexterabert.cpp:1861-1935).
+
+    encode() takes and returns host arrays; forward() runs on device tensors without
+    synchronising (for timing and for callers that keep activations on the GPU)."""
+
+    def __init__(self, path: os.PathLike, act_max: int = 127, load_threads: int = 0, verbosity: int = 0):
+        L = load_library()
+        self._h = None
+        params = EncoderParams(act_max, load_threads, verbosity)
+        h = ctypes.c_void_p()
+        _check(L.nxg_encoder_load(os.fsencode(str(path)), ctypes.byref(params), ctypes.byref(h)), "encoder_load")
+        self._h = h
+
+    def close(self) -> None:
+        if self._h is not None:
+            load_library().nxg_encoder_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def n_embd(self) -> int:
+        return load_library().nxg_encoder_n_embd(self._h)
+
+    @property
+    def n_vocab(self) -> int:
+        return load_library().nxg_encoder_n_vocab(self._h)
+
+    @property
+    def n_layer(self) -> int:
+        return load_library().nxg_encoder_n_layer(self._h)
+
+    @property
+    def n_token_types(self) -> int:
+        return load_library().nxg_encoder_n_token_types(self._h)
+
+    @property
+    def device_bytes(self) -> int:
+        return int(load_library().nxg_encoder_device_bytes(self._h))
+
+    @property
+    def last_ms(self) -> float:
+        return float(load_library().nxg_encoder_last_ms(self._h))
+
+    def set_layers(self, n_layers: int) -> None:
+        """Run only the first n_layers blocks, returning the residual stream (-1: all)."""
+        load_library().nxg_encoder_set_layers(self._h, n_layers)
+
+    def encode(self, tokens, lengths, token_types=None, hidden: bool = True, pooled: bool = False,
+               normalize: bool = False):
+        """Host arrays in, host arrays out: (hidden [sum(lengths)][n_embd] or None,
+        pooled [n_seqs][n_embd] or None)."""
+        tok = np.ascontiguousarray(tokens, dtype=np.int32)
+        lens = np.ascontiguousarray(lengths, dtype=np.int32)
+        typ = None if token_types is None else np.ascontiguousarray(token_types, dtype=np.int32)
+        if typ is not None and typ.size != tok.size:
+            raise ValueError("token_types must have one id per token")
+        if lens.size == 0 or int(lens.sum()) != tok.size:
+            raise ValueError("lengths must sum to the number of tokens")
+        C = self.n_embd
+        h = np.empty((tok.size, C), np.float32) if hidden else None
+        p = np.empty((lens.size, C), np.float32) if pooled else None
+        _check(load_library().nxg_encoder_encode(self._h, _np_ptr(tok), _np_ptr(typ), _np_ptr(lens), lens.size,
+                                                 _np_ptr(h), _np_ptr(p), 1 if normalize else 0), "encoder_encode")
+        return h, p
+
+    def forward(self, tokens, lengths, token_types=None, hidden=None, pooled=None, normalize: bool = False,
+                stream=None):
+        """Device int32 tokens (and types) in; writes the device tensors hidden [T][n_embd]
+        and / or pooled [n_seqs][n_embd] that are given."""
+        torch = _torch()
+        lens = np.ascontiguousarray(lengths, dtype=np.int32)
+        T, C = int(lens.sum()), self.n_embd
+        for name, t in (("tokens", tokens), ("token_types", token_types)):
+            if t is not None and (t.dtype != torch.int32 or t.numel() != T or not t.is_cuda or not t.is_contiguous()):
+                raise ValueError(f"{name} must be a contiguous int32 device tensor of {T} ids")
+        if hidden is not None:
+            _check_rows(hidden, T, C, "hidden")
+        if pooled is not None:
+            _check_rows(pooled, lens.size, C, "pooled")
+        _check(load_library().nxg_encoder_forward(
+            self._h, tokens.data_ptr(), token_types.data_ptr() if token_types is not None else None, _np_ptr(lens),
+            lens.size, hidden.data_ptr() if hidden is not None else None,
+            pooled.data_ptr() if pooled is not None else None, 1 if normalize else 0, _stream_ptr(stream)),
+            "encoder_forward")
 
 
 def cu_offsets_of(lengths: Sequence[int]) -> np.ndarray:

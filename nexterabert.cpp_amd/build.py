@@ -78,6 +78,9 @@ def build(verbose: bool = False) -> Path:
     hip_only = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
     _run(["g++", *common, "-pthread", "-c", CSRC / "nxg_host.cpp", "-o", OBJ / "nxg_host.o"], verbose)
     _run(["g++", *common, "-c", CSRC / "nxg_gguf.cpp", "-o", OBJ / "nxg_gguf.o"], verbose)
+    rocm = Path(_hipcc()).resolve().parent.parent
+    _run(["g++", *common, "-D__HIP_PLATFORM_AMD__", f"-I{rocm / 'include'}", "-c", CSRC / "nxg_encoder.cpp",
+          "-o", OBJ / "nxg_encoder.o"], verbose)
     cmd = [str(c) for c in (_hipcc(), *hip_only, *common, "-Rpass-analysis=kernel-resource-usage",
                             "-c", CSRC / "nxg_linear.hip", "-o", OBJ / "nxg_linear.o")]
     if verbose:
@@ -89,10 +92,9 @@ def build(verbose: bool = False) -> Path:
     (OBJ / "kernel_resources.txt").write_text(_check_resources(r.stderr) + "\n")
     tmp = LIB.with_suffix(".so.tmp")
     _run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread",
-          OBJ / "nxg_linear.o", OBJ / "nxg_host.o", OBJ / "nxg_gguf.o", "-o", tmp], verbose)
+          OBJ / "nxg_linear.o", OBJ / "nxg_host.o", OBJ / "nxg_gguf.o", OBJ / "nxg_encoder.o", "-o", tmp], verbose)
     os.replace(tmp, LIB)
     # the C++ driver over the C ABI (nxg-cli: --info, --bench), linked against libnxg.so
-    rocm = Path(_hipcc()).resolve().parent.parent
     _run(["g++", "-O2", "-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}", f"-I{rocm / 'include'}",
           CSRC / "nxg_cli.cpp", "-o", CLI, f"-L{PKG}", "-lnxg", f"-L{rocm / 'lib'}", "-lamdhip64",
           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{rocm / 'lib'}"], verbose)

@@ -323,6 +323,32 @@ void enc_q8_0(const float * x, uint8_t * b) {
     for (int j = 0; j < 32; ++j) b[2 + j] = (uint8_t) (int8_t) std::lround(std::min(127.0f, std::max(-127.0f, x[j] * id)));
 }
 
+// Q5_0 from the published block format: d = m / -16 with m the element of largest
+// magnitude (its sign kept), q = min(31, trunc(x / d + 16.5)) split into a low nibble and
+// a high bit; decodes as (q - 16) * d.
+void enc_q5_0(const float * x, uint8_t * b) {
+    float amax = 0.0f, m = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+        if (std::fabs(x[j]) > amax) {
+            amax = std::fabs(x[j]);
+            m = x[j];
+        }
+    }
+    const float d = m / -16.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t h = float_to_half(d);
+    b[0] = (uint8_t) h;
+    b[1] = (uint8_t) (h >> 8);
+    uint32_t qh = 0;
+    for (int j = 0; j < 16; ++j) {
+        const int q0 = std::min(31, (int) (int8_t) (x[j] * id + 16.5f));
+        const int q1 = std::min(31, (int) (int8_t) (x[j + 16] * id + 16.5f));
+        b[6 + j] = (uint8_t) ((q0 & 0x0f) | ((q1 & 0x0f) << 4));
+        qh |= (uint32_t) ((q0 >> 4) & 1) << j;
+        qh |= (uint32_t) ((q1 >> 4) & 1) << (j + 16);
+    }
+    std::memcpy(b + 2, &qh, 4);
+}
+
 void put_scale_min_k4(int j, int sc, int mn, uint8_t * s) {
     if (j < 4) {
         s[j] = (uint8_t) ((s[j] & 0xc0) | sc);
@@ -512,9 +538,10 @@ int32_t nxg_quantize_weight(int32_t type, const float * x, int64_t n_in, int64_t
     int blck = 0, bytes = 0;
     switch (type) {
         case NXG_TYPE_Q8_0: enc = enc_q8_0; blck = 32; bytes = 34; break;
+        case NXG_TYPE_Q5_0: enc = enc_q5_0; blck = 32; bytes = 22; break;
         case NXG_TYPE_Q4_K: enc = enc_q4_k; blck = 256; bytes = 144; break;
         case NXG_TYPE_Q6_K: enc = enc_q6_k; blck = 256; bytes = 210; break;
-        default: return host_fail(NXG_EINVAL, "quantize_weight: only Q8_0, Q4_K and Q6_K are encoded");
+        default: return host_fail(NXG_EINVAL, "quantize_weight: only Q8_0, Q5_0, Q4_K and Q6_K are encoded");
     }
     uint8_t * o = (uint8_t *) out;
     for (int64_t r = 0; r < n_rows; ++r) {

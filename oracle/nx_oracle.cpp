@@ -413,6 +413,34 @@ void orc_doc_mean(const float * x, const int32_t * cu, int n_seqs, int C, int no
     }
 }
 
+// The scale op_attention applies to one document of n keys (src/nexterabert.cpp:1196-1201):
+// 1 / sqrt(head_dim) times builder::ssmax_scale (:1172-1181) -- 1 (mode 0: "none", or an
+// swa layer), s * ln n (mode 1), s * ln n + ssmax_base + max(b, 0) (mode 2), ln n =
+// logf(max(n, 1)). GCC's default contraction (the reference's -O3 -march=native build)
+// makes s * ln n + ssmax_base one fma.
+float orc_attention_scale(int n, int head_dim, int mode, float s, float b, float ssmax_base) {
+    const float base = 1.0f / std::sqrt((float) head_dim);
+    if (mode == 0) return base * 1.0f;
+    const float ln = std::log((float) std::max(n, 1));
+    const float f = mode == 1 ? s * ln : std::fma(s, ln, ssmax_base) + std::max(b, 0.0f);
+    return base * f;
+}
+
+// build_rope (src/nexterabert.cpp:1322-1338): cos / sin of t * (1 / base^(2i / head_dim)),
+// each step a float C library call or operation. out [n_pos][head_dim / 2].
+void orc_rope_table(int n_pos, float base, int head_dim, float * cos_out, float * sin_out) {
+    const int half = head_dim / 2;
+    std::vector<float> inv(half);
+    for (int i = 0; i < half; ++i) inv[i] = 1.0f / std::pow(base, (float) (2 * i) / (float) head_dim);
+    for (int t = 0; t < n_pos; ++t) {
+        for (int i = 0; i < half; ++i) {
+            const float a = (float) t * inv[i];
+            cos_out[(size_t) t * half + i] = std::cos(a);
+            sin_out[(size_t) t * half + i] = std::sin(a);
+        }
+    }
+}
+
 // op_block_mean (src/nexterabert.cpp:638-659): per document, runs of `block` tokens
 // (the last one shorter), out = 0, out = fma(h, g, out) per token (out + h without g),
 // then out * (1 / n). Output rows: ceil(len / block) per document, in order.

@@ -65,6 +65,9 @@ def lib() -> ctypes.CDLL:
         L.orc_layer_norm.argtypes = [P, P, P, ctypes.c_float, i32, i32, P]
         L.orc_layer_norm.restype = None
         L.orc_doc_mean.argtypes, L.orc_doc_mean.restype = [P, P, i32, i32, i32, P], None
+        L.orc_attention_scale.argtypes = [i32, i32, i32, ctypes.c_float, ctypes.c_float, ctypes.c_float]
+        L.orc_attention_scale.restype = ctypes.c_float
+        L.orc_rope_table.argtypes, L.orc_rope_table.restype = [i32, ctypes.c_float, i32, P, P], None
         L.orc_attention.argtypes = [P, P, P, P, i32, P, i32, i32, i32, i32, P]
         L.orc_attention.restype = None
         L.orc_expf_rows.argtypes, L.orc_expf_rows.restype = [P, i64, P], None
@@ -254,6 +257,20 @@ def doc_mean(x: np.ndarray, cu_offsets, normalize: bool = False) -> np.ndarray:
     out = np.empty((cu.size - 1, C), np.float32)
     lib().orc_doc_mean(_p(x), _p(cu), cu.size - 1, C, 1 if normalize else 0, _p(out))
     return out
+
+
+def attention_scale(n: int, head_dim: int, mode: int, s: float = 0.0, b: float = 0.0, ssmax_base: float = 0.1):
+    """op_attention's scale for a document of n keys (src/nexterabert.cpp:1172-1201);
+    mode 0 none / swa, 1 ssmax, 2 sssmax."""
+    return np.float32(lib().orc_attention_scale(n, head_dim, mode, s, b, ssmax_base))
+
+
+def rope_table(n_pos: int, base: float, head_dim: int):
+    """build_rope (src/nexterabert.cpp:1322-1338): (cos, sin) [n_pos][head_dim / 2]."""
+    c = np.empty((n_pos, head_dim // 2), np.float32)
+    s = np.empty_like(c)
+    lib().orc_rope_table(n_pos, base, head_dim, _p(c), _p(s))
+    return c, s
 
 
 def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_offsets, scale, n_head: int, n_kv_head: int,

@@ -1,0 +1,139 @@
+"""GPU: the whole encoder forward (include/nxg_encoder.h) bit for bit against the oracle's
+restatement (oracle/encoder.py) on random-init GGUF files written by synth.py:
+
+  * small models with every block type (SnowLily, sliding-window and full attention, HRA)
+    at n_embd 128 (the MLP's c_fc through fp32 rows, K-quants falling back to Q5_0) and 256
+    (c_fc -> relu^2 -> int8 fused), Q4_K_M and Q8_0, with segment embeddings, ragged
+    batches, one-token sequences and sequences shorter than an HRA block: hidden rows and
+    pooled vectors (mean and L2-normalised);
+  * a sequence alone gives its bits inside the batch; nxg_encoder_set_layers returns the
+    residual stream after the given block; the device-buffer entry point equals the host
+    one; bad ids and empty sequences are refused;
+  * the 213M-parameter model (18 blocks, Q4_K_M) on one 1,024-token sequence: hidden bit for
+    bit, and token cosine >= 0.99999 against the oracle.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "no GPU"
+    return t
+
+
+@pytest.fixture(scope="module")
+def synth(nxg):
+    from nexterabert_cpp_amd import synth as S
+    return S
+
+
+@pytest.fixture(scope="module")
+def enc():
+    from oracle import encoder as E
+    return E
+
+
+SMALL = {
+    "c128_q4km": dict(n_embd=128, n_inter=256, n_head=2, n_kv_head=1, preset="Q4_K_M"),
+    "c256_q8": dict(n_embd=256, n_inter=512, n_head=4, n_kv_head=2, preset="Q8_0"),
+}
+
+
+@pytest.fixture(scope="module")
+def small_models(nxg, synth, enc, tmp_path_factory):
+    out = {}
+    for key, cfg in SMALL.items():
+        cfg = dict(cfg)
+        preset = cfg.pop("preset")
+        d = synth.Dims(n_vocab=500, lily_rank=64, swa_window=8, n_types=2,
+                       block_types=["lily", "swa", "attn", "hra", "lily", "hra"], **cfg)
+        path = tmp_path_factory.mktemp("enc") / f"{key}.gguf"
+        synth.write_random_model(nxg, path, preset, seed=len(key), dims=d)
+        out[key] = (path, d, enc.from_gguf(nxg, path))
+    return out
+
+
+BATCHES = [[1], [7], [3, 1, 9, 33, 2], [130, 5, 64]]
+
+
+@pytest.mark.parametrize("key", list(SMALL))
+@pytest.mark.parametrize("lengths", BATCHES)
+def test_encoder_matches_oracle(nxg, enc, torch, small_models, key, lengths):
+    path, d, m = small_models[key]
+    say(f"encoder {key} lengths={lengths}")
+    rng = np.random.default_rng(sum(lengths))
+    T = sum(lengths)
+    tok = rng.integers(0, d.n_vocab, T).astype(np.int32)
+    typ = rng.integers(0, 2, T).astype(np.int32)
+    with nxg.Encoder(path) as e:
+        assert (e.n_embd, e.n_layer, e.n_vocab, e.n_token_types) == (d.n_embd, len(d.block_types), d.n_vocab, 2)
+        for types in (None, typ):
+            for normalize in (False, True):
+                h, p = e.encode(tok, lengths, types, pooled=True, normalize=normalize)
+                hr, pr = enc.encode(m, tok, lengths, types, normalize=normalize)
+                assert (bits(h) == bits(hr)).all(), f"hidden differs: types={types is not None}"
+                assert (bits(p) == bits(pr)).all(), f"pooled differs: normalize={normalize}"
+
+
+def test_encoder_batch_invariance_and_layers(nxg, enc, torch, small_models):
+    path, d, m = small_models["c256_q8"]
+    say("encoder batch invariance, set_layers, device entry point")
+    lengths = [40, 1, 17, 5]
+    cu = np.concatenate([[0], np.cumsum(lengths)])
+    rng = np.random.default_rng(5)
+    tok = rng.integers(0, d.n_vocab, cu[-1]).astype(np.int32)
+    with nxg.Encoder(path) as e:
+        h, p = e.encode(tok, lengths, pooled=True)
+        for i, n in enumerate(lengths):
+            hi, pi = e.encode(tok[cu[i]:cu[i + 1]], [n], pooled=True)
+            assert (bits(hi) == bits(h[cu[i]:cu[i + 1]])).all() and (bits(pi) == bits(p[i:i + 1])).all()
+        outs = []
+        enc.encode(m, tok, lengths, layer_outputs=outs)
+        for k in (1, 4):
+            e.set_layers(k)
+            hk, _ = e.encode(tok, lengths)
+            assert (bits(hk) == bits(outs[k - 1])).all()
+        e.set_layers(-1)
+        # the device entry point, on torch's stream
+        td = torch.from_numpy(tok).cuda()
+        hd = torch.empty((int(cu[-1]), d.n_embd), dtype=torch.float32, device="cuda")
+        pd = torch.empty((len(lengths), d.n_embd), dtype=torch.float32, device="cuda")
+        e.forward(td, lengths, hidden=hd, pooled=pd)
+        torch.cuda.synchronize()
+        assert (bits(hd.cpu().numpy()) == bits(h)).all() and (bits(pd.cpu().numpy()) == bits(p)).all()
+        with pytest.raises(ValueError):
+            e.encode(np.array([0, d.n_vocab], np.int32), [2])          # id out of range
+        with pytest.raises(ValueError):
+            e.encode(np.array([0, 1], np.int32), [2, 0])               # an empty sequence
+        assert e.last_ms > 0 and e.device_bytes > 0
+
+
+def test_encoder_full_model_1024(nxg, synth, enc, torch, tmp_path):
+    """The 213M-parameter model, Q4_K_M, one 1,024-token sequence of uniform random ids."""
+    say("encoder: full model (18 blocks, Q4_K_M), 1,024 tokens")
+    path = tmp_path / "full_q4km.gguf"
+    synth.write_random_model(nxg, path, "Q4_K_M", seed=0)
+    tok = np.random.default_rng(0).integers(0, 50368, 1024).astype(np.int32)
+    with nxg.Encoder(path) as e:
+        h, p = e.encode(tok, [1024], pooled=True)
+    say("encoder: oracle forward")
+    m = enc.from_gguf(nxg, path)
+    hr, pr = enc.encode(m, tok, [1024])
+    cos = np.sum(h.astype(np.float64) * hr, 1) / (np.linalg.norm(h.astype(np.float64), axis=1) * np.linalg.norm(hr, axis=1))
+    say(f"encoder: min token cosine {cos.min():.9f}")
+    assert cos.min() >= 0.99999
+    assert (bits(h) == bits(hr)).all() and (bits(p) == bits(pr)).all()
