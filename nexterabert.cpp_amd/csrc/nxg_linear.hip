@@ -307,7 +307,7 @@ __device__ __forceinline__ float dot_sq_ref16(const float * xr, int n, int c) {
 }
 
 // op_rms_norm feeding an int8 linear (src/nexterabert.cpp:463-482 through for_rows'
-// quantize_row, :414-438): one workgroup per 16-row group, 16 lanes per row. Each row's
+// quantize_row, :414-438): one workgroup per (16-row group, block), 16 lanes per row. Each row's
 // dot_f32(x, x) in the reference's order (dot_sq_ref16), inv = 1 / sqrt(dot / C + eps)
 // correctly rounded, then every block re-read and quantized as (x * inv) * gain. C % 32
 // == 0, so the reference's remainder loops never run.
@@ -316,16 +316,17 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(const float * __r
                                                                float eps, int T, int n_in, int KS, int n_blk,
                                                                int8_t * __restrict__ q, float * __restrict__ sx) {
     __shared__ __attribute__((aligned(16))) int stage[4 * FRAG / 4];
-    const int g = blockIdx.x;
+    // workgroup b runs on XCD b % 8: the n_blk workgroups of one row group share an XCD
+    // (and its L2, which serves their repeated reads of the rows for the dot)
+    const int xcd = (int) (blockIdx.x & 7u), slot = (int) (blockIdx.x >> 3);
+    const int g = (slot / n_blk) * 8 + xcd, B = slot % n_blk;
+    if (g * 16 >= T) return;                   // the padding of the grid to whole XCD rounds
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t = g * 16 + wave * 4 + (lane >> 4);
     const int c = lane & 15;
     const float dot = dot_sq_ref16(t < T ? x + (size_t) t * n_in : nullptr, n_in, c);
     const float inv = 1.0f / __builtin_sqrtf(dot / (float) n_in + eps);
-    for (int B = 0; B < n_blk; ++B) {
-        quantize_block<ACT_MAX>(src_rms{src_rows{x, n_in}, gain, inv}, T, n_in, KS, n_blk, q, sx, g, B, stage);
-        __syncthreads();                       // the stores have read the stage buffer
-    }
+    quantize_block<ACT_MAX>(src_rms{src_rows{x, n_in}, gain, inv}, T, n_in, KS, n_blk, q, sx, g, B, stage);
 }
 
 // ---------------------------------------------------------------------------
@@ -650,6 +651,226 @@ __global__ __launch_bounds__(64) void attention_kernel(attn_params p) {
     float acc = 0.0f;
     for (int j = 0; j < n; ++j) acc = __builtin_fmaf(sc[j] * inv, vh[(size_t) j * 64 + lane], acc);
     o[lane] = acc;
+}
+
+// The same attention for a tile of (query, head) pairs: the ATT_P pairs of one workgroup are
+// ATT_P / rep consecutive query rows times the rep query heads of one KV head, so that every
+// key and value row read into LDS serves all of them. Per pair the operations and their
+// order are attention_kernel's (the reference's scores_d64, softmax_exp, values_d64):
+//   scores    one thread per (pair, key): the 8 FMA chains (a_l = q[l] k[l], then
+//             fma(q[8c+l], k[8c+l], a_l) for c = 1..7) and the HADD tree (keys of whole
+//             groups of 8) or hsum256's (the last n % 8 keys) in registers, times the scale;
+//             kept in LDS, [pair][key - the pair's first key]
+//   softmax   16 threads per pair: the maximum (a NaN first score wins), exp256 / the C
+//             library's expf in place, then threads l < 8 add the keys 8i + l in order of i
+//             (the 8 lanes of softmax_exp's accumulator) and hsum256 over them, the tail keys
+//             added after; each weight becomes w * (1 / sum)
+//   values    thread (dim d, 4 pairs): acc = fma(w_j, v_j[d], acc) over the keys in order.
+// Keys are staged ATT_KT at a time ([key][ATT_KS] floats; the padding puts the 16 rows one
+// wave reads on different banks). Pairs whose keys exceed smax get NaN, as attention_kernel.
+constexpr int ATT_P = 16;      // (query, head) pairs per workgroup
+constexpr int ATT_KT = 32;     // keys per staged tile
+constexpr int ATT_KS = 68;     // floats per staged row
+
+__global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int smax) {
+    extern __shared__ __attribute__((aligned(16))) float att_lds[];
+    float * S = att_lds;                                   // [ATT_P][smax]
+    float * tile = att_lds + (size_t) ATT_P * smax;        // [ATT_KT][ATT_KS]
+    __shared__ int lo_s[ATT_P], hi_s[ATT_P];
+    __shared__ float scale_s[ATT_P], inv_s[ATT_P];
+    const int tid = (int) threadIdx.x;
+    const int rep = p.H / p.G, nq = ATT_P / rep;
+    const int n_qblk = (p.T + nq - 1) / nq;
+    const int g = (int) blockIdx.x / n_qblk, t0 = ((int) blockIdx.x - g * n_qblk) * nq;
+
+    if (tid < ATT_P) {
+        const int t = t0 + tid / rep;
+        int lo = 0, hi = 0;
+        float sc = 0.0f;
+        if (t < p.T) {
+            const doc_rows dr = doc_of(p.cu, p.n_seqs, t, p.T);
+            lo = dr.lo;
+            hi = dr.hi;
+            if (p.half >= 0) {
+                lo = max(lo, t - p.half);
+                hi = min(hi, t + p.half + 1);
+            }
+            sc = p.scale[dr.d];
+        }
+        lo_s[tid] = lo;
+        hi_s[tid] = hi;
+        scale_s[tid] = sc;
+    }
+    __syncthreads();
+    // keys any pair reads: [kl, kh)
+    int kl = INT_MAX, kh = INT_MIN;
+#pragma unroll
+    for (int i = 0; i < ATT_P; ++i) {
+        if (hi_s[i] > lo_s[i] && hi_s[i] - lo_s[i] <= smax) {
+            kl = min(kl, lo_s[i]);
+            kh = max(kh, hi_s[i]);
+        }
+    }
+    const float * kg = p.k + (size_t) g * p.T * 64;
+    const float * vg = p.v + (size_t) g * p.T * 64;
+
+    // scores: thread (pair sp, key slots sk and sk + 16 of each tile)
+    const int sp = tid >> 4, sk = tid & 15;
+    const int plo = lo_s[sp], n_p = hi_s[sp] - plo, ng_p = n_p & ~7;
+    const bool valid = n_p > 0 && n_p <= smax;
+    float qv[64];
+    {
+        const int t = t0 + sp / rep, h = g * rep + sp % rep;
+        const float * qr = p.q + (size_t) min(t, p.T - 1) * p.H * 64 + (size_t) h * 64;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const v4f f = *reinterpret_cast<const v4f *>(qr + 4 * i);
+            qv[4 * i] = f.x; qv[4 * i + 1] = f.y; qv[4 * i + 2] = f.z; qv[4 * i + 3] = f.w;
+        }
+    }
+    const float scale = scale_s[sp];
+    float * Sp = S + (size_t) sp * smax;
+    // staged rows: thread tid moves row (tid >> 4) + 16 r, floats 4 (tid & 15) .. + 3, r < 2;
+    // the next tile's rows are fetched into registers while the current one is scored
+    const int st_r = tid >> 4, st_c = 4 * (tid & 15);
+    v4f pre[2];
+    auto fetch = [&](const float * src, int j0) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int j = j0 + st_r + 16 * r;
+            pre[r] = j < kh ? *reinterpret_cast<const v4f *>(src + (size_t) j * 64 + st_c) : v4f{ 0.0f, 0.0f, 0.0f, 0.0f };
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) *reinterpret_cast<v4f *>(tile + (st_r + 16 * r) * ATT_KS + st_c) = pre[r];
+    };
+    if (kl < kh) fetch(kg, kl);
+    for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
+        __syncthreads();                                   // the previous tile has been read
+        stage();
+        __syncthreads();
+        if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int jr = j0 + sk + 16 * r - plo;
+            if (!valid || jr < 0 || jr >= n_p) continue;
+            const float * kp = tile + (sk + 16 * r) * ATT_KS;
+            float a[8];
+            {
+                const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
+                a[0] = qv[0] * k0.x; a[1] = qv[1] * k0.y; a[2] = qv[2] * k0.z; a[3] = qv[3] * k0.w;
+                a[4] = qv[4] * k1.x; a[5] = qv[5] * k1.y; a[6] = qv[6] * k1.z; a[7] = qv[7] * k1.w;
+            }
+#pragma unroll
+            for (int c = 1; c < 8; ++c) {
+                const v4f k0 = *reinterpret_cast<const v4f *>(kp + 8 * c);
+                const v4f k1 = *reinterpret_cast<const v4f *>(kp + 8 * c + 4);
+                a[0] = __builtin_fmaf(qv[8 * c + 0], k0.x, a[0]);
+                a[1] = __builtin_fmaf(qv[8 * c + 1], k0.y, a[1]);
+                a[2] = __builtin_fmaf(qv[8 * c + 2], k0.z, a[2]);
+                a[3] = __builtin_fmaf(qv[8 * c + 3], k0.w, a[3]);
+                a[4] = __builtin_fmaf(qv[8 * c + 4], k1.x, a[4]);
+                a[5] = __builtin_fmaf(qv[8 * c + 5], k1.y, a[5]);
+                a[6] = __builtin_fmaf(qv[8 * c + 6], k1.z, a[6]);
+                a[7] = __builtin_fmaf(qv[8 * c + 7], k1.w, a[7]);
+            }
+            const float tot = jr < ng_p ? ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))
+                                        : ((a[0] + a[4]) + (a[2] + a[6])) + ((a[1] + a[5]) + (a[3] + a[7]));
+            Sp[jr] = tot * scale;
+        }
+    }
+    __syncthreads();
+
+    // softmax: 16 threads per pair
+    if (valid) {
+        const float s0 = Sp[0];
+        float mx = -__builtin_inff();
+        for (int j = sk; j < n_p; j += 16) mx = fmaxf(mx, Sp[j]);
+#pragma unroll
+        for (int sft = 8; sft >= 1; sft >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sft));
+        const float m = __builtin_isnan(s0) ? s0 : mx;
+        for (int j = sk; j < n_p; j += 16) Sp[j] = j < ng_p ? exp_cephes(Sp[j] - m) : expf_libm(Sp[j] - m);
+    }
+    __syncthreads();
+    {
+        float ls = 0.0f;
+        if (valid && sk < 8) {
+            for (int j = sk; j < ng_p; j += 8) ls = ls + Sp[j];
+        }
+        ls = ls + __shfl_xor(ls, 4);                       // lanes 8..15 hold 0 and stay among themselves
+        ls = ls + __shfl_xor(ls, 2);
+        ls = ls + __shfl_xor(ls, 1);
+        if (valid && sk == 0) {
+            float sum = ls;
+            for (int j = ng_p; j < n_p; ++j) sum = sum + Sp[j];
+            inv_s[sp] = 1.0f / sum;
+        }
+    }
+    __syncthreads();
+    if (valid) {
+        const float inv = inv_s[sp];
+        for (int j = sk; j < n_p; j += 16) Sp[j] = Sp[j] * inv;
+    }
+
+    // values: thread (dim d, pairs 4 pg .. 4 pg + 3); pg is the wave's, so the pairs' key
+    // ranges are scalars and a key outside a pair's range costs a scalar branch
+    const int d = tid & 63, pg = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int vlo[4], vn[4];
+    float acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int pp = 4 * pg + i;
+        vlo[i] = __builtin_amdgcn_readfirstlane(lo_s[pp]);
+        vn[i] = __builtin_amdgcn_readfirstlane(hi_s[pp] - lo_s[pp]);
+        if (vn[i] > smax) vn[i] = 0;
+        acc[i] = 0.0f;
+    }
+    if (kl < kh) fetch(vg, kl);
+    for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
+        __syncthreads();                                   // weights written / previous tile read
+        stage();
+        __syncthreads();
+        if (j0 + ATT_KT < kh) fetch(vg, j0 + ATT_KT);
+        const int jn = min(ATT_KT, kh - j0);
+        int a[4], b[4];
+        bool full = jn == ATT_KT;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {                      // keys [a, b) of the tile are pair i's
+            a[i] = min(max(vlo[i] - j0, 0), jn);
+            b[i] = max(min(vlo[i] + vn[i] - j0, jn), a[i]);
+            full = full && a[i] == 0 && b[i] == jn;
+        }
+        const float * w0 = S + (size_t) (4 * pg + 0) * smax + (j0 - vlo[0]);
+        const float * w1 = S + (size_t) (4 * pg + 1) * smax + (j0 - vlo[1]);
+        const float * w2 = S + (size_t) (4 * pg + 2) * smax + (j0 - vlo[2]);
+        const float * w3 = S + (size_t) (4 * pg + 3) * smax + (j0 - vlo[3]);
+        if (full) {
+#pragma unroll 8
+            for (int jj = 0; jj < ATT_KT; ++jj) {
+                const float v = tile[jj * ATT_KS + d];
+                acc[0] = __builtin_fmaf(w0[jj], v, acc[0]);
+                acc[1] = __builtin_fmaf(w1[jj], v, acc[1]);
+                acc[2] = __builtin_fmaf(w2[jj], v, acc[2]);
+                acc[3] = __builtin_fmaf(w3[jj], v, acc[3]);
+            }
+        } else {
+            for (int jj = 0; jj < jn; ++jj) {
+                const float v = tile[jj * ATT_KS + d];
+                if (jj >= a[0] && jj < b[0]) acc[0] = __builtin_fmaf(w0[jj], v, acc[0]);
+                if (jj >= a[1] && jj < b[1]) acc[1] = __builtin_fmaf(w1[jj], v, acc[1]);
+                if (jj >= a[2] && jj < b[2]) acc[2] = __builtin_fmaf(w2[jj], v, acc[2]);
+                if (jj >= a[3] && jj < b[3]) acc[3] = __builtin_fmaf(w3[jj], v, acc[3]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int pp = 4 * pg + i, t = t0 + pp / rep, h = g * rep + pp % rep;
+        if (t >= p.T) continue;
+        const int n = hi_s[pp] - lo_s[pp];
+        p.out[(size_t) t * p.H * 64 + (size_t) h * 64 + d] = (n > 0 && n <= smax) ? acc[i] : __uint_as_float(0x7fc00000u);
+    }
 }
 
 // tanh256 (src/nexterabert.cpp:103-117) lane by lane: big = (1 - t) / (1 + t) with t =
@@ -2023,6 +2244,30 @@ static int32_t launch_produce(const char * what, const Src & src, int32_t T, int
     return launch_check(what);
 }
 
+// Dynamic LDS the tiled attention kernel may take on the current device: the device's
+// shared memory per workgroup less the kernel's static arrays, with the attribute that
+// allows more than the default raised to it once.
+static size_t attention_tile_lds_limit() {
+    static size_t limit = 0;
+    static bool done = false;
+    if (!done) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 1024) {
+            const size_t want = (size_t) v - 1024;           // static arrays of the kernel: 4 x ATT_P words
+            if (hipFuncSetAttribute((const void *) attention_tile_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int) want) == hipSuccess) {
+                limit = want;
+            } else {
+                (void) hipGetLastError();
+                limit = 65536 - 1024;
+            }
+        }
+        done = true;
+    }
+    return limit;
+}
+
 // Lanes per row of the fp32 row kernels: the largest power of two <= min(64, C / 4).
 static int row_lanes_log2(int C) {
     int lg = 0;
@@ -2103,7 +2348,9 @@ int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps
     if (!x || !gain || !q || !sx) return fail(NXG_EINVAL, "rmsnorm_quantize: null buffer");
     int rc = check_device();
     if (rc) return rc;
-    const dim3 grid((unsigned) (d.MP / 16));
+    const long long n_wg = (long long) ((d.MP / 16 + 7) / 8) * 8 * d.n_blk;   // (row group, block), whole XCD rounds
+    if (n_wg > INT32_MAX) return fail(NXG_EINVAL, "rmsnorm_quantize: T=%d n_in=%d too large", T, n_in);
+    const dim3 grid((unsigned) n_wg);
     hipStream_t s = (hipStream_t) stream;
     if (act_max == 127) rmsnorm_quantize_kernel<127><<<grid, 256, 0, s>>>(x, gain, eps, T, n_in, d.KS, d.n_blk, q, sx);
     else                rmsnorm_quantize_kernel<63><<<grid, 256, 0, s>>>(x, gain, eps, T, n_in, d.KS, d.n_blk, q, sx);
@@ -2162,6 +2409,15 @@ int32_t nxg_attention(const float * q, const float * k, const float * v, const i
     int rc = check_device();
     if (rc) return rc;
     attn_params p{q, k, v, cu_offsets, scale, out, n_seqs, T, n_head, n_kv_head, half < 0 ? -1 : half, max_keys};
+    // the tiled kernel when its LDS (scores of ATT_P pairs + one staged tile) fits a workgroup
+    const int rep = n_head / n_kv_head;
+    const int smax = (max_keys + 3) & ~3;
+    const size_t tile_lds = ((size_t) ATT_P * smax + (size_t) ATT_KT * ATT_KS) * sizeof(float);
+    if (ATT_P % rep == 0 && tile_lds <= attention_tile_lds_limit()) {
+        const long long n_tiles = (long long) n_kv_head * ((T + ATT_P / rep - 1) / (ATT_P / rep));
+        attention_tile_kernel<<<dim3((unsigned) n_tiles), dim3(256), tile_lds, (hipStream_t) stream>>>(p, smax);
+        return launch_check("attention_tile_kernel");
+    }
     attention_kernel<<<dim3((unsigned) n_wg), dim3(64), (size_t) max_keys * sizeof(float), (hipStream_t) stream>>>(p);
     return launch_check("attention_kernel");
 }
