@@ -18,7 +18,9 @@ included, 2 ops per MAC of the GEMMs); `roofline` describes the GEMM kernel from
 HIP events around every GEMM launch of the timed steps; `cpu_baseline` times the
 CPU oracle (the same path on VPDPBUSD, the reference's instruction) on a row
 sample on this host. The 1,024-token encoder line is the same path at M=1024,
-replayed from a HIP graph.
+replayed from a HIP graph; `encoder` times the whole encoder forward (nxg_encoder:
+embedding, every block, out_norm) on the 213M-parameter model at 1x1024 and 8x1024
+tokens, beside the reference's published CPU timings of the same calls.
 """
 from __future__ import annotations
 
@@ -111,6 +113,83 @@ def time_graph(path, steps: int, warmup: int):
     s1.record()
     torch.cuda.synchronize()
     return s0.elapsed_time(s1) / steps
+
+
+def time_encoder(nxg, steps: int, warmup: int, preset: str = "Q4_K_M"):
+    """The whole encoder (nxg_encoder) on the 213M-parameter model with random-init
+    weights written to a temporary GGUF file: one 1,024-token sequence and a batch of
+    8 of them, uniform random ids. Timed with HIP events on the launching stream,
+    launched eagerly and replayed from a HIP graph (each replay's output compared bit
+    for bit with the eager one, eager work between replays). tokens/s = 1000 T B /
+    median ms, the reference CLI's rule (tools/cli.cpp:188-203)."""
+    import tempfile
+    import torch
+    from nexterabert_cpp_amd import synth
+    out = {"model": f"NexteraBERT 213M (18 blocks: 8 lily, 5 swa, 3 attn, 2 hra), random init, {preset}",
+           "data": "synthetic (uniform random token ids)"}
+    with tempfile.TemporaryDirectory() as tmp:
+        path = Path(tmp) / "nexterabert_random.gguf"
+        t0 = time.perf_counter()
+        info = synth.write_random_model(nxg, path, preset, seed=0)
+        enc = nxg.Encoder(path)
+        log(f"encoder model: {info['n_params']} parameters written and loaded in {time.perf_counter() - t0:.1f} s")
+    out["n_params"] = info["n_params"]
+    rng = np.random.default_rng(0)
+    for B in (1, 8):
+        lens = [1024] * B
+        T = 1024 * B
+        tok = torch.from_numpy(rng.integers(0, 50368, T).astype(np.int32)).cuda()
+        h = torch.empty((T, 1024), dtype=torch.float32, device="cuda")
+        for _ in range(warmup):
+            enc.forward(tok, lens, hidden=h)
+        torch.cuda.synchronize()
+        ev = []
+        for _ in range(steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            enc.forward(tok, lens, hidden=h)
+            b.record()
+            ev.append((a, b))
+        torch.cuda.synchronize()
+        ms = statistics.median(a.elapsed_time(b) for a, b in ev)
+        ref = h.clone()
+        g = torch.cuda.CUDAGraph()
+        hg = torch.empty_like(h)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            enc.forward(tok, lens, hidden=hg)                # layout uploaded before capture
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            enc.forward(tok, lens, hidden=hg)
+        gev, same = [], True
+        for i in range(steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            hg.zero_()
+            a.record()
+            g.replay()
+            b.record()
+            torch.cuda.synchronize()
+            gev.append(a.elapsed_time(b))
+            same = same and bool(torch.equal(hg.view(torch.int32), ref.view(torch.int32)))
+            if i % 4 == 0:
+                enc.forward(tok, lens, hidden=h)             # eager work between replays
+        gms = statistics.median(gev)
+        out[f"{B}x1024"] = {"ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                            "graph_ms": round(gms, 4), "graph_tokens_per_s": round(T / (gms * 1e-3), 1),
+                            "graph_replays_equal_eager": same}
+        log(f"encoder {B}x1024: {ms:.3f} ms launched, {gms:.3f} ms from a graph -> "
+            f"{T / (ms * 1e-3):.0f} / {T / (gms * 1e-3):.0f} tokens/s")
+        del g
+    enc.close()
+    pub = {"1x1024_ms": 104.9, "8x1024_ms": 876.3,
+           "source": "reference README.md:60, results/bench_short.json:224 (Intel Core Ultra 7 265K, 18 threads, "
+                     "AVX-VNNI int8 path, Q4_K_M)"}
+    out["reference_published_cpu"] = pub
+    out["speedup_vs_published_1x1024"] = round(pub["1x1024_ms"] / out["1x1024"]["ms"], 1)
+    out["speedup_vs_published_8x1024"] = round(pub["8x1024_ms"] / out["8x1024"]["ms"], 1)
+    return out
 
 
 def cpu_baseline(path, rows: int, reps: int):
@@ -232,6 +311,7 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=2048)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-encoder1024", action="store_true")
+    ap.add_argument("--no-encoder", action="store_true", help="skip the whole-encoder timing")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one plain device copy of this many MiB first (PMC counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -322,6 +402,10 @@ def main() -> int:
         log(f"encoder linear path at 1024 tokens: {ms1k:.3f} ms -> {enc['tokens_per_s']:.0f} tokens/s")
         del p1k
 
+    full = None
+    if not args.no_encoder:
+        full = time_encoder(nxg, max(args.steps, 20), args.warmup)
+
     cpu = None
     if not args.no_cpu:
         t0 = time.perf_counter()
@@ -354,6 +438,7 @@ def main() -> int:
         "quantize": {"ms_per_step": round(quant_ms, 4),
                      "gb_per_s": round(path.quant_bytes / (quant_ms * 1e-3) / 1e9, 1) if quant_ms else None},
         "encoder_1024": enc,
+        "encoder": full,
         "roofline": roof,
         "roofline_relu2_q8": roof_relu2,
         "cpu_baseline": cpu,

@@ -13,6 +13,15 @@ median_ms. The producers of the activations are not on the path and run as synth
 rows (see encoder.py). Weights are random Q8_0 unless -m names a GGUF file holding the
 encoder's tensors. --graph replays the pass from a HIP graph instead of launching it.
 --profile adds the device time per kind of launch from HIP events on one extra pass.
+
+    python nexterabert.cpp_amd/cli.py --bench T --encode [--batch B] [--reps R] [-m model.gguf]
+
+--encode times the whole encoder instead (nxg_encoder_encode, the counterpart of
+nextera_encode, on host buffers), exactly as tools/cli.cpp:177-204 times nextera_encode:
+ids uniform in [1000, min(vocab, 40000)) from a fixed seed with CLS first and SEP last in
+each sequence, the pooled vectors L2-normalised as the only output. Without -m the model
+is the 213M-parameter architecture with random-init weights, written as Q4_K_M to a
+temporary file.
 """
 from __future__ import annotations
 
@@ -52,6 +61,7 @@ def parse_args(argv: Optional[List[str]] = None) -> argparse.Namespace:
     ap.add_argument("--profile", action="store_true", help="with --bench: print where the time goes")
     ap.add_argument("--graph", action="store_true", help="with --bench: replay each pass from a HIP graph")
     ap.add_argument("--no-fuse-mlp", action="store_true", help="c_fc writes fp32 rows, then relu^2 + quantize")
+    ap.add_argument("--encode", action="store_true", help="with --bench: time the whole encoder (nxg_encoder)")
     args = ap.parse_args(argv)
     if args.bench < 0 or args.batch < 1 or args.reps < 1:
         ap.error("--bench T >= 1, --batch B >= 1 and --reps R >= 1")
@@ -123,6 +133,47 @@ def bench(nxg, args, gguf) -> str:
     return "\n".join(lines)
 
 
+def bench_encoder(nxg, args) -> str:
+    """--bench --encode: the reference CLI's encode benchmark on nxg_encoder."""
+    import tempfile
+    import numpy as np
+    with tempfile.TemporaryDirectory() as tmp:
+        path = args.model
+        if path is None:
+            from nexterabert_cpp_amd import synth
+            path = str(Path(tmp) / "nexterabert_random_q4km.gguf")
+            synth.write_random_model(nxg, path, "Q4_K_M", seed=0)
+        with nxg.GGUF(path) as g:
+            ftype = ftype_name(g.get("general.file_type"))
+            cls_id = int(g.get("tokenizer.ggml.cls_token_id", -1))
+            sep_id = int(g.get("tokenizer.ggml.seperator_token_id", -1))
+        enc = nxg.Encoder(path)
+    T, B = args.bench, args.batch
+    rng = np.random.default_rng(0)
+    hi = min(enc.n_vocab, 40000)
+    tok = rng.integers(min(1000, hi - 1), hi, T * B).astype(np.int32)      # a tiny vocabulary: from below 1000
+    for b in range(B):
+        if 0 <= cls_id < enc.n_vocab:
+            tok[b * T] = cls_id
+        if 0 <= sep_id < enc.n_vocab:
+            tok[(b + 1) * T - 1] = sep_id
+    lens = [T] * B
+    ms = []
+    try:
+        for r in range(args.reps + 3):
+            t0 = time.perf_counter()
+            enc.encode(tok, lens, hidden=False, pooled=True, normalize=True)
+            t1 = time.perf_counter()
+            if r >= 3:
+                ms.append((t1 - t0) * 1e3)
+    finally:
+        enc.close()
+    ms.sort()
+    med = ms[len(ms) // 2]
+    return (f"bench: {ftype}  T={T}  batch={B}  encoder  median {med:.3f} ms  min {ms[0]:.3f} ms  "
+            f"({1000.0 * T * B / med:.0f} tokens/s)")
+
+
 def main(argv: Optional[List[str]] = None) -> int:
     args = parse_args(argv)
     nxg = _package()
@@ -131,7 +182,7 @@ def main(argv: Optional[List[str]] = None) -> int:
         if args.info or not args.bench:
             print("\n".join(info(nxg, gguf)), flush=True)
         if args.bench:
-            print(bench(nxg, args, gguf), flush=True)
+            print(bench_encoder(nxg, args) if args.encode else bench(nxg, args, gguf), flush=True)
     finally:
         if gguf is not None:
             gguf.close()

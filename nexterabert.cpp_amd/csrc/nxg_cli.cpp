@@ -7,6 +7,12 @@
 //
 //   nxg-cli --info [-m model.gguf]
 //   nxg-cli --bench T [--batch B] [--reps R] [--graph] [--profile] [-m model.gguf]
+//   nxg-cli --bench T --encode -m model.gguf [--batch B] [--reps R]
+//
+// --encode times the whole encoder instead (include/nxg_encoder.h: nxg_encoder_encode on
+// host buffers, the counterpart of nextera_encode) with the reference CLI's inputs: ids
+// uniform in [1000, min(vocab, 40000)) from mt19937(0), CLS first and SEP last in each
+// sequence, L2-normalised pooled vectors as the only output.
 //
 // A pass runs every int8 projection of the 18 layers (src/nexterabert.cpp:1185-1289) over B
 // packed sequences of T tokens: per layer each distinct activation is quantized once
@@ -33,6 +39,7 @@
 #include <string>
 #include <vector>
 
+#include "nxg_encoder.h"
 #include "nxg_gguf.h"
 #include "nxg_linear.h"
 
@@ -337,6 +344,7 @@ void usage(const char * argv0) {
             "  --batch B    sequences per pass (default 1)\n"
             "  --reps R     timed repetitions (default 20)\n"
             "  --graph      replay each pass from a HIP graph\n"
+            "  --encode     with --bench and -m: time the whole encoder (nxg_encoder_encode)\n"
             "  --profile    print the device time per kind of launch\n",
             argv0);
 }
@@ -345,7 +353,7 @@ void usage(const char * argv0) {
 
 int main(int argc, char ** argv) {
     const char * model = nullptr;
-    bool info = false, graph = false, profile = false;
+    bool info = false, graph = false, profile = false, encode = false;
     int bench_t = 0, batch = 1, reps = 20;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
@@ -363,6 +371,7 @@ int main(int argc, char ** argv) {
         else if (a == "--reps") reps = atoi(next());
         else if (a == "--graph") graph = true;
         else if (a == "--profile") profile = true;
+        else if (a == "--encode") encode = true;
         else if (a == "-h" || a == "--help") {
             usage(argv[0]);
             return 0;
@@ -390,6 +399,47 @@ int main(int argc, char ** argv) {
             printf("model: GGUF v%u, %s, %lld tensors\n", nxg_gguf_version(g), ftype_of(g).c_str(),
                    (long long) nxg_gguf_n_tensors(g));
         }
+    }
+    if (bench_t > 0 && encode) {
+        if (!model) {
+            fprintf(stderr, "nxg-cli: --encode needs -m model.gguf\n");
+            return 1;
+        }
+        auto kv_id = [&](const char * key) -> int32_t {
+            const int64_t i = nxg_gguf_find_key(g, key);
+            int64_t v = -1;
+            return i >= 0 && nxg_gguf_get_i64(g, i, &v) == NXG_OK ? (int32_t) v : -1;
+        };
+        const int32_t cls = kv_id("tokenizer.ggml.cls_token_id"), sep = kv_id("tokenizer.ggml.seperator_token_id");
+        nxg_encoder_params ep = nxg_encoder_default_params();
+        nxg_encoder * enc = nullptr;
+        check(nxg_encoder_load(model, &ep, &enc), "encoder_load");
+        const int32_t n_vocab = nxg_encoder_n_vocab(enc), n_embd = nxg_encoder_n_embd(enc);
+        std::mt19937 rng(0);
+        const int32_t hi = std::min(n_vocab, 40000);
+        std::uniform_int_distribution<int32_t> dist(std::min(1000, hi - 1), hi - 1);   // a tiny vocabulary: from below 1000
+        std::vector<int32_t> tokens((size_t) bench_t * batch), lengths(batch, bench_t);
+        for (int32_t & t : tokens) t = dist(rng);
+        for (int b = 0; b < batch; ++b) {
+            if (cls >= 0 && cls < n_vocab) tokens[(size_t) b * bench_t] = cls;
+            if (sep >= 0 && sep < n_vocab) tokens[(size_t) (b + 1) * bench_t - 1] = sep;
+        }
+        std::vector<float> pooled((size_t) batch * n_embd);
+        std::vector<double> ms;
+        for (int r = 0; r < reps + 3; ++r) {
+            const auto t0 = std::chrono::steady_clock::now();
+            check(nxg_encoder_encode(enc, tokens.data(), nullptr, lengths.data(), batch, nullptr, pooled.data(), 1),
+                  "encoder_encode");
+            const auto t1 = std::chrono::steady_clock::now();
+            if (r >= 3) ms.push_back(std::chrono::duration<double, std::milli>(t1 - t0).count());
+        }
+        std::sort(ms.begin(), ms.end());
+        const double med = ms[ms.size() / 2];
+        printf("bench: %s  T=%d  batch=%d  encoder  median %.3f ms  min %.3f ms  (%.0f tokens/s)\n", ftype_of(g).c_str(),
+               bench_t, batch, med, ms.front(), 1000.0 * bench_t * batch / med);
+        nxg_encoder_free(enc);
+        nxg_gguf_close(g);
+        return 0;
     }
     if (bench_t > 0) {
         check(nxg_init(), "init");

@@ -137,3 +137,25 @@ def test_encoder_full_model_1024(nxg, synth, enc, torch, tmp_path):
     say(f"encoder: min token cosine {cos.min():.9f}")
     assert cos.min() >= 0.99999
     assert (bits(h) == bits(hr)).all() and (bits(p) == bits(pr)).all()
+
+
+def test_cli_encode_bench(nxg, torch, small_models, capsys):
+    """--bench --encode in both drivers: the reference CLI's encode benchmark on nxg_encoder."""
+    import importlib.util
+    import subprocess
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    path, d, _ = small_models["c256_q8"]
+    spec = importlib.util.spec_from_file_location("nxg_cli", root / "nexterabert.cpp_amd" / "cli.py")
+    cli = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(cli)
+    say("cli --bench 48 --batch 2 --reps 3 --encode")
+    assert cli.main(["--bench", "48", "--batch", "2", "--reps", "3", "--encode", "-m", str(path)]) == 0
+    line = next(l for l in capsys.readouterr().out.splitlines() if l.startswith("bench: "))
+    assert line.startswith("bench: Q8_0  T=48  batch=2  encoder  median") and "tokens/s" in line
+    say("nxg-cli --bench 48 --batch 2 --reps 3 --encode")
+    r = subprocess.run([str(root / "nexterabert.cpp_amd" / "nxg-cli"), "--bench", "48", "--batch", "2", "--reps", "3",
+                        "--encode", "-m", str(path)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    line = next(l for l in r.stdout.splitlines() if l.startswith("bench: "))
+    assert line.startswith("bench: Q8_0  T=48  batch=2  encoder  median") and "tokens/s" in line
