@@ -633,7 +633,8 @@ __global__ __launch_bounds__(64) void attention_kernel(attn_params p) {
     for (int sft = 32; sft >= 1; sft >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sft));
     const float m = __builtin_isnan(sc[0]) ? sc[0] : mx;
     __syncthreads();
-    for (int j = lane; j < n; j += 64) sc[j] = j < ng ? exp_cephes(sc[j] - m) : expf_libm(sc[j] - m);
+    for (int j = lane; j < ng; j += 64) sc[j] = exp_cephes(sc[j] - m);
+    for (int j = ng + lane; j < n; j += 64) sc[j] = expf_libm(sc[j] - m);
     __syncthreads();
     // lane sums of the whole groups (lane l < 8 takes elements 8i + l in order), hsum256
     float ls = 0.0f;
@@ -651,6 +652,58 @@ __global__ __launch_bounds__(64) void attention_kernel(attn_params p) {
     float acc = 0.0f;
     for (int j = 0; j < n; ++j) acc = __builtin_fmaf(sc[j] * inv, vh[(size_t) j * 64 + lane], acc);
     o[lane] = acc;
+}
+
+// softmax_exp (src/nexterabert.cpp:177-200) for one (query, head) pair whose n scores sit in
+// LDS at Sp, by the 16 lanes sk of the pair (one wave's 16-lane group), in three steps with a
+// workgroup barrier between them (the callers hold it):
+//   softmax_max_exp   m (a NaN first score wins, else the largest score), then exp256(s - m)
+//                     in place for the n & ~7 grouped keys and the C library's expf for the rest
+//   softmax_inv       lanes l < 8 add keys 8i + l in order of i, hsum256 over the 8 lanes, the
+//                     tail keys added after in order; returns 1 / sum (on lane 0 of the group)
+//   softmax_weights   w = e * (1 / sum) in place
+// Loads are issued 16 at a time ahead of the adds that consume them in order.
+__device__ __forceinline__ void softmax_max_exp(float * Sp, int n, int sk) {
+    const int ng = n & ~7;
+    const float s0 = Sp[0];
+    float mx = -__builtin_inff();
+#pragma unroll 8
+    for (int j = sk; j < n; j += 16) mx = fmaxf(mx, Sp[j]);
+#pragma unroll
+    for (int sft = 8; sft >= 1; sft >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sft));
+    const float m = __builtin_isnan(s0) ? s0 : mx;
+#pragma unroll 4
+    for (int j = sk; j < ng; j += 16) Sp[j] = exp_cephes(Sp[j] - m);
+    for (int j = ng + sk; j < n; j += 16) Sp[j] = expf_libm(Sp[j] - m);
+}
+
+__device__ __forceinline__ float softmax_inv(const float * Sp, int n, int sk, bool active) {
+    const int ng = n & ~7;
+    float ls = 0.0f;
+    if (active && sk < 8) {
+        int j = sk;
+        for (; j + 8 * 15 < ng; j += 8 * 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = Sp[j + 8 * u];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) ls = ls + v[u];
+        }
+        for (; j < ng; j += 8) ls = ls + Sp[j];
+    }
+    ls = ls + __shfl_xor(ls, 4);                           // lanes 8..15 hold 0 and stay among themselves
+    ls = ls + __shfl_xor(ls, 2);
+    ls = ls + __shfl_xor(ls, 1);
+    float sum = ls;
+    if (active && sk == 0) {
+        for (int j = ng; j < n; ++j) sum = sum + Sp[j];
+    }
+    return 1.0f / sum;
+}
+
+__device__ __forceinline__ void softmax_weights(float * Sp, int n, int sk, float inv) {
+#pragma unroll 4
+    for (int j = sk; j < n; j += 16) Sp[j] = Sp[j] * inv;
 }
 
 // The same attention for a tile of (query, head) pairs: the ATT_P pairs of one workgroup are
@@ -783,35 +836,14 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
     __syncthreads();
 
     // softmax: 16 threads per pair
-    if (valid) {
-        const float s0 = Sp[0];
-        float mx = -__builtin_inff();
-        for (int j = sk; j < n_p; j += 16) mx = fmaxf(mx, Sp[j]);
-#pragma unroll
-        for (int sft = 8; sft >= 1; sft >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sft));
-        const float m = __builtin_isnan(s0) ? s0 : mx;
-        for (int j = sk; j < n_p; j += 16) Sp[j] = j < ng_p ? exp_cephes(Sp[j] - m) : expf_libm(Sp[j] - m);
-    }
+    if (valid) softmax_max_exp(Sp, n_p, sk);
     __syncthreads();
     {
-        float ls = 0.0f;
-        if (valid && sk < 8) {
-            for (int j = sk; j < ng_p; j += 8) ls = ls + Sp[j];
-        }
-        ls = ls + __shfl_xor(ls, 4);                       // lanes 8..15 hold 0 and stay among themselves
-        ls = ls + __shfl_xor(ls, 2);
-        ls = ls + __shfl_xor(ls, 1);
-        if (valid && sk == 0) {
-            float sum = ls;
-            for (int j = ng_p; j < n_p; ++j) sum = sum + Sp[j];
-            inv_s[sp] = 1.0f / sum;
-        }
+        const float inv = softmax_inv(Sp, n_p, sk, valid);
+        if (valid && sk == 0) inv_s[sp] = inv;
     }
     __syncthreads();
-    if (valid) {
-        const float inv = inv_s[sp];
-        for (int j = sk; j < n_p; j += 16) Sp[j] = Sp[j] * inv;
-    }
+    if (valid) softmax_weights(Sp, n_p, sk, inv_s[sp]);
 
     // values: thread (dim d, pairs 4 pg .. 4 pg + 3); pg is the wave's, so the pairs' key
     // ranges are scalars and a key outside a pair's range costs a scalar branch
