@@ -188,8 +188,8 @@ NXG_API int32_t nxg_block_mean_quantize_rows(const float * h, const float * g, c
  *   cu_offsets, n_seqs  the packed layout on the device (as the producers take it)
  *   scale     device float [n_seqs]: the per-document scale (nxg_attention_scales)
  *   half      -1: every key of the document; >= 0: the band |i - j| <= half (swa)
- *   max_keys  an upper bound of keys per query, <= 16384 (a document longer than it gets
- *             NaN outputs); sizes the kernel's LDS
+ *   max_keys  an upper bound of keys per query (a query with more gets NaN outputs); with
+ *             n_head / n_kv_head not dividing 16, at most 16384
  *   out       device float [T][n_head * 64] */
 NXG_API int32_t nxg_attention(const float * q, const float * k, const float * v, const int32_t * cu_offsets,
                               int32_t n_seqs, const float * scale, int32_t T, int32_t n_head, int32_t n_kv_head,

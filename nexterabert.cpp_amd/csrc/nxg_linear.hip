@@ -905,6 +905,227 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
     }
 }
 
+// One key's score for a query held in registers, before the scale (scores_d64,
+// src/nexterabert.cpp:704-731): the 8 chains a_l = q_l k_l, fma(q[8c+l], k[8c+l], a_l) for
+// c = 1..7, then the HADD tree for a key of a whole group of 8, hsum256's for a tail key.
+__device__ __forceinline__ float score_d64(const float (&qv)[64], const float * kp, bool grouped) {
+    float a[8];
+    {
+        const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
+        a[0] = qv[0] * k0.x; a[1] = qv[1] * k0.y; a[2] = qv[2] * k0.z; a[3] = qv[3] * k0.w;
+        a[4] = qv[4] * k1.x; a[5] = qv[5] * k1.y; a[6] = qv[6] * k1.z; a[7] = qv[7] * k1.w;
+    }
+#pragma unroll
+    for (int c = 1; c < 8; ++c) {
+        const v4f k0 = *reinterpret_cast<const v4f *>(kp + 8 * c);
+        const v4f k1 = *reinterpret_cast<const v4f *>(kp + 8 * c + 4);
+        a[0] = __builtin_fmaf(qv[8 * c + 0], k0.x, a[0]);
+        a[1] = __builtin_fmaf(qv[8 * c + 1], k0.y, a[1]);
+        a[2] = __builtin_fmaf(qv[8 * c + 2], k0.z, a[2]);
+        a[3] = __builtin_fmaf(qv[8 * c + 3], k0.w, a[3]);
+        a[4] = __builtin_fmaf(qv[8 * c + 4], k1.x, a[4]);
+        a[5] = __builtin_fmaf(qv[8 * c + 5], k1.y, a[5]);
+        a[6] = __builtin_fmaf(qv[8 * c + 6], k1.z, a[6]);
+        a[7] = __builtin_fmaf(qv[8 * c + 7], k1.w, a[7]);
+    }
+    return grouped ? ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))
+                   : ((a[0] + a[4]) + (a[2] + a[6])) + ((a[1] + a[5]) + (a[3] + a[7]));
+}
+
+// attention_tile_kernel's pairs, thread mapping and per-pair order for documents whose
+// scores do not fit in LDS: nothing is kept per key; the scores are computed three times,
+// bit-identically.
+//   pass 1  the maximum (a NaN first score wins, else the largest score that is not NaN)
+//   pass 2  e = exp256(s - m) (grouped keys) or the C library's expf (the n % 8 tail keys);
+//           each tile's e go through LDS so that lanes l < 8 of a pair add keys 8i + l in
+//           order of i, as softmax_exp's 8 accumulator lanes do; the tail e are kept apart and
+//           added after hsum256, in order
+//   pass 3  w = e * (1 / sum) per key through LDS, then thread (dim d, 4 pairs) acc = fma(w,
+//           v[d], acc) over the keys in order, as attention_tile_kernel
+// Keys and values are staged ATT_KT at a time ([key][ATT_KS]).
+__global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
+    __shared__ __attribute__((aligned(16))) float tile[ATT_KT * ATT_KS];
+    __shared__ float E[ATT_P][ATT_KT + 1];                 // one tile's e (pass 2) or w (pass 3)
+    __shared__ float tail_e[ATT_P][8];
+    __shared__ int lo_s[ATT_P], hi_s[ATT_P];
+    __shared__ float scale_s[ATT_P], m_s[ATT_P], s0_s[ATT_P], inv_s[ATT_P];
+    const int tid = (int) threadIdx.x;
+    const int rep = p.H / p.G, nq = ATT_P / rep;
+    const int n_qblk = (p.T + nq - 1) / nq;
+    const int g = (int) blockIdx.x / n_qblk, t0 = ((int) blockIdx.x - g * n_qblk) * nq;
+
+    if (tid < ATT_P) {
+        const int t = t0 + tid / rep;
+        int lo = 0, hi = 0;
+        float sc = 0.0f;
+        if (t < p.T) {
+            const doc_rows dr = doc_of(p.cu, p.n_seqs, t, p.T);
+            lo = dr.lo;
+            hi = dr.hi;
+            if (p.half >= 0) {
+                lo = max(lo, t - p.half);
+                hi = min(hi, t + p.half + 1);
+            }
+            sc = p.scale[dr.d];
+        }
+        lo_s[tid] = lo;
+        hi_s[tid] = hi;
+        scale_s[tid] = sc;
+    }
+    __syncthreads();
+    int kl = INT_MAX, kh = INT_MIN;
+#pragma unroll
+    for (int i = 0; i < ATT_P; ++i) {
+        if (hi_s[i] > lo_s[i] && hi_s[i] - lo_s[i] <= p.max_keys) {
+            kl = min(kl, lo_s[i]);
+            kh = max(kh, hi_s[i]);
+        }
+    }
+    const float * kg = p.k + (size_t) g * p.T * 64;
+    const float * vg = p.v + (size_t) g * p.T * 64;
+
+    const int sp = tid >> 4, sk = tid & 15;
+    const int plo = lo_s[sp], n_p = hi_s[sp] - plo, ng_p = n_p & ~7;
+    const bool valid = n_p > 0 && n_p <= p.max_keys;     // more keys than max_keys: NaN, as the other kernels
+    float qv[64];
+    {
+        const int t = t0 + sp / rep, h = g * rep + sp % rep;
+        const float * qr = p.q + (size_t) min(t, p.T - 1) * p.H * 64 + (size_t) h * 64;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const v4f f = *reinterpret_cast<const v4f *>(qr + 4 * i);
+            qv[4 * i] = f.x; qv[4 * i + 1] = f.y; qv[4 * i + 2] = f.z; qv[4 * i + 3] = f.w;
+        }
+    }
+    const float scale = scale_s[sp];
+    const int st_r = tid >> 4, st_c = 4 * (tid & 15);
+    v4f pre[2];
+    auto fetch = [&](const float * src, int j0) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int j = j0 + st_r + 16 * r;
+            pre[r] = j < kh ? *reinterpret_cast<const v4f *>(src + (size_t) j * 64 + st_c) : v4f{ 0.0f, 0.0f, 0.0f, 0.0f };
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) *reinterpret_cast<v4f *>(tile + (st_r + 16 * r) * ATT_KS + st_c) = pre[r];
+    };
+
+    // pass 1: the maximum
+    {
+        float mx = -__builtin_inff();
+        if (kl < kh) fetch(kg, kl);
+        for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
+            __syncthreads();
+            stage();
+            __syncthreads();
+            if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int jr = j0 + sk + 16 * r - plo;
+                if (!valid || jr < 0 || jr >= n_p) continue;
+                const float s = score_d64(qv, tile + (sk + 16 * r) * ATT_KS, jr < ng_p) * scale;
+                mx = fmaxf(mx, s);
+                if (jr == 0) s0_s[sp] = s;
+            }
+        }
+#pragma unroll
+        for (int sft = 8; sft >= 1; sft >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sft));
+        __syncthreads();                                   // s0_s written
+        if (valid && sk == 0) m_s[sp] = __builtin_isnan(s0_s[sp]) ? s0_s[sp] : mx;
+        __syncthreads();
+    }
+    const float m = m_s[sp];
+
+    // pass 2: the ordered sum of the exponentials
+    {
+        float ls = 0.0f;
+        if (kl < kh) fetch(kg, kl);
+        for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
+            __syncthreads();                               // E and the tile are free
+            stage();
+            __syncthreads();
+            if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int kt = sk + 16 * r, jr = j0 + kt - plo;
+                if (!valid || jr < 0 || jr >= n_p) continue;
+                const float s = score_d64(qv, tile + kt * ATT_KS, jr < ng_p) * scale;
+                if (jr < ng_p) E[sp][kt] = exp_cephes(s - m);
+                else tail_e[sp][jr - ng_p] = expf_libm(s - m);
+            }
+            __syncthreads();
+            if (valid && sk < 8) {
+                // the tile's keys jr = 8 i + sk (jr < ng) in order
+                const int jt = j0 - plo;                   // jr of the tile's first key
+                int kt0 = ((sk - jt) % 8 + 8) % 8;
+                for (int kt = kt0; kt < ATT_KT; kt += 8) {
+                    const int jr = jt + kt;
+                    if (jr >= 0 && jr < ng_p) ls = ls + E[sp][kt];
+                }
+            }
+        }
+        ls = ls + __shfl_xor(ls, 4);                       // lanes 8..15 hold 0 and stay among themselves
+        ls = ls + __shfl_xor(ls, 2);
+        ls = ls + __shfl_xor(ls, 1);
+        __syncthreads();                                   // tail_e written
+        if (valid && sk == 0) {
+            float sum = ls;
+            for (int j = 0; j < n_p - ng_p; ++j) sum = sum + tail_e[sp][j];
+            inv_s[sp] = 1.0f / sum;
+        }
+        __syncthreads();
+    }
+    const float inv = inv_s[sp];
+
+    // pass 3: the weights, then the values
+    const int d = tid & 63, pg = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int vlo[4], vn[4];
+    float acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int n = hi_s[4 * pg + i] - lo_s[4 * pg + i];
+        vlo[i] = __builtin_amdgcn_readfirstlane(lo_s[4 * pg + i]);
+        vn[i] = __builtin_amdgcn_readfirstlane(n <= p.max_keys ? n : 0);
+        acc[i] = 0.0f;
+    }
+    if (kl < kh) fetch(kg, kl);
+    for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
+        __syncthreads();                                   // E and the tile are free
+        stage();
+        __syncthreads();
+        fetch(vg, j0);                                     // this tile's values, staged after the weights
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int kt = sk + 16 * r, jr = j0 + kt - plo;
+            if (!valid || jr < 0 || jr >= n_p) continue;
+            const float s = score_d64(qv, tile + kt * ATT_KS, jr < ng_p) * scale;
+            E[sp][kt] = (jr < ng_p ? exp_cephes(s - m) : expf_libm(s - m)) * inv;
+        }
+        __syncthreads();                                   // the keys have been read
+        stage();
+        __syncthreads();
+        if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
+        const int jn = min(ATT_KT, kh - j0);
+        for (int jj = 0; jj < jn; ++jj) {
+            const float v = tile[jj * ATT_KS + d];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int jr = j0 + jj - vlo[i];
+                if (jr >= 0 && jr < vn[i]) acc[i] = __builtin_fmaf(E[4 * pg + i][jj], v, acc[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int pp = 4 * pg + i, t = t0 + pp / rep, h = g * rep + pp % rep;
+        if (t >= p.T) continue;
+        const int n = hi_s[pp] - lo_s[pp];
+        p.out[(size_t) t * p.H * 64 + (size_t) h * 64 + d] = (n > 0 && n <= p.max_keys) ? acc[i] : __uint_as_float(0x7fc00000u);
+    }
+}
+
 // tanh256 (src/nexterabert.cpp:103-117) lane by lane: big = (1 - t) / (1 + t) with t =
 // exp256(|x| * -2) and x's sign bit ORed in, small = the fused odd polynomial * x, small
 // where |x| < 0.1 (ordered: a NaN takes big).
@@ -2431,9 +2652,7 @@ int32_t nxg_attention(const float * q, const float * k, const float * v, const i
     if (T < 0 || n_seqs < 1 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head != 0) {
         return fail(NXG_EINVAL, "attention: T=%d n_seqs=%d n_head=%d n_kv_head=%d", T, n_seqs, n_head, n_kv_head);
     }
-    if (max_keys < 1 || max_keys > NXG_ATTN_MAX_KEYS) {
-        return fail(NXG_EINVAL, "attention: max_keys=%d (1..%d)", max_keys, NXG_ATTN_MAX_KEYS);
-    }
+    if (max_keys < 1) return fail(NXG_EINVAL, "attention: max_keys=%d (must be >= 1)", max_keys);
     if (T == 0) return NXG_OK;
     if (!q || !k || !v || !cu_offsets || !scale || !out) return fail(NXG_EINVAL, "attention: null buffer");
     const long long n_wg = (long long) T * n_head;
@@ -2445,10 +2664,18 @@ int32_t nxg_attention(const float * q, const float * k, const float * v, const i
     const int rep = n_head / n_kv_head;
     const int smax = (max_keys + 3) & ~3;
     const size_t tile_lds = ((size_t) ATT_P * smax + (size_t) ATT_KT * ATT_KS) * sizeof(float);
-    if (ATT_P % rep == 0 && tile_lds <= attention_tile_lds_limit()) {
+    if (ATT_P % rep == 0) {
         const long long n_tiles = (long long) n_kv_head * ((T + ATT_P / rep - 1) / (ATT_P / rep));
-        attention_tile_kernel<<<dim3((unsigned) n_tiles), dim3(256), tile_lds, (hipStream_t) stream>>>(p, smax);
-        return launch_check("attention_tile_kernel");
+        if (tile_lds <= attention_tile_lds_limit()) {
+            attention_tile_kernel<<<dim3((unsigned) n_tiles), dim3(256), tile_lds, (hipStream_t) stream>>>(p, smax);
+            return launch_check("attention_tile_kernel");
+        }
+        attention_long_kernel<<<dim3((unsigned) n_tiles), dim3(256), 0, (hipStream_t) stream>>>(p);
+        return launch_check("attention_long_kernel");
+    }
+    if (max_keys > NXG_ATTN_MAX_KEYS) {
+        return fail(NXG_EINVAL, "attention: max_keys=%d: with n_head / n_kv_head = %d (not a divisor of %d) at most %d",
+                    max_keys, rep, ATT_P, NXG_ATTN_MAX_KEYS);
     }
     attention_kernel<<<dim3((unsigned) n_wg), dim3(64), (size_t) max_keys * sizeof(float), (hipStream_t) stream>>>(p);
     return launch_check("attention_kernel");

@@ -1,7 +1,9 @@
 """GPU: op_attention (head_dim 64) bit for bit against the oracle (src/nexterabert.cpp:704-852):
-documents of 1 to 2,500 tokens (key counts off multiples of 8 send the last keys through
+documents of 1 to 4,000 tokens (key counts off multiples of 8 send the last keys through
 hsum256 and the C library's expf), full and banded (swa) attention, 16 query / 8 KV heads,
-per-document scales, and scores large enough to underflow exp in both its forms."""
+per-document scales, and scores large enough to underflow exp in both its forms. The kernel
+depends on the keys per query: the tile kernel up to ~2,400 (scores in LDS), the three-pass
+kernel beyond (scores recomputed), the row kernel for head ratios that do not divide 16."""
 from __future__ import annotations
 
 import numpy as np
@@ -71,6 +73,36 @@ def test_attention_long_document(nxg, orc, torch, dev):
     k, v = (rng.standard_normal((G, 2500, 64)).astype(np.float32) for _ in range(2))
     scale = np.array([0.125], np.float32)
     assert (bits(run(nxg, torch, q, k, v, cu, scale, H, G, -1)) == bits(orc.attention(q, k, v, cu, scale, H, G))).all()
+
+
+@pytest.mark.parametrize("lengths,half", [([4000], 1500), ([3000, 5, 700], -1)])
+def test_attention_long_documents(nxg, orc, torch, dev, lengths, half):
+    """Past the tile kernel's LDS: the three-pass kernel, banded and packed."""
+    say(f"attention long lengths={lengths} half={half}")
+    rng = np.random.default_rng(len(lengths) + 3)
+    H, G = 2, 1
+    cu = nxg.cu_offsets_of(lengths)
+    T = int(cu[-1])
+    q = rng.standard_normal((T, H * 64)).astype(np.float32)
+    k, v = (rng.standard_normal((G, T, 64)).astype(np.float32) for _ in range(2))
+    scale = rng.uniform(0.05, 0.2, len(lengths)).astype(np.float32)
+    y = run(nxg, torch, q, k, v, cu, scale, H, G, half)
+    assert (bits(y) == bits(orc.attention(q, k, v, cu, scale, H, G, half))).all()
+
+
+def test_attention_head_ratio_3(nxg, orc, torch, dev):
+    """6 query heads over 2 KV heads (3 does not divide 16): the row kernel."""
+    say("attention H=6 G=2")
+    rng = np.random.default_rng(31)
+    H, G = 6, 2
+    cu = nxg.cu_offsets_of([17, 1, 64])
+    T = int(cu[-1])
+    q = rng.standard_normal((T, H * 64)).astype(np.float32)
+    k, v = (rng.standard_normal((G, T, 64)).astype(np.float32) for _ in range(2))
+    scale = np.array([0.1, 0.2, 0.15], np.float32)
+    for half in (-1, 4):
+        y = run(nxg, torch, q, k, v, cu, scale, H, G, half)
+        assert (bits(y) == bits(orc.attention(q, k, v, cu, scale, H, G, half))).all()
 
 
 def test_attention_extreme_scores(nxg, orc, torch, dev):
