@@ -20,7 +20,8 @@ CPU oracle (the same path on VPDPBUSD, the reference's instruction) on a row
 sample on this host. The 1,024-token encoder line is the same path at M=1024,
 replayed from a HIP graph; `encoder` times the whole encoder forward (nxg_encoder:
 embedding, every block, out_norm) on the 213M-parameter model at 1x1024 and 8x1024
-tokens, beside the reference's published CPU timings of the same calls.
+tokens and on one 8,192- and one 65,536-token document, beside the reference's published CPU timings of
+the same calls.
 """
 from __future__ import annotations
 
@@ -115,10 +116,11 @@ def time_graph(path, steps: int, warmup: int):
     return s0.elapsed_time(s1) / steps
 
 
-def time_encoder(nxg, steps: int, warmup: int, preset: str = "Q4_K_M"):
+def time_encoder(nxg, steps: int, warmup: int, preset: str = "Q4_K_M", long_tokens=(8192, 65536)):
     """The whole encoder (nxg_encoder) on the 213M-parameter model with random-init
     weights written to a temporary GGUF file: one 1,024-token sequence and a batch of
-    8 of them, uniform random ids. Timed with HIP events on the launching stream,
+    8 of them, uniform random ids, then one document of each of `long_tokens` (best of 2
+    passes after one warm-up). Timed with HIP events on the launching stream,
     launched eagerly and replayed from a HIP graph (each replay's output compared bit
     for bit with the eager one, eager work between replays). tokens/s = 1000 T B /
     median ms, the reference CLI's rule (tools/cli.cpp:188-203)."""
@@ -182,13 +184,33 @@ def time_encoder(nxg, steps: int, warmup: int, preset: str = "Q4_K_M"):
         log(f"encoder {B}x1024: {ms:.3f} ms launched, {gms:.3f} ms from a graph -> "
             f"{T / (ms * 1e-3):.0f} / {T / (gms * 1e-3):.0f} tokens/s")
         del g
+    for T in long_tokens:
+        # one long document: the three-pass attention kernel on its full-attention layers
+        tok = torch.from_numpy(rng.integers(0, 50368, T).astype(np.int32)).cuda()
+        h = torch.empty((T, 1024), dtype=torch.float32, device="cuda")
+        enc.forward(tok, [T], hidden=h)
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(2):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            enc.forward(tok, [T], hidden=h)
+            b.record()
+            torch.cuda.synchronize()
+            ms.append(a.elapsed_time(b))
+        out[f"1x{T}"] = {"ms": round(min(ms), 2), "tokens_per_s": round(T / (min(ms) * 1e-3), 1),
+                         "finite": bool(torch.isfinite(h).all())}
+        log(f"encoder 1x{T}: {min(ms):.1f} ms -> {T / (min(ms) * 1e-3):.0f} tokens/s")
+        del h, tok
+        torch.cuda.empty_cache()
     enc.close()
-    pub = {"1x1024_ms": 104.9, "8x1024_ms": 876.3,
-           "source": "reference README.md:60, results/bench_short.json:224 (Intel Core Ultra 7 265K, 18 threads, "
-                     "AVX-VNNI int8 path, Q4_K_M)"}
+    pub = {"1x1024_ms": 104.9, "8x1024_ms": 876.3, "1x8192_ms": 1716.76, "1x65536_ms": 98951.67,
+           "source": "reference README.md:60,76, results/bench_short.json:224, results/bench.json:109-110 "
+                     "(Intel Core Ultra 7 265K, 18 threads, AVX-VNNI int8 path, Q4_K_M)"}
     out["reference_published_cpu"] = pub
-    out["speedup_vs_published_1x1024"] = round(pub["1x1024_ms"] / out["1x1024"]["ms"], 1)
-    out["speedup_vs_published_8x1024"] = round(pub["8x1024_ms"] / out["8x1024"]["ms"], 1)
+    for k in ("1x1024", "8x1024", "1x8192", "1x65536"):
+        if k in out:
+            out[f"speedup_vs_published_{k}"] = round(pub[f"{k}_ms"] / out[k]["ms"], 1)
     return out
 
 
@@ -312,6 +334,8 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-encoder1024", action="store_true")
     ap.add_argument("--no-encoder", action="store_true", help="skip the whole-encoder timing")
+    ap.add_argument("--encoder-long", default="8192,65536", metavar="T1,T2",
+                    help="also time the whole encoder on one document of each of these lengths ('': none)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one plain device copy of this many MiB first (PMC counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -404,7 +428,8 @@ def main() -> int:
 
     full = None
     if not args.no_encoder:
-        full = time_encoder(nxg, max(args.steps, 20), args.warmup)
+        long_tokens = [int(t) for t in args.encoder_long.split(",") if t.strip()]
+        full = time_encoder(nxg, max(args.steps, 20), args.warmup, long_tokens=long_tokens)
 
     cpu = None
     if not args.no_cpu:

@@ -249,7 +249,7 @@ NXG_API int32_t nxg_layer_norm(const float * x, const float * w, const float * b
 
 /* nextera_encode's pooled output (src/nexterabert.cpp:1913-1925) and op_doc_mean (:659-672): the
  * sum of each document's rows in row order, times 1 / n, or with normalize != 0 times
- * 1 / sqrt(dot_f32(p, p)) (0 for a zero vector; C % 32 == 0, C <= 16384).
+ * 1 / sqrt(dot_f32(p, p)) (0 for a zero vector; C % 32 == 0).
  *   x  device float [T][C];  cu_offsets device int32 [n_seqs + 1];  out  device float [n_seqs][C] */
 NXG_API int32_t nxg_doc_mean(const float * x, const int32_t * cu_offsets, int32_t n_seqs, int32_t T, int32_t C,
                              int32_t normalize, float * out, void * stream);

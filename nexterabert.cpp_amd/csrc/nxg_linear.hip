@@ -41,7 +41,6 @@ constexpr int WBN = 256;         // relu^2 -> int8 GEMM tile columns: one 256-in
 constexpr int WTHREADS = 512;    // relu^2 -> int8 GEMM: 8 waves, 2 x 4, each 64 x 64
 constexpr int N_XCD = 8;         // MI355X: 8 XCDs, workgroups dispatched round-robin
 #define NXG_ATTN_MAX_KEYS 16384          // keys per query the attention's LDS holds (64 KiB)
-#define NXG_DOC_MEAN_MAX_C 16384         // columns the normalized document mean keeps in LDS (64 KiB)
 #ifndef NXG_WG_PER_CU
 #define NXG_WG_PER_CU 2          // persistent GEMM workgroups per CU (0: one workgroup per tile)
 #endif
@@ -277,23 +276,12 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict_
     else                 quantize_block<ACT_MAX>(in, T, n_in, KS, n_blk, q, sx, g, B, stage);
 }
 
-// dot_f32(x, x) over a row of n floats (n % 32 == 0) in the reference's AVX2 order
-// (src/nexterabert.cpp:124-149), on the 16 lanes c = 0..15 of a lane group (xr null: the
-// row does not exist, the lanes still join the shuffles). 32 FMA chains, chain a taking
-// elements 32m + a (lane c runs chains 2c and 2c+1); then (s0 + s1) + (s2 + s3) lane-wise
-// (chains 8k + j are accumulator s_k, lane j); then hsum256: lanes j and j+4, then 0+2
-// and 1+3, then those two. fp32 addition is commutative, so both lanes of a shuffle pair
+// The end of dot_f32 (src/nexterabert.cpp:124-149) on the 16 lanes c = 0..15 of a lane
+// group, lane c holding the sums of chains 2c (a0) and 2c + 1 (a1): (s0 + s1) + (s2 + s3)
+// lane-wise (chains 8k + j are accumulator s_k, lane j), then hsum256: lanes j and j+4, then
+// 0+2 and 1+3, then those two. fp32 addition is commutative, so both lanes of a shuffle pair
 // get the same bits and every lane of the group returns the dot.
-__device__ __forceinline__ float dot_sq_ref16(const float * xr, int n, int c) {
-    float a0 = 0.0f, a1 = 0.0f;                // chains 2c and 2c + 1
-    if (xr) {
-        xr += 2 * c;
-        for (int m = 0; m < n / 32; ++m) {
-            const float2 v = *reinterpret_cast<const float2 *>(xr + 32 * m);
-            a0 = __builtin_fmaf(v.x, v.x, a0);
-            a1 = __builtin_fmaf(v.y, v.y, a1);
-        }
-    }
+__device__ __forceinline__ float dot_tree16(float a0, float a1) {
     // lane c holds s_k[j], s_k[j+1] with k = c/4, j = 2(c%4)
     a0 = a0 + __shfl_xor(a0, 4);               // s0 + s1, s2 + s3
     a1 = a1 + __shfl_xor(a1, 4);
@@ -304,6 +292,23 @@ __device__ __forceinline__ float dot_sq_ref16(const float * xr, int n, int c) {
     a0 = a0 + __shfl_xor(a0, 1);               // (v0+v4) + (v2+v6), (v1+v5) + (v3+v7)
     a1 = a1 + __shfl_xor(a1, 1);
     return a0 + a1;
+}
+
+// dot_f32(x, x) over a row of n floats (n % 32 == 0) in the reference's AVX2 order
+// (src/nexterabert.cpp:124-149), on the 16 lanes c = 0..15 of a lane group (xr null: the
+// row does not exist, the lanes still join the shuffles). 32 FMA chains, chain a taking
+// elements 32m + a (lane c runs chains 2c and 2c+1), then dot_tree16.
+__device__ __forceinline__ float dot_sq_ref16(const float * xr, int n, int c) {
+    float a0 = 0.0f, a1 = 0.0f;                // chains 2c and 2c + 1
+    if (xr) {
+        xr += 2 * c;
+        for (int m = 0; m < n / 32; ++m) {
+            const float2 v = *reinterpret_cast<const float2 *>(xr + 32 * m);
+            a0 = __builtin_fmaf(v.x, v.x, a0);
+            a1 = __builtin_fmaf(v.y, v.y, a1);
+        }
+    }
+    return dot_tree16(a0, a1);
 }
 
 // op_rms_norm feeding an int8 linear (src/nexterabert.cpp:463-482 through for_rows'
@@ -327,6 +332,83 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(const float * __r
     const float dot = dot_sq_ref16(t < T ? x + (size_t) t * n_in : nullptr, n_in, c);
     const float inv = 1.0f / __builtin_sqrtf(dot / (float) n_in + eps);
     quantize_block<ACT_MAX>(src_rms{src_rows{x, n_in}, gain, inv}, T, n_in, KS, n_blk, q, sx, g, B, stage);
+}
+
+// The same op for n_in = 256 NB with the whole row group in registers: one workgroup per
+// 16-row group, 16 lanes per row; lane c holds inputs 32m + 2c and 32m + 2c + 1 for every m,
+// exactly what the reference's dot chains 2c and 2c + 1 consume (dot_sq_ref16's order), so
+// each input is read from HBM once. Every block is then quantized from those registers:
+// amax over the row's 16 lanes, quant1, and the int8 pairs gathered in LDS in fragment
+// order (input kb + 32m' + 2c + e goes to k-step 4B + m'/2, piece row + 16 (kq / 16), byte
+// kq % 16, kq = 32 (m' % 2) + 2c + e), then each wave stores whole 1 KiB fragments. A
+// NaN anywhere in the group's normalized values sends the group through quantize_block,
+// whose fold gives the reference's MAXPS result; without NaN that fold is the plain max.
+template <int ACT_MAX, int NB>
+__global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float * __restrict__ x, const float * __restrict__ gain,
+                                                         float eps, int T, int8_t * __restrict__ q,
+                                                         float * __restrict__ sx) {
+    constexpr int n_in = NB * BLK, M = n_in / 32, KS = 4 * NB;
+    __shared__ __attribute__((aligned(16))) int stage[KS * FRAG / 4];
+    const int g = (int) blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rl = wave * 4 + (lane >> 4), t = g * 16 + rl, c = lane & 15;
+    float2 v[M];
+    if (t < T) {
+        const float * xr = x + (size_t) t * n_in + 2 * c;
+#pragma unroll
+        for (int m = 0; m < M; ++m) v[m] = *reinterpret_cast<const float2 *>(xr + 32 * m);
+    } else {
+#pragma unroll
+        for (int m = 0; m < M; ++m) v[m] = float2{ 0.0f, 0.0f };
+    }
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        a0 = __builtin_fmaf(v[m].x, v[m].x, a0);
+        a1 = __builtin_fmaf(v[m].y, v[m].y, a1);
+    }
+    const float dot = dot_tree16(a0, a1);
+    const float inv = 1.0f / __builtin_sqrtf(dot / (float) n_in + eps);
+    bool nan = false;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float2 gv = *reinterpret_cast<const float2 *>(gain + 32 * m + 2 * c);
+        v[m].x = (v[m].x * inv) * gv.x;
+        v[m].y = (v[m].y * inv) * gv.y;
+        nan |= __builtin_isnan(v[m].x) || __builtin_isnan(v[m].y);
+    }
+    if (__syncthreads_or(nan)) {
+        const src_rms src{src_rows{x, n_in}, gain, inv};
+        for (int B = 0; B < NB; ++B) {
+            quantize_block<ACT_MAX>(src, T, n_in, KS, NB, q, sx, g, B, stage);
+            __syncthreads();
+        }
+        return;
+    }
+    unsigned short * st16 = reinterpret_cast<unsigned short *>(stage);
+#pragma unroll
+    for (int B = 0; B < NB; ++B) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fmaxf(abs_bits(v[8 * B + i].x), abs_bits(v[8 * B + i].y)));
+#pragma unroll
+        for (int sft = 1; sft < 16; sft <<= 1) amax = fmaxf(amax, __shfl_xor(amax, sft));
+        const float scale = amax / (float) ACT_MAX;
+        const float qinv = amax > 0.0f ? (float) ACT_MAX / amax : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int kq = 32 * (i & 1) + 2 * c;
+            const int pair = (quant1<ACT_MAX>(v[8 * B + i].x, qinv) & 0xff) | ((quant1<ACT_MAX>(v[8 * B + i].y, qinv) & 0xff) << 8);
+            st16[((4 * B + (i >> 1)) * FRAG + (rl + 16 * (kq >> 4)) * 16 + (kq & 15)) / 2] = (unsigned short) pair;
+        }
+        if (c == 0) sx[((size_t) (t >> 2) * NB + B) * 4 + (t & 3)] = t < T ? scale : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int f = wave; f < KS; f += 4) {
+        const int4 w = reinterpret_cast<const int4 *>(stage)[f * 64 + lane];
+        *reinterpret_cast<int4 *>(q + ((size_t) g * KS + f) * FRAG + lane * 16) = w;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1275,38 +1357,69 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float * __restric
 // The pooled vector of nextera_encode (src/nexterabert.cpp:1913-1925) and op_doc_mean
 // (:659-672): the sum of the document's rows in row order (axpy_f32 with weight 1, one
 // rounding per row) times 1 / n -- or, with normalize, times 1 / sqrt(dot_f32(p, p)) (0
-// for a zero vector; dot in the reference's order, C % 32 == 0). One workgroup per
-// document, 4 columns per thread per step; with normalize the sums are kept in LDS
-// (dynamic, C floats) for the dot.
-__global__ __launch_bounds__(256) void doc_mean_kernel(const float * __restrict__ x, const int32_t * __restrict__ cu,
-                                                       int T, int C, int normalize, float * __restrict__ out) {
-    extern __shared__ float pooled[];
-    __shared__ float scale_s;
-    const int d = (int) blockIdx.x;
+// for a zero vector; dot in the reference's order, C % 32 == 0).
+//
+// doc_sum_kernel: one workgroup per (document, 32-column slice). The row order fixes one
+// dependent chain of adds per column, so the slice's 32 columns are summed by 32 lanes of
+// wave 0 out of LDS, while all 256 threads stream the next 256-row chunk of the slice
+// (128-byte row pieces, one float4 per thread and row group) into registers. mean != 0
+// applies 1 / n; otherwise the raw sums are written for doc_norm_kernel.
+constexpr int DS_COLS = 32, DS_ROWS = 256;
+__global__ __launch_bounds__(256) void doc_sum_kernel(const float * __restrict__ x, const int32_t * __restrict__ cu,
+                                                      int T, int C, int n_slices, int mean, float * __restrict__ out) {
+    __shared__ __attribute__((aligned(16))) float tile[DS_ROWS * DS_COLS];
+    const int d = (int) blockIdx.x / n_slices, c0 = ((int) blockIdx.x % n_slices) * DS_COLS;
     const int lo = min(max(cu[d], 0), T), hi = min(max(cu[d + 1], lo), T);
-    float * o = out + (size_t) d * C;
-    for (int col = 4 * (int) threadIdx.x; col < C; col += 1024) {
-        v4f acc = { 0.0f, 0.0f, 0.0f, 0.0f };
-        for (int t = lo; t < hi; ++t) acc = acc + *reinterpret_cast<const v4f *>(x + (size_t) t * C + col);
-        *reinterpret_cast<v4f *>(o + col) = acc;
-        if (normalize) *reinterpret_cast<v4f *>(pooled + col) = acc;
-    }
-    float scale = 1.0f / (float) (hi - lo);
-    if (normalize) {
+    const int tid = (int) threadIdx.x;
+    const int lr = tid >> 3, lc = (tid & 7) * 4;              // row in a 32-row group, column in the slice
+    const bool col_ok = c0 + lc < C;                          // C % 4 == 0: a float4 is all in or all out
+    const float * xs = x + c0 + lc;
+    v4f buf[DS_ROWS / 32];
+    auto load = [&](int base) {
+#pragma unroll
+        for (int j = 0; j < DS_ROWS / 32; ++j) {
+            const int r = base + lr + 32 * j;
+            buf[j] = (col_ok && r < hi) ? *reinterpret_cast<const v4f *>(xs + (size_t) r * C) : v4f{ 0.0f, 0.0f, 0.0f, 0.0f };
+        }
+    };
+    float acc = 0.0f;
+    load(lo);
+    for (int base = lo; base < hi; base += DS_ROWS) {
+#pragma unroll
+        for (int j = 0; j < DS_ROWS / 32; ++j) *reinterpret_cast<v4f *>(tile + (lr + 32 * j) * DS_COLS + lc) = buf[j];
         __syncthreads();
-        if (threadIdx.x < 16) {
-            const float dot = dot_sq_ref16(pooled, C, (int) threadIdx.x);
-            if (threadIdx.x == 0) {
-                const float nrm = __builtin_sqrtf(dot);
-                scale_s = nrm > 0.0f ? 1.0f / nrm : 0.0f;
+        if (base + DS_ROWS < hi) load(base + DS_ROWS);
+        if (tid < DS_COLS) {
+            const int n = min(DS_ROWS, hi - base);
+            if (n == DS_ROWS) {
+#pragma unroll 32
+                for (int r = 0; r < DS_ROWS; ++r) acc = acc + tile[r * DS_COLS + tid];
+            } else {
+                for (int r = 0; r < n; ++r) acc = acc + tile[r * DS_COLS + tid];
             }
         }
         __syncthreads();
-        scale = scale_s;
     }
+    if (tid < DS_COLS && c0 + tid < C) out[(size_t) d * C + c0 + tid] = mean ? acc * (1.0f / (float) (hi - lo)) : acc;
+}
+
+// doc_norm_kernel: one workgroup per document scales its column sums by 1 / sqrt(dot_f32(p, p))
+// (0 for a zero vector), the dot on 16 lanes in the reference's order.
+__global__ __launch_bounds__(256) void doc_norm_kernel(int C, float * __restrict__ out) {
+    __shared__ float scale_s;
+    float * p = out + (size_t) blockIdx.x * C;
+    if (threadIdx.x < 16) {
+        const float dot = dot_sq_ref16(p, C, (int) threadIdx.x);
+        if (threadIdx.x == 0) {
+            const float nrm = __builtin_sqrtf(dot);
+            scale_s = nrm > 0.0f ? 1.0f / nrm : 0.0f;
+        }
+    }
+    __syncthreads();
+    const float scale = scale_s;
     for (int col = 4 * (int) threadIdx.x; col < C; col += 1024) {
-        const v4f a = *reinterpret_cast<const v4f *>(o + col);
-        *reinterpret_cast<v4f *>(o + col) = v4f{ a.x * scale, a.y * scale, a.z * scale, a.w * scale };
+        const v4f a = *reinterpret_cast<const v4f *>(p + col);
+        *reinterpret_cast<v4f *>(p + col) = v4f{ a.x * scale, a.y * scale, a.z * scale, a.w * scale };
     }
 }
 
@@ -2601,10 +2714,27 @@ int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps
     if (!x || !gain || !q || !sx) return fail(NXG_EINVAL, "rmsnorm_quantize: null buffer");
     int rc = check_device();
     if (rc) return rc;
+    hipStream_t s = (hipStream_t) stream;
+    if (n_in % BLK == 0) {
+        // the whole row group in registers: n_in = 256, 512, 1024 or 2048
+        const dim3 grid((unsigned) (d.MP / 16));
+#define NXG_RMS_Q8(NB)                                                                                        \
+        case NB:                                                                                              \
+            if (act_max == 127) rmsnorm_q8_kernel<127, NB><<<grid, 256, 0, s>>>(x, gain, eps, T, q, sx);       \
+            else                rmsnorm_q8_kernel<63, NB><<<grid, 256, 0, s>>>(x, gain, eps, T, q, sx);        \
+            return launch_check("rmsnorm_q8_kernel");
+        switch (d.n_blk) {
+            NXG_RMS_Q8(1)
+            NXG_RMS_Q8(2)
+            NXG_RMS_Q8(4)
+            NXG_RMS_Q8(8)
+            default: break;
+        }
+#undef NXG_RMS_Q8
+    }
     const long long n_wg = (long long) ((d.MP / 16 + 7) / 8) * 8 * d.n_blk;   // (row group, block), whole XCD rounds
     if (n_wg > INT32_MAX) return fail(NXG_EINVAL, "rmsnorm_quantize: T=%d n_in=%d too large", T, n_in);
     const dim3 grid((unsigned) n_wg);
-    hipStream_t s = (hipStream_t) stream;
     if (act_max == 127) rmsnorm_quantize_kernel<127><<<grid, 256, 0, s>>>(x, gain, eps, T, n_in, d.KS, d.n_blk, q, sx);
     else                rmsnorm_quantize_kernel<63><<<grid, 256, 0, s>>>(x, gain, eps, T, n_in, d.KS, d.n_blk, q, sx);
     return launch_check("rmsnorm_quantize_kernel");
@@ -2765,18 +2895,21 @@ int32_t nxg_layer_norm(const float * x, const float * w, const float * b, float 
 int32_t nxg_doc_mean(const float * x, const int32_t * cu_offsets, int32_t n_seqs, int32_t T, int32_t C, int32_t normalize,
                      float * out, void * stream) {
     if (n_seqs < 0 || T < 0 || C < 4 || C % 4 != 0) return fail(NXG_EINVAL, "doc_mean: n_seqs=%d T=%d C=%d", n_seqs, T, C);
-    if (normalize && (C % 32 != 0 || C > NXG_DOC_MEAN_MAX_C)) {
-        return fail(NXG_EINVAL, "doc_mean: normalize needs C a multiple of 32 and <= %d, got %d", NXG_DOC_MEAN_MAX_C, C);
-    }
+    if (normalize && C % 32 != 0) return fail(NXG_EINVAL, "doc_mean: normalize needs C a multiple of 32, got %d", C);
     if (n_seqs == 0) return NXG_OK;
     if (!x || !cu_offsets || !out || !aligned16(x) || !aligned16(out)) {
         return fail(NXG_EINVAL, "doc_mean: null or unaligned buffer");
     }
     int rc = check_device();
     if (rc) return rc;
-    const size_t lds = normalize ? (size_t) C * sizeof(float) : 0;
-    doc_mean_kernel<<<(unsigned) n_seqs, 256, lds, (hipStream_t) stream>>>(x, cu_offsets, T, C, normalize ? 1 : 0, out);
-    return launch_check("doc_mean_kernel");
+    const int n_slices = (C + DS_COLS - 1) / DS_COLS;
+    if ((int64_t) n_seqs * n_slices > INT32_MAX) return fail(NXG_EINVAL, "doc_mean: %d documents of %d columns", n_seqs, C);
+    doc_sum_kernel<<<(unsigned) (n_seqs * n_slices), 256, 0, (hipStream_t) stream>>>(x, cu_offsets, T, C, n_slices,
+                                                                                     normalize ? 0 : 1, out);
+    rc = launch_check("doc_sum_kernel");
+    if (rc || !normalize) return rc;
+    doc_norm_kernel<<<(unsigned) n_seqs, 256, 0, (hipStream_t) stream>>>(C, out);
+    return launch_check("doc_norm_kernel");
 }
 
 int32_t nxg_qact_export(const int8_t * q, const float * sx, int32_t T, int32_t n_in, int32_t act_max,

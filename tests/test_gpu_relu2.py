@@ -185,7 +185,8 @@ def test_relu2_q8_bad_shapes_raise(nxg, torch, dev):
         nxg.linear_i8_relu2_q8(dw2, nxg.quantize_rows(x2), out=nxg.qact_alloc(64, 128))
 
 
-@pytest.mark.parametrize("T,n_in", [(333, 1024), (100, 2304), (17, 32), (50, 96), (1, 4096)])
+@pytest.mark.parametrize("T,n_in", [(333, 1024), (100, 2304), (17, 32), (50, 96), (1, 4096),
+                                    (1000, 256), (45, 512), (70, 2048), (4111, 1024)])
 @pytest.mark.parametrize("act_max", [127, 63])
 def test_rmsnorm_quantize_matches_oracle(nxg, orc, torch, dev, T, n_in, act_max):
     """op_rms_norm feeding an int8 linear: the oracle's RMSNorm (AVX2 dot order), then
@@ -194,6 +195,8 @@ def test_rmsnorm_quantize_matches_oracle(nxg, orc, torch, dev, T, n_in, act_max)
     rng = np.random.default_rng(T + n_in + act_max)
     x = (rng.standard_normal((T, n_in)) * 10.0 ** rng.integers(-6, 6, (T, 1))).astype(np.float32)
     g = (1.0 + 0.2 * rng.standard_normal(n_in)).astype(np.float32)
+    if T > 1000:
+        x[-1, 9] = np.nan                # a NaN in the last row group only
     if T > 8:
         x[1] = 0.0                       # eps 0: inv = inf, 0 * inf = NaN everywhere
         x[2, 5] = np.nan

@@ -115,6 +115,20 @@ def test_doc_mean(nxg, orc, torch, dev, lengths, normalize):
     assert (bits(y) == bits(orc.doc_mean(x, cu, normalize=normalize))).all()
 
 
+@pytest.mark.parametrize("lengths,C", [([3000, 1, 257], 1024), ([513, 0, 40], 100), ([256, 255], 36), ([600], 2048)])
+def test_doc_mean_long_and_narrow(nxg, orc, torch, dev, lengths, C):
+    """Documents spanning several 256-row chunks (and exactly one), an empty document
+    (mean 0 * (1 / 0): NaN, as the oracle), column counts that leave a partial 32-column slice."""
+    say(f"doc_mean lengths={lengths} C={C}")
+    rng = np.random.default_rng(C + len(lengths))
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)    # cu_offsets_of refuses empty ones
+    x = (rng.standard_normal((int(cu[-1]), C)) * 3).astype(np.float32)
+    for normalize in ([False, True] if C % 32 == 0 else [False]):
+        y = nxg.doc_mean(cuda(torch, x), cu, normalize=normalize).cpu().numpy()
+        ref = orc.doc_mean(x, cu, normalize=normalize)
+        assert ((bits(y) == bits(ref)) | (np.isnan(y) & np.isnan(ref))).all(), f"normalize={normalize}"
+
+
 def test_row_op_errors(nxg, torch, dev):
     x = torch.zeros(4, 1024, device="cuda")
     with pytest.raises(ValueError):
