@@ -807,6 +807,7 @@ constexpr int ATT_P = 16;      // (query, head) pairs per workgroup
 constexpr int ATT_KT = 32;     // keys per staged tile
 constexpr int ATT_KS = 68;     // floats per staged row
 
+template <bool PAIR2>
 __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int smax) {
     extern __shared__ __attribute__((aligned(16))) float att_lds[];
     float * S = att_lds;                                   // [ATT_P][smax]
@@ -849,24 +850,13 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
     const float * kg = p.k + (size_t) g * p.T * 64;
     const float * vg = p.v + (size_t) g * p.T * 64;
 
-    // scores: thread (pair sp, key slots sk and sk + 16 of each tile)
+    // softmax threads: 16 per pair, pair sp
     const int sp = tid >> 4, sk = tid & 15;
-    const int plo = lo_s[sp], n_p = hi_s[sp] - plo, ng_p = n_p & ~7;
+    const int n_p = hi_s[sp] - lo_s[sp];
     const bool valid = n_p > 0 && n_p <= smax;
-    float qv[64];
-    {
-        const int t = t0 + sp / rep, h = g * rep + sp % rep;
-        const float * qr = p.q + (size_t) min(t, p.T - 1) * p.H * 64 + (size_t) h * 64;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const v4f f = *reinterpret_cast<const v4f *>(qr + 4 * i);
-            qv[4 * i] = f.x; qv[4 * i + 1] = f.y; qv[4 * i + 2] = f.z; qv[4 * i + 3] = f.w;
-        }
-    }
-    const float scale = scale_s[sp];
     float * Sp = S + (size_t) sp * smax;
     // staged rows: thread tid moves row (tid >> 4) + 16 r, floats 4 (tid & 15) .. + 3, r < 2;
-    // the next tile's rows are fetched into registers while the current one is scored
+    // the next tile's rows are fetched into registers while the current one is used
     const int st_r = tid >> 4, st_c = 4 * (tid & 15);
     v4f pre[2];
     auto fetch = [&](const float * src, int j0) {
@@ -880,39 +870,118 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
 #pragma unroll
         for (int r = 0; r < 2; ++r) *reinterpret_cast<v4f *>(tile + (st_r + 16 * r) * ATT_KS + st_c) = pre[r];
     };
-    if (kl < kh) fetch(kg, kl);
-    for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
-        __syncthreads();                                   // the previous tile has been read
-        stage();
-        __syncthreads();
-        if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
+
+    // scores, PAIR2: thread (pairs 2 sq and 2 sq + 1, key slot sj of each tile): both query
+    // rows in registers, so each staged key row is read from LDS once for two pairs (twice
+    // the registers: for launches whose LDS admits at most two workgroups per CU anyway)
+    if constexpr (PAIR2) {
+        const int sq = tid >> 5, sj = tid & 31;
+        float qv[2][64];
+        int plo[2], np[2], ngp[2];
+        bool ok[2];
+        float scl[2];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int jr = j0 + sk + 16 * r - plo;
-            if (!valid || jr < 0 || jr >= n_p) continue;
-            const float * kp = tile + (sk + 16 * r) * ATT_KS;
-            float a[8];
+        for (int u = 0; u < 2; ++u) {
+            const int pq = 2 * sq + u, t = t0 + pq / rep, h = g * rep + pq % rep;
+            const float * qr = p.q + (size_t) min(t, p.T - 1) * p.H * 64 + (size_t) h * 64;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const v4f f = *reinterpret_cast<const v4f *>(qr + 4 * i);
+                qv[u][4 * i] = f.x; qv[u][4 * i + 1] = f.y; qv[u][4 * i + 2] = f.z; qv[u][4 * i + 3] = f.w;
+            }
+            plo[u] = lo_s[pq];
+            np[u] = hi_s[pq] - plo[u];
+            ngp[u] = np[u] & ~7;
+            ok[u] = np[u] > 0 && np[u] <= smax;
+            scl[u] = scale_s[pq];
+        }
+        if (kl < kh) fetch(kg, kl);
+        for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
+            __syncthreads();                               // the previous tile has been read
+            stage();
+            __syncthreads();
+            if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
+            const int jr0 = j0 + sj - plo[0], jr1 = j0 + sj - plo[1];
+            const bool in0 = ok[0] && jr0 >= 0 && jr0 < np[0], in1 = ok[1] && jr1 >= 0 && jr1 < np[1];
+            if (!in0 && !in1) continue;
+            const float * kp = tile + sj * ATT_KS;
+            float a[2][8];
             {
                 const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
-                a[0] = qv[0] * k0.x; a[1] = qv[1] * k0.y; a[2] = qv[2] * k0.z; a[3] = qv[3] * k0.w;
-                a[4] = qv[4] * k1.x; a[5] = qv[5] * k1.y; a[6] = qv[6] * k1.z; a[7] = qv[7] * k1.w;
+                const float kk[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) a[u][l] = qv[u][l] * kk[l];
             }
 #pragma unroll
             for (int c = 1; c < 8; ++c) {
                 const v4f k0 = *reinterpret_cast<const v4f *>(kp + 8 * c);
                 const v4f k1 = *reinterpret_cast<const v4f *>(kp + 8 * c + 4);
-                a[0] = __builtin_fmaf(qv[8 * c + 0], k0.x, a[0]);
-                a[1] = __builtin_fmaf(qv[8 * c + 1], k0.y, a[1]);
-                a[2] = __builtin_fmaf(qv[8 * c + 2], k0.z, a[2]);
-                a[3] = __builtin_fmaf(qv[8 * c + 3], k0.w, a[3]);
-                a[4] = __builtin_fmaf(qv[8 * c + 4], k1.x, a[4]);
-                a[5] = __builtin_fmaf(qv[8 * c + 5], k1.y, a[5]);
-                a[6] = __builtin_fmaf(qv[8 * c + 6], k1.z, a[6]);
-                a[7] = __builtin_fmaf(qv[8 * c + 7], k1.w, a[7]);
+                const float kk[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) a[u][l] = __builtin_fmaf(qv[u][8 * c + l], kk[l], a[u][l]);
             }
-            const float tot = jr < ng_p ? ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))
-                                        : ((a[0] + a[4]) + (a[2] + a[6])) + ((a[1] + a[5]) + (a[3] + a[7]));
-            Sp[jr] = tot * scale;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int jr = u ? jr1 : jr0;
+                if (!(u ? in1 : in0)) continue;
+                const float (&e)[8] = a[u];
+                const float tot = jr < ngp[u] ? ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]))
+                                              : ((e[0] + e[4]) + (e[2] + e[6])) + ((e[1] + e[5]) + (e[3] + e[7]));
+                S[(size_t) (2 * sq + u) * smax + jr] = tot * scl[u];
+            }
+        }
+    } else {
+        // scores: thread (pair sp, key slots sk and sk + 16 of each tile)
+        const int plo = lo_s[sp], ng_p = n_p & ~7;
+        float qv[64];
+        {
+            const int t = t0 + sp / rep, h = g * rep + sp % rep;
+            const float * qr = p.q + (size_t) min(t, p.T - 1) * p.H * 64 + (size_t) h * 64;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const v4f f = *reinterpret_cast<const v4f *>(qr + 4 * i);
+                qv[4 * i] = f.x; qv[4 * i + 1] = f.y; qv[4 * i + 2] = f.z; qv[4 * i + 3] = f.w;
+            }
+        }
+        const float scale = scale_s[sp];
+        if (kl < kh) fetch(kg, kl);
+        for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
+            __syncthreads();                               // the previous tile has been read
+            stage();
+            __syncthreads();
+            if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int jr = j0 + sk + 16 * r - plo;
+                if (!valid || jr < 0 || jr >= n_p) continue;
+                const float * kp = tile + (sk + 16 * r) * ATT_KS;
+                float a[8];
+                {
+                    const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
+                    a[0] = qv[0] * k0.x; a[1] = qv[1] * k0.y; a[2] = qv[2] * k0.z; a[3] = qv[3] * k0.w;
+                    a[4] = qv[4] * k1.x; a[5] = qv[5] * k1.y; a[6] = qv[6] * k1.z; a[7] = qv[7] * k1.w;
+                }
+#pragma unroll
+                for (int c = 1; c < 8; ++c) {
+                    const v4f k0 = *reinterpret_cast<const v4f *>(kp + 8 * c);
+                    const v4f k1 = *reinterpret_cast<const v4f *>(kp + 8 * c + 4);
+                    a[0] = __builtin_fmaf(qv[8 * c + 0], k0.x, a[0]);
+                    a[1] = __builtin_fmaf(qv[8 * c + 1], k0.y, a[1]);
+                    a[2] = __builtin_fmaf(qv[8 * c + 2], k0.z, a[2]);
+                    a[3] = __builtin_fmaf(qv[8 * c + 3], k0.w, a[3]);
+                    a[4] = __builtin_fmaf(qv[8 * c + 4], k1.x, a[4]);
+                    a[5] = __builtin_fmaf(qv[8 * c + 5], k1.y, a[5]);
+                    a[6] = __builtin_fmaf(qv[8 * c + 6], k1.z, a[6]);
+                    a[7] = __builtin_fmaf(qv[8 * c + 7], k1.w, a[7]);
+                }
+                const float tot = jr < ng_p ? ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))
+                                            : ((a[0] + a[4]) + (a[2] + a[6])) + ((a[1] + a[5]) + (a[3] + a[7]));
+                Sp[jr] = tot * scale;
+            }
         }
     }
     __syncthreads();
@@ -955,26 +1024,29 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
             b[i] = max(min(vlo[i] + vn[i] - j0, jn), a[i]);
             full = full && a[i] == 0 && b[i] == jn;
         }
-        const float * w0 = S + (size_t) (4 * pg + 0) * smax + (j0 - vlo[0]);
-        const float * w1 = S + (size_t) (4 * pg + 1) * smax + (j0 - vlo[1]);
-        const float * w2 = S + (size_t) (4 * pg + 2) * smax + (j0 - vlo[2]);
-        const float * w3 = S + (size_t) (4 * pg + 3) * smax + (j0 - vlo[3]);
+        // the tile's weights: pair i's weight of key j0 + l in lane l (l < 32), read once and
+        // broadcast per key (readlane), so the key loop reads only the value row from LDS
+        float wl[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int jr = j0 + (d & 31) - vlo[i];
+            wl[i] = (jr >= 0 && jr < vn[i]) ? S[(size_t) (4 * pg + i) * smax + jr] : 0.0f;
+        }
+        auto wk = [&](int i, int jj) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl[i]), jj)); };
         if (full) {
-#pragma unroll 8
-            for (int jj = 0; jj < ATT_KT; ++jj) {
-                const float v = tile[jj * ATT_KS + d];
-                acc[0] = __builtin_fmaf(w0[jj], v, acc[0]);
-                acc[1] = __builtin_fmaf(w1[jj], v, acc[1]);
-                acc[2] = __builtin_fmaf(w2[jj], v, acc[2]);
-                acc[3] = __builtin_fmaf(w3[jj], v, acc[3]);
-            }
+            float vt[ATT_KT];                              // the tile's values of dimension d, read up front
+#pragma unroll
+            for (int jj = 0; jj < ATT_KT; ++jj) vt[jj] = tile[jj * ATT_KS + d];
+#pragma unroll
+            for (int jj = 0; jj < ATT_KT; ++jj)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(wk(i, jj), vt[jj], acc[i]);
         } else {
             for (int jj = 0; jj < jn; ++jj) {
                 const float v = tile[jj * ATT_KS + d];
-                if (jj >= a[0] && jj < b[0]) acc[0] = __builtin_fmaf(w0[jj], v, acc[0]);
-                if (jj >= a[1] && jj < b[1]) acc[1] = __builtin_fmaf(w1[jj], v, acc[1]);
-                if (jj >= a[2] && jj < b[2]) acc[2] = __builtin_fmaf(w2[jj], v, acc[2]);
-                if (jj >= a[3] && jj < b[3]) acc[3] = __builtin_fmaf(w3[jj], v, acc[3]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (jj >= a[i] && jj < b[i]) acc[i] = __builtin_fmaf(wk(i, jj), v, acc[i]);
             }
         }
     }
@@ -2621,7 +2693,9 @@ static size_t attention_tile_lds_limit() {
         if (hipGetDevice(&dev) == hipSuccess &&
             hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 1024) {
             const size_t want = (size_t) v - 1024;           // static arrays of the kernel: 4 x ATT_P words
-            if (hipFuncSetAttribute((const void *) attention_tile_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+            if (hipFuncSetAttribute((const void *) attention_tile_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int) want) == hipSuccess &&
+                hipFuncSetAttribute((const void *) attention_tile_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                     (int) want) == hipSuccess) {
                 limit = want;
             } else {
@@ -2796,8 +2870,14 @@ int32_t nxg_attention(const float * q, const float * k, const float * v, const i
     const size_t tile_lds = ((size_t) ATT_P * smax + (size_t) ATT_KT * ATT_KS) * sizeof(float);
     if (ATT_P % rep == 0) {
         const long long n_tiles = (long long) n_kv_head * ((T + ATT_P / rep - 1) / (ATT_P / rep));
-        if (tile_lds <= attention_tile_lds_limit()) {
-            attention_tile_kernel<<<dim3((unsigned) n_tiles), dim3(256), tile_lds, (hipStream_t) stream>>>(p, smax);
+        const size_t lds_max = attention_tile_lds_limit();
+        if (tile_lds <= lds_max) {
+            // fewer than 3 workgroups per CU by LDS (the static 1 KiB included): the two-pair scores
+            if (3 * (tile_lds + 1024) > lds_max + 1024) {
+                attention_tile_kernel<true><<<dim3((unsigned) n_tiles), dim3(256), tile_lds, (hipStream_t) stream>>>(p, smax);
+            } else {
+                attention_tile_kernel<false><<<dim3((unsigned) n_tiles), dim3(256), tile_lds, (hipStream_t) stream>>>(p, smax);
+            }
             return launch_check("attention_tile_kernel");
         }
         attention_long_kernel<<<dim3((unsigned) n_tiles), dim3(256), 0, (hipStream_t) stream>>>(p);

@@ -135,18 +135,23 @@ class EncoderLinearPath:
         if events is None:
             fn()
             return
-        torch = self.torch
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
+        e = self.torch.cuda.Event(enable_timing=True)
         fn()
-        e1.record()
-        events.append((e0, e1) + tag)
+        e.record()
+        events.append((self._mark, e) + tag)
+        self._mark = e                         # this launch's end is the next one's start
 
     def step(self, gemm_events: Optional[List] = None, quant_events: Optional[List] = None) -> None:
         """One forward of the path on the current stream. With event lists, every GEMM
-        (tagged with its group and kind) and every quantization is bracketed by HIP events."""
+        (tagged with its group and kind) and every quantization is bracketed by HIP events:
+        one event before the first launch and one after each launch, so consecutive launches
+        share the event between them."""
         nxg = self.nxg
+        if gemm_events is not None or quant_events is not None:
+            if gemm_events is None or quant_events is None:
+                raise ValueError("step: pass both event lists or neither")
+            self._mark = self.torch.cuda.Event(enable_timing=True)
+            self._mark.record()
         for steps in self.layers:
             for key, first, wname, okey, res, g, gkind in steps:
                 qa = self.qacts[key]
