@@ -792,15 +792,19 @@ __device__ __forceinline__ void softmax_weights(float * Sp, int n, int sk, float
 // ATT_P / rep consecutive query rows times the rep query heads of one KV head, so that every
 // key and value row read into LDS serves all of them. Per pair the operations and their
 // order are attention_kernel's (the reference's scores_d64, softmax_exp, values_d64):
-//   scores    one thread per (pair, key): the 8 FMA chains (a_l = q[l] k[l], then
-//             fma(q[8c+l], k[8c+l], a_l) for c = 1..7) and the HADD tree (keys of whole
-//             groups of 8) or hsum256's (the last n % 8 keys) in registers, times the scale;
-//             kept in LDS, [pair][key - the pair's first key]
+//   scores    the 8 FMA chains (a_l = q[l] k[l], then fma(q[8c+l], k[8c+l], a_l) for
+//             c = 1..7) and the HADD tree (keys of whole groups of 8) or hsum256's (the last
+//             n % 8 keys) in registers, times the scale; kept in LDS, [pair][key - the pair's
+//             first key]. One thread per (pair, key), or with PAIR2 per (2 pairs, key), so
+//             that each staged key row is read from LDS once for both pairs: twice the query
+//             registers, chosen when the scores' LDS already limits a CU to two workgroups
 //   softmax   16 threads per pair: the maximum (a NaN first score wins), exp256 / the C
 //             library's expf in place, then threads l < 8 add the keys 8i + l in order of i
 //             (the 8 lanes of softmax_exp's accumulator) and hsum256 over them, the tail keys
 //             added after; each weight becomes w * (1 / sum)
-//   values    thread (dim d, 4 pairs): acc = fma(w_j, v_j[d], acc) over the keys in order.
+//   values    thread (dim d, 4 pairs): acc = fma(w_j, v_j[d], acc) over the keys in order;
+//             a tile's 32 weights of a pair are read once (lane l holds key j0 + l) and
+//             broadcast per key by readlane, so the key loop reads only v_j[d] from LDS.
 // Keys are staged ATT_KT at a time ([key][ATT_KS] floats; the padding puts the 16 rows one
 // wave reads on different banks). Pairs whose keys exceed smax get NaN, as attention_kernel.
 constexpr int ATT_P = 16;      // (query, head) pairs per workgroup
@@ -1849,9 +1853,10 @@ __device__ __forceinline__ void dma16s(const int8_t * base, uint32_t voff, uint3
 //    counts constant); wave 0 adds block B's scales at k-step 4B;
 //  - the wait at each k-step is therefore a constant vmcnt: 8, or 9 on wave 0 for
 //    the two k-steps whose later loads include its scale load;
-//  - the output phase first waits for all loads (the next tile's first three
-//    k-steps are then in LDS, so its first block waits only at k-step 3) and only
-//    then issues its stores, which the later waits count but no longer wait behind.
+//  - the output phase issues its stores at once (they write slot 3, free after the
+//    tile's last barrier); vmcnt counts loads and stores, which may complete out of
+//    order, so the next tile's first k-step waits for every outstanding operation
+//    (its three prefetched k-steps and the stores) before the constant counts resume.
 // The residual rows are loaded after the tile's last MFMAs, under the last epilogue.
 template <bool RES>
 __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
@@ -1978,7 +1983,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
         auto run_block = [&](int B, auto last_tag) {
             constexpr bool last = decltype(last_tag)::value;
             // k-step 4B (slot 0). In block 0 k-steps 0..2 are already in LDS.
-            if (B > 0) arrive(0); else lds_barrier();
+            // block 0: the tile's first three k-steps were loaded under the previous tile; the
+            // previous tile's output stores went out after them, so wait for everything
+            if (B > 0) arrive(0); else { wait_vm<0>(); lds_barrier(); }
             issue(cur, 4 * B + 3, 3);
             if (wave == 0) dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, ring + 3 * SLOT + SLOT_AB);
             mma(0, true);
@@ -2026,7 +2033,6 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
         // (lane: token lane%16, features 16ni + 4(lane/16) + 0..3), read it back as 4
         // rows of 256 bytes per instruction and store whole lines.
         lds_barrier();
-        wait_vm<0>();
         float * stg = reinterpret_cast<float *>(ring + 3 * SLOT + wave * 4352);
         const int trow = lane & 15, tcol = 4 * (lane >> 4);
 #pragma unroll
