@@ -1099,7 +1099,8 @@ __device__ __forceinline__ float score_d64(const float (&qv)[64], const float * 
 //           order of i, as softmax_exp's 8 accumulator lanes do; the tail e are kept apart and
 //           added after hsum256, in order
 //   pass 3  w = e * (1 / sum) per key through LDS, then thread (dim d, 4 pairs) acc = fma(w,
-//           v[d], acc) over the keys in order, as attention_tile_kernel
+//           v[d], acc) over the keys in order, as attention_tile_kernel (the tile's weights
+//           read once per lane and broadcast per key by readlane)
 // Keys and values are staged ATT_KT at a time ([key][ATT_KS]).
 __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
     __shared__ __attribute__((aligned(16))) float tile[ATT_KT * ATT_KS];
@@ -1266,12 +1267,32 @@ __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
         __syncthreads();
         if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
         const int jn = min(ATT_KT, kh - j0);
-        for (int jj = 0; jj < jn; ++jj) {
-            const float v = tile[jj * ATT_KS + d];
+        // pair i's weights of the tile: lane l holds key j0 + l (l < 32), broadcast per key
+        int a[4], b[4];
+        bool full = jn == ATT_KT;
+        float wl[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int jr = j0 + jj - vlo[i];
-                if (jr >= 0 && jr < vn[i]) acc[i] = __builtin_fmaf(E[4 * pg + i][jj], v, acc[i]);
+        for (int i = 0; i < 4; ++i) {                      // keys [a, b) of the tile are pair i's
+            a[i] = min(max(vlo[i] - j0, 0), jn);
+            b[i] = max(min(vlo[i] + vn[i] - j0, jn), a[i]);
+            full = full && a[i] == 0 && b[i] == jn;
+            wl[i] = E[4 * pg + i][d & 31];
+        }
+        auto wk = [&](int i, int jj) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl[i]), jj)); };
+        if (full) {
+            float vt[ATT_KT];
+#pragma unroll
+            for (int jj = 0; jj < ATT_KT; ++jj) vt[jj] = tile[jj * ATT_KS + d];
+#pragma unroll
+            for (int jj = 0; jj < ATT_KT; ++jj)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(wk(i, jj), vt[jj], acc[i]);
+        } else {
+            for (int jj = 0; jj < jn; ++jj) {
+                const float v = tile[jj * ATT_KS + d];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (jj >= a[i] && jj < b[i]) acc[i] = __builtin_fmaf(wk(i, jj), v, acc[i]);
             }
         }
     }
