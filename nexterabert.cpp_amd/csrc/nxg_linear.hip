@@ -788,6 +788,29 @@ __device__ __forceinline__ void softmax_weights(float * Sp, int n, int sk, float
     for (int j = sk; j < n; j += 16) Sp[j] = Sp[j] * inv;
 }
 
+// acc[i] = fma(w_i[lane L of this lane's 16-lane row], v, acc[i]) for i < 4: v_fmac_f32 (one
+// rounding, as fmaf) with its first operand broadcast by DPP row_newbcast. With w_i holding
+// key k of a 16-key group in lanes k, k + 16, k + 32, k + 48, every lane gets key L's weight.
+// The s_nop gives a DPP read its two wait states after any VALU write of w_i.
+template <int L>
+__device__ __forceinline__ void fmac_bcast4(float (&acc)[4], const float (&w)[4], float v) {
+    asm("s_nop 1\n\t"
+        "v_fmac_f32_dpp %0, %4, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %1, %5, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %2, %6, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %3, %7, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
+        : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
+        : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(v), "n"(L));
+}
+
+// 16 keys of a tile in order: key k (< 16) has its weights in lane k of each row of w and its
+// value in vt[k].
+template <int L = 0>
+__device__ __forceinline__ void fmac_bcast4_16(float (&acc)[4], const float (&w)[4], const float * vt) {
+    fmac_bcast4<L>(acc, w, vt[L]);
+    if constexpr (L + 1 < 16) fmac_bcast4_16<L + 1>(acc, w, vt);
+}
+
 // The same attention for a tile of (query, head) pairs: the ATT_P pairs of one workgroup are
 // ATT_P / rep consecutive query rows times the rep query heads of one KV head, so that every
 // key and value row read into LDS serves all of them. Per pair the operations and their
@@ -803,8 +826,9 @@ __device__ __forceinline__ void softmax_weights(float * Sp, int n, int sk, float
 //             (the 8 lanes of softmax_exp's accumulator) and hsum256 over them, the tail keys
 //             added after; each weight becomes w * (1 / sum)
 //   values    thread (dim d, 4 pairs): acc = fma(w_j, v_j[d], acc) over the keys in order;
-//             a tile's 32 weights of a pair are read once (lane l holds key j0 + l) and
-//             broadcast per key by readlane, so the key loop reads only v_j[d] from LDS.
+//             a tile's weights of a pair are read once, key j0 + 16h + k in lane k of every
+//             16-lane row of register h, and each fma takes its weight through DPP row_newbcast
+//             (readlane on partial tiles), so the key loop reads only v_j[d] from LDS.
 // Keys are staged ATT_KT at a time ([key][ATT_KS] floats; the padding puts the 16 rows one
 // wave reads on different banks). Pairs whose keys exceed smax get NaN, as attention_kernel.
 constexpr int ATT_P = 16;      // (query, head) pairs per workgroup
@@ -1030,21 +1054,23 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
         }
         // the tile's weights: pair i's weight of key j0 + l in lane l (l < 32), read once and
         // broadcast per key (readlane), so the key loop reads only the value row from LDS
-        float wl[4];
+        // weights of keys j0 + k (w0) and j0 + 16 + k (w1) of pair i in lane k of every 16-lane row
+        float w0[4], w1[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int jr = j0 + (d & 31) - vlo[i];
-            wl[i] = (jr >= 0 && jr < vn[i]) ? S[(size_t) (4 * pg + i) * smax + jr] : 0.0f;
+            const int jr = j0 + (d & 15) - vlo[i];
+            w0[i] = (jr >= 0 && jr < vn[i]) ? S[(size_t) (4 * pg + i) * smax + jr] : 0.0f;
+            w1[i] = (jr + 16 >= 0 && jr + 16 < vn[i]) ? S[(size_t) (4 * pg + i) * smax + jr + 16] : 0.0f;
         }
-        auto wk = [&](int i, int jj) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl[i]), jj)); };
+        auto wk = [&](int i, int jj) {
+            return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(jj < 16 ? w0[i] : w1[i]), jj & 15));
+        };
         if (full) {
             float vt[ATT_KT];                              // the tile's values of dimension d, read up front
 #pragma unroll
             for (int jj = 0; jj < ATT_KT; ++jj) vt[jj] = tile[jj * ATT_KS + d];
-#pragma unroll
-            for (int jj = 0; jj < ATT_KT; ++jj)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(wk(i, jj), vt[jj], acc[i]);
+            fmac_bcast4_16(acc, w0, vt);
+            fmac_bcast4_16(acc, w1, vt + 16);
         } else {
             for (int jj = 0; jj < jn; ++jj) {
                 const float v = tile[jj * ATT_KS + d];
@@ -1100,7 +1126,7 @@ __device__ __forceinline__ float score_d64(const float (&qv)[64], const float * 
 //           added after hsum256, in order
 //   pass 3  w = e * (1 / sum) per key through LDS, then thread (dim d, 4 pairs) acc = fma(w,
 //           v[d], acc) over the keys in order, as attention_tile_kernel (the tile's weights
-//           read once per lane and broadcast per key by readlane)
+//           read once per lane and broadcast per key by DPP row_newbcast or readlane)
 // Keys and values are staged ATT_KT at a time ([key][ATT_KS]).
 __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
     __shared__ __attribute__((aligned(16))) float tile[ATT_KT * ATT_KS];
@@ -1270,23 +1296,24 @@ __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
         // pair i's weights of the tile: lane l holds key j0 + l (l < 32), broadcast per key
         int a[4], b[4];
         bool full = jn == ATT_KT;
-        float wl[4];
+        float w0[4], w1[4];                                // keys j0 + k, j0 + 16 + k in lane k of each row
 #pragma unroll
         for (int i = 0; i < 4; ++i) {                      // keys [a, b) of the tile are pair i's
             a[i] = min(max(vlo[i] - j0, 0), jn);
             b[i] = max(min(vlo[i] + vn[i] - j0, jn), a[i]);
             full = full && a[i] == 0 && b[i] == jn;
-            wl[i] = E[4 * pg + i][d & 31];
+            w0[i] = E[4 * pg + i][d & 15];
+            w1[i] = E[4 * pg + i][16 + (d & 15)];
         }
-        auto wk = [&](int i, int jj) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl[i]), jj)); };
+        auto wk = [&](int i, int jj) {
+            return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(jj < 16 ? w0[i] : w1[i]), jj & 15));
+        };
         if (full) {
             float vt[ATT_KT];
 #pragma unroll
             for (int jj = 0; jj < ATT_KT; ++jj) vt[jj] = tile[jj * ATT_KS + d];
-#pragma unroll
-            for (int jj = 0; jj < ATT_KT; ++jj)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(wk(i, jj), vt[jj], acc[i]);
+            fmac_bcast4_16(acc, w0, vt);
+            fmac_bcast4_16(acc, w1, vt + 16);
         } else {
             for (int jj = 0; jj < jn; ++jj) {
                 const float v = tile[jj * ATT_KS + d];
