@@ -79,7 +79,10 @@ NXG_API int32_t nxg_encoder_encode(nxg_encoder * e, const int32_t * tokens, cons
 /* The same forward on device buffers, launched on `stream` (a hipStream_t; NULL: the
  * default stream) without synchronising: tokens / token_types device int32, hidden / pooled
  * device float (either may be NULL); lengths stay on the host. Token ids are not checked
- * here (the kernels clamp them into the table): the caller validates them. */
+ * here (the kernels clamp them into the table): the caller validates them. A call whose
+ * lengths differ from the previous call's waits for `stream` and uploads the new offsets,
+ * scales and RoPE tables (and may grow the work area); a call with the same lengths does
+ * neither, so only such calls may be captured into a HIP graph. */
 NXG_API int32_t nxg_encoder_forward(nxg_encoder * e, const int32_t * tokens, const int32_t * token_types,
                                     const int32_t * lengths, int32_t n_seqs, float * hidden, float * pooled,
                                     int32_t normalize, void * stream);

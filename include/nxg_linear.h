@@ -304,6 +304,16 @@ NXG_API int32_t nxg_linear_i8(const nxg_weight * w, const int8_t * q, const floa
 NXG_API int32_t nxg_linear_i8_rows(const nxg_weight * w, const int8_t * q, const float * sx, int32_t T,
                                    const float * residual, float * out, void * stream);
 
+/* nxg_linear_i8_rows for projections that share an input, fused along n_out into one weight
+ * (rows and per-block scales concatenated): columns [c_k, c_k + cols[k]) of the product,
+ * c_k = cols[0] + ... + cols[k-1], go to outs[k], a dense device float [T][cols[k]] array,
+ * so one launch replaces n_seg calls of builder::linear (src/nexterabert.cpp:1121-1138) on
+ * the same qact. Each column is computed exactly as by nxg_linear_i8_rows. No residual;
+ * n_in % 256 == 0; 1 <= n_seg <= 4; every boundary c_k (k > 0) a multiple of 64 and every
+ * cols[k] a multiple of 4, summing to n_out; outs[k] 16-byte aligned. */
+NXG_API int32_t nxg_linear_i8_rows_split(const nxg_weight * w, const int8_t * q, const float * sx, int32_t T,
+                                         int32_t n_seg, const int32_t * cols, float * const * outs, void * stream);
+
 /* The MLP's c_fc -> relu^2 -> int8 in one pass (src/nexterabert.cpp:1286-1288: linear
  * of c_fc, then op_relu_sqr quantized for the int8 c_proj): the fp32 linear output f of
  * nxg_linear_i8 (no residual) is never written; q_out, sx_out receive exactly what

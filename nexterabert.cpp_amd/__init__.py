@@ -109,6 +109,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_weight_device_bytes": ([P], sz),
         "nxg_linear_i8": ([P, P, P, P, i32, P, P, P], i32),
         "nxg_linear_i8_rows": ([P, P, P, i32, P, P, P], i32),
+        "nxg_linear_i8_rows_split": ([P, P, P, i32, i32, P, P, P], i32),
         "nxg_linear_i8_block_sums": ([P, P, i32, P, P], i32),
         "nxg_linear_i8_relu2_q8": ([P, P, P, P, i32, i32, P, P, P], i32),
         "nxg_linear_i8_relu2_q8_rows": ([P, P, P, i32, i32, P, P, P], i32),
@@ -668,6 +669,29 @@ def linear_i8(weight: DeviceWeight, qa: QAct, residual=None, cu_offsets: Optiona
                                   out.data_ptr(), _stream_ptr(stream))
     _check(rc, "linear_i8")
     return out
+
+
+def linear_i8_split(weight: DeviceWeight, qa: QAct, cols: Sequence[int], outs=None, stream=None):
+    """linear_i8 of a weight fused along n_out from several projections of the same input:
+    one launch; columns [c_k, c_k + cols[k]) go to outs[k], a [T][cols[k]] float32 tensor
+    (allocated when outs is None). Every boundary c_k must be a multiple of 64."""
+    torch = _torch()
+    if qa.n_in != weight.n_in:
+        raise ValueError(f"n_in mismatch: activations {qa.n_in}, weight {weight.n_in}")
+    cols = [int(c) for c in cols]
+    T = qa.T
+    if outs is None:
+        outs = [torch.empty((T, c), dtype=torch.float32, device=qa.q.device) for c in cols]
+    if len(outs) != len(cols):
+        raise ValueError("one output per segment")
+    for o, c in zip(outs, cols):
+        _check_rows(o, T, c, "out")
+    cols_a = np.ascontiguousarray(cols, dtype=np.int32)
+    ptrs = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    _check(load_library().nxg_linear_i8_rows_split(weight.handle, qa.q.data_ptr(), qa.sx.data_ptr(), T, len(cols),
+                                                   _np_ptr(cols_a), ctypes.cast(ptrs, ctypes.c_void_p),
+                                                   _stream_ptr(stream)), "linear_i8_split")
+    return outs
 
 
 def linear_i8_relu2_q8(weight: DeviceWeight, qa: QAct, act_max: int = 127,

@@ -131,6 +131,12 @@ struct nxg_encoder {
     int32_t act_max = 127;
     int32_t n_layers_run = -1;                 // nextera_debug_set_layers
     std::unordered_map<std::string, nxg_weight *> i8;
+    // projections of one input fused along n_out (key: group name), launched as one split GEMM
+    struct fused_w {
+        nxg_weight * w = nullptr;
+        std::vector<int32_t> cols;
+    };
+    std::unordered_map<std::string, fused_w> fused;
     std::unordered_map<std::string, f32_tensor> f32;
     std::unordered_map<std::string, float> scalar;   // 1-element tensors (scalable_factor.s / .b)
     size_t weight_bytes = 0;
@@ -167,6 +173,9 @@ struct nxg_encoder {
                 int32_t normalize, hipStream_t s);
     // the pieces of builder (src/nexterabert.cpp:1080-1268)
     int32_t linear(const std::string & name, const qact & in, int32_t rows, const float * res, float * out, hipStream_t s);
+    // the projections `names` of `in` (fused group `key` when it exists) into outs
+    int32_t project(const std::string & key, const std::vector<std::string> & names, const qact & in, int32_t rows,
+                    std::initializer_list<float *> outs, hipStream_t s);
     int32_t attention(const std::string & pre, const qact & h, int32_t rows, const int32_t * cu_dev, int32_t n_seqs,
                       const rope_dev & rope, int32_t half, const float * scale, int32_t max_keys, float * out,
                       hipStream_t s);
@@ -176,6 +185,7 @@ struct nxg_encoder {
 
 nxg_encoder::~nxg_encoder() {
     for (auto & kv : i8) nxg_weight_destroy(kv.second);
+    for (auto & kv : fused) nxg_weight_destroy(kv.second.w);
     for (auto & kv : f32) release(kv.second.dev);
     for (rope_dev & r : rope) {
         release(r.cos);
@@ -289,7 +299,7 @@ int32_t nxg_encoder::prepare(const int32_t * lens, int32_t n_seqs, hipStream_t s
     // the previous forward may still read the offsets, scales and tables being replaced
     NXG_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
     NXG_TRY(ensure_work(total, total_b, n_seqs));
-    lengths.assign(lens, lens + n_seqs);
+    lengths.clear();                           // recorded again once every upload below has succeeded
     T = (int32_t) total;
     TB = (int32_t) total_b;
     max_len = mx;
@@ -336,6 +346,7 @@ int32_t nxg_encoder::prepare(const int32_t * lens, int32_t n_seqs, hipStream_t s
     NXG_HIP(hipMemcpy(cub, cub_h.data(), cub_h.size() * sizeof(int32_t), hipMemcpyHostToDevice), "hipMemcpy(cu)");
     NXG_HIP(hipMemcpy(scales, scales_h.data(), scales_h.size() * sizeof(float), hipMemcpyHostToDevice),
             "hipMemcpy(scales)");
+    lengths.assign(lens, lens + n_seqs);
     return NXG_OK;
 }
 
@@ -344,15 +355,60 @@ int32_t nxg_encoder::linear(const std::string & name, const qact & in, int32_t r
     return nxg_linear_i8_rows(i8.at(name), in.q, in.sx, rows, res, out, s);
 }
 
+int32_t nxg_encoder::project(const std::string & key, const std::vector<std::string> & names, const qact & in,
+                             int32_t rows, std::initializer_list<float *> outs, hipStream_t s) {
+    const auto f = fused.find(key);
+    if (f != fused.end()) {
+        float * o[4] = {};
+        int n = 0;
+        for (float * p : outs) o[n++] = p;
+        return nxg_linear_i8_rows_split(f->second.w, in.q, in.sx, rows, n, f->second.cols.data(), o, s);
+    }
+    auto it = outs.begin();
+    for (const std::string & name : names) NXG_TRY(linear(name, in, rows, nullptr, *it++, s));
+    return NXG_OK;
+}
+
+namespace {
+
+// The projection groups that read one input: fused along n_out at load when the split GEMM
+// takes them (n_in % 256 == 0, boundaries at multiples of 64).
+struct proj_group {
+    std::string key;
+    std::vector<std::string> names;
+};
+
+std::vector<proj_group> proj_groups(const hparams & hp) {
+    std::vector<proj_group> v;
+    for (int32_t l = 0; l < hp.n_layer; ++l) {
+        const std::string pre = "blocks." + std::to_string(l) + ".attn.";
+        const proj_group qkv{ pre + "qkv", { pre + "c_q.weight", pre + "c_k.weight", pre + "c_v.weight" } };
+        switch (hp.block_types[l]) {
+            case MIX_SWA:
+            case MIX_ATTN: v.push_back(qkv); break;
+            case MIX_LILY:
+                v.push_back({ pre + "lily_in", { pre + "ltc_conv.in_proj.weight", pre + "ltc_conv.A.weight",
+                                                 pre + "x_proj.weight", pre + "B_proj.weight" } });
+                break;
+            case MIX_HRA:
+                v.push_back({ pre + "hra_in", { pre + "qkv_in.weight", pre + "qkv_gate.weight", pre + "c_C.weight" } });
+                v.push_back(qkv);
+                break;
+        }
+    }
+    return v;
+}
+
+} // namespace
+
 // builder::attention (src/nexterabert.cpp:1184-1204): q / k / v projections of h, q and k
 // through qk_prep (k head-major), v head-major, then op_attention inside each document.
 int32_t nxg_encoder::attention(const std::string & pre, const qact & h, int32_t rows, const int32_t * cu_dev,
                                int32_t n_seqs, const rope_dev & r, int32_t half, const float * scale,
                                int32_t max_keys, float * out, hipStream_t s) {
     const int32_t H = hp.n_head, G = hp.n_kv_head, D = hp.head_dim;
-    NXG_TRY(linear(pre + "c_q.weight", h, rows, nullptr, F[0], s));
-    NXG_TRY(linear(pre + "c_k.weight", h, rows, nullptr, K[0], s));
-    NXG_TRY(linear(pre + "c_v.weight", h, rows, nullptr, K[2], s));
+    NXG_TRY(project(pre + "qkv", { pre + "c_q.weight", pre + "c_k.weight", pre + "c_v.weight" }, h, rows,
+                    { F[0], K[0], K[2] }, s));
     NXG_TRY(nxg_qk_prep(F[0], w(pre + "q_norm.alpha"), w(pre + "q_norm.beta"), r.cos, r.sin, r.n_pos, cu_dev, n_seqs,
                         rows, H, D, 0, F[1], s));
     NXG_TRY(nxg_qk_prep(K[0], w(pre + "k_norm.alpha"), w(pre + "k_norm.beta"), r.cos, r.sin, r.n_pos, cu_dev, n_seqs,
@@ -401,14 +457,13 @@ int32_t nxg_encoder::run(const int32_t * ids_dev, const int32_t * types_dev, int
                 break;
             }
             case MIX_LILY: {                   // mix_lily (:1224-1244)
-                NXG_TRY(linear(pre + "ltc_conv.in_proj.weight", qa_h, T, nullptr, Z[0], s));
-                NXG_TRY(linear(pre + "ltc_conv.A.weight", qa_h, T, nullptr, Z[1], s));
+                NXG_TRY(project(pre + "lily_in", { pre + "ltc_conv.in_proj.weight", pre + "ltc_conv.A.weight",
+                                                   pre + "x_proj.weight", pre + "B_proj.weight" },
+                                qa_h, T, { Z[0], Z[1], F[1], F[2] }, s));
                 const f32_tensor & ltc = f32.at(pre + "ltc_conv.kernel");
                 NXG_TRY(nxg_dwconv_quantize_rows(Z[0], Z[1], ltc.dev, ltc.rows, cu, n_seqs, T, R, act_max, qa_R.q,
                                                  qa_R.sx, s));
                 NXG_TRY(linear(pre + "ltc_conv.out_proj.weight", qa_R, T, nullptr, F[0], s));
-                NXG_TRY(linear(pre + "x_proj.weight", qa_h, T, nullptr, F[1], s));
-                NXG_TRY(linear(pre + "B_proj.weight", qa_h, T, nullptr, F[2], s));
                 const f32_tensor & st = f32.at(pre + "state_conv.depthwise.weight");
                 NXG_TRY(nxg_lily_state_quantize_rows(F[0], F[1], F[2], st.dev, st.rows, cu, n_seqs, T, C, act_max,
                                                      qa_g.q, qa_g.sx, s));
@@ -416,14 +471,13 @@ int32_t nxg_encoder::run(const int32_t * ids_dev, const int32_t * types_dev, int
                 break;
             }
             case MIX_HRA: {                    // mix_hra (:1246-1268)
-                NXG_TRY(linear(pre + "qkv_in.weight", qa_h, T, nullptr, F[4], s));
+                NXG_TRY(project(pre + "hra_in", { pre + "qkv_in.weight", pre + "qkv_gate.weight", pre + "c_C.weight" },
+                                qa_h, T, { F[4], F[6], F[7] }, s));
                 const f32_tensor & qc = f32.at(pre + "qkv_conv.depthwise.weight");
                 NXG_TRY(nxg_dwconv_rows(F[4], nullptr, qc.dev, qc.rows, cu, n_seqs, T, C, F[5], s));
-                NXG_TRY(linear(pre + "qkv_gate.weight", qa_h, T, nullptr, F[6], s));
                 NXG_TRY(nxg_block_mean_quantize_rows(F[5], F[6], cu, cub, n_seqs, T, TB, hp.hra_block, C, act_max,
                                                      qa_hb.q, qa_hb.sx, s));
                 NXG_TRY(attention(pre, qa_hb, TB, cub, n_seqs, rope[0], -1, scale, max_blocks, F[2], s));
-                NXG_TRY(linear(pre + "c_C.weight", qa_h, T, nullptr, F[7], s));
                 NXG_TRY(nxg_upsample_add(F[2], F[7], cu, cub, n_seqs, T, TB, hp.hra_block, C, F[4], s));
                 const f32_tensor & co = f32.at(pre + "c_o.depthwise.weight");
                 NXG_TRY(nxg_dwconv_rows(F[4], nullptr, co.dev, co.rows, cu, n_seqs, T, C, F[5], s));
@@ -511,6 +565,51 @@ std::vector<need> needed(const hparams & hp) {
         v.push_back({ blk + "mlp.c_proj.weight", hp.n_inter, C });
     }
     return v;
+}
+
+// One int8 weight from the linears `names` of the open file, concatenated along n_out: each
+// expanded as nxg_gguf_weight_create does (build_i8_weight, src/nexterabert.cpp:1010-1049),
+// rows appended, and the per-block scales of block B side by side in the same order.
+int32_t fuse_weights(nxg_gguf * g, const std::unordered_map<std::string, int64_t> & index,
+                     const std::vector<std::string> & names, int32_t n_threads, nxg_weight ** out) {
+    try {
+        std::vector<int8_t> W;
+        std::vector<std::vector<float>> S;
+        std::vector<int32_t> n_outs;
+        int64_t n_in = -1, N = 0;
+        for (const std::string & name : names) {
+            const auto at = index.find(name);
+            if (at == index.end()) return fail(NXG_EINVAL, "encoder: '%s' missing", name.c_str());
+            int32_t type = 0, nd = 0;
+            int64_t ne[4];
+            NXG_TRY(nxg_gguf_tensor_info(g, at->second, &type, &nd, ne, nullptr, nullptr));
+            if (n_in < 0) n_in = ne[0];
+            if (ne[0] != n_in || ne[1] <= 0 || ne[1] > INT32_MAX) return fail(NXG_EINVAL, "encoder: '%s' cannot join its group", name.c_str());
+            const int32_t n_o = (int32_t) ne[1];
+            const int64_t n_blk = (n_in + NXG_BLOCK - 1) / NXG_BLOCK;
+            std::vector<int8_t> w((size_t) (n_in * n_o));
+            std::vector<float> sc((size_t) (n_blk * n_o));
+            NXG_TRY(nxg_expand_weight(type, nxg_gguf_tensor_data(g, at->second), (int32_t) n_in, n_o, 128, n_threads,
+                                      w.data(), sc.data(), nullptr));
+            W.insert(W.end(), w.begin(), w.end());
+            S.push_back(std::move(sc));
+            n_outs.push_back(n_o);
+            N += n_o;
+        }
+        if (N > INT32_MAX) return fail(NXG_EINVAL, "encoder: fused group of %lld rows", (long long) N);
+        const int64_t n_blk = (n_in + NXG_BLOCK - 1) / NXG_BLOCK;
+        std::vector<float> SC((size_t) (n_blk * N));
+        for (int64_t B = 0; B < n_blk; ++B) {
+            int64_t o = 0;
+            for (size_t k = 0; k < S.size(); ++k) {
+                std::copy_n(S[k].begin() + B * n_outs[k], n_outs[k], SC.begin() + B * N + o);
+                o += n_outs[k];
+            }
+        }
+        return nxg_weight_create(W.data(), SC.data(), (int32_t) n_in, (int32_t) N, out);
+    } catch (const std::bad_alloc &) {
+        return fail(NXG_ENOMEM, "encoder: out of host memory fusing '%s'", names.front().c_str());
+    }
 }
 
 bool encoder_tensor(const std::string & name) {
@@ -664,6 +763,35 @@ int32_t load_into(nxg_encoder & e, const char * path, const nxg_encoder_params &
         if (!ok) return fail(NXG_EINVAL, "encoder: tensor '%s' has an unexpected shape (%d x %d)", nd.name.c_str(), t.rows, t.cols);
     }
     e.fuse_mlp = hp.n_embd % 256 == 0;         // nxg_linear_i8_relu2_q8's shape rule (n_out % 32 checked above)
+    // projections of one input fused along n_out, one split GEMM launch each (the separate
+    // weights are then freed); the split GEMM needs n_in % 256 == 0 and boundaries at
+    // multiples of 64, otherwise the group stays separate
+    if (hp.n_embd % 256 == 0) {
+        std::unordered_map<std::string, int64_t> index;
+        for (int64_t i = 0; i < n_tensors; ++i) index[nxg_gguf_tensor_name(g, i)] = i;
+        for (const proj_group & pg : proj_groups(hp)) {
+            std::vector<int32_t> cols;
+            int64_t end = 0;
+            bool ok = pg.names.size() <= 4;
+            for (size_t k = 0; k < pg.names.size(); ++k) {
+                const int32_t c = nxg_weight_n_out(e.i8.at(pg.names[k]));
+                cols.push_back(c);
+                end += c;
+                if (c % 4 != 0 || (k + 1 < pg.names.size() && end % 64 != 0)) ok = false;
+            }
+            if (!ok) continue;
+            nxg_encoder::fused_w f;
+            f.cols = cols;
+            NXG_TRY(fuse_weights(g, index, pg.names, params.load_threads, &f.w));
+            e.fused[pg.key] = f;
+            e.weight_bytes += nxg_weight_device_bytes(f.w);
+            for (const std::string & n : pg.names) {
+                e.weight_bytes -= nxg_weight_device_bytes(e.i8[n]);
+                nxg_weight_destroy(e.i8[n]);
+                e.i8.erase(n);
+            }
+        }
+    }
     return NXG_OK;
 }
 

@@ -1589,7 +1589,31 @@ struct gemm_params {
     int8_t *       qo;    // MF x KSo fragments
     float *        sxo;   // [MP/4][n_nt][4]
     int KSo;              // ceil(N / 64)
+    // split output (0: none): columns [seg_end[k-1], seg_end[k]) go to seg_out[k], a dense
+    // [T][seg_end[k] - seg_end[k-1]] array; every boundary is a multiple of 64
+    int n_seg;
+    int seg_end[4];
+    float * seg_out[4];
 };
+
+// Where output column n of row t goes: base + t * ld + col.
+struct out_map {
+    float * base;
+    int col, ld;
+};
+__device__ __forceinline__ out_map out_of(const gemm_params & p, int n) {
+    out_map m{ p.out, n, p.N };
+    if (p.n_seg > 0) {
+        int lo = 0, hi = p.seg_end[0];
+        float * b = p.seg_out[0];
+        // the segments are kernel arguments: selected, not indexed
+        if (p.n_seg > 1 && n >= p.seg_end[0]) { b = p.seg_out[1]; lo = p.seg_end[0]; hi = p.seg_end[1]; }
+        if (p.n_seg > 2 && n >= p.seg_end[1]) { b = p.seg_out[2]; lo = p.seg_end[1]; hi = p.seg_end[2]; }
+        if (p.n_seg > 3 && n >= p.seg_end[2]) { b = p.seg_out[3]; lo = p.seg_end[2]; hi = p.seg_end[3]; }
+        m = out_map{ b, n - lo, hi - lo };
+    }
+    return m;
+}
 
 // Tiles of one workgroup. Workgroups are dispatched to the 8 XCDs round-robin
 // (workgroup w runs on XCD w % 8). Each XCD owns a contiguous range of tile
@@ -2081,6 +2105,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
         // (lane: token lane%16, features 16ni + 4(lane/16) + 0..3), read it back as 4
         // rows of 256 bytes per instruction and store whole lines.
         lds_barrier();
+        const out_map om = out_of(p, ncol);
         float * stg = reinterpret_cast<float *>(ring + 3 * SLOT + wave * 4352);
         const int trow = lane & 15, tcol = 4 * (lane >> 4);
 #pragma unroll
@@ -2098,7 +2123,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
                 const int t = tbase + mi * 16 + row;
                 if (t < p.T && col_ok) {
                     if (RES) y = rv[mi][q] + y;
-                    __builtin_nontemporal_store(y, reinterpret_cast<v4f *>(p.out + (size_t) t * p.N + ncol));
+                    __builtin_nontemporal_store(y, reinterpret_cast<v4f *>(om.base + (size_t) t * om.ld + om.col));
                 }
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -2332,7 +2357,8 @@ __global__ __launch_bounds__(64) void gemm_small(gemm_params p) {
             if (n >= p.N) continue;
             v4f y = { f[j][i][0], f[j][i][1], f[j][i][2], f[j][i][3] };
             if (RES) y = rv[j][i] + y;
-            *reinterpret_cast<v4f *>(p.out + (size_t) t * p.N + n) = y;
+            const out_map om = out_of(p, n);
+            *reinterpret_cast<v4f *>(om.base + (size_t) t * om.ld + om.col) = y;
         }
     }
 }
@@ -3121,6 +3147,9 @@ struct gemm_out {
     int8_t *      qo = nullptr;
     float *       sxo = nullptr;
     int           act_max = 127;
+    int           n_seg = 0;                 // split output: column counts and buffers
+    const int32_t * seg_cols = nullptr;
+    float * const * seg_out = nullptr;
 };
 
 static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float * sx, int32_t T,
@@ -3128,10 +3157,32 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     if (!W) return fail(NXG_EINVAL, "linear: null weight");
     if (T < 0) return fail(NXG_EINVAL, "linear: T=%d", T);
     if (T == 0) return NXG_OK;
-    if (!q || (!o.sums && !sx) || (!o.sums && !o.qo && !o.out) || (o.qo && !o.sxo)) {
+    const bool k256 = W->KS % 4 == 0;
+    if (o.n_seg) {
+        // split output: n_in % 256 == 0 (gemm_k256 / gemm_small), boundaries at multiples of 64
+        if (o.n_seg < 1 || o.n_seg > 4 || !o.seg_cols || !o.seg_out || o.residual || o.sums || o.qo) {
+            return fail(NXG_EINVAL, "linear_split: n_seg=%d (1..4, no residual)", o.n_seg);
+        }
+        if (!k256 || W->n_out % 4 != 0 || NXG_WG_PER_CU <= 0) {
+            return fail(NXG_EINVAL, "linear_split: needs n_in %% 256 == 0 and n_out %% 4 == 0 (n_in=%d n_out=%d)",
+                        W->n_in, W->n_out);
+        }
+        int end = 0;
+        for (int k = 0; k < o.n_seg; ++k) {
+            if (o.seg_cols[k] <= 0 || (k + 1 < o.n_seg && (end + o.seg_cols[k]) % 64 != 0) || o.seg_cols[k] % 4 != 0) {
+                return fail(NXG_EINVAL, "linear_split: segment %d has %d columns (boundaries at multiples of 64)", k,
+                            o.seg_cols[k]);
+            }
+            if (!o.seg_out[k] || ((uintptr_t) o.seg_out[k] & 15)) {
+                return fail(NXG_EINVAL, "linear_split: segment %d: null or unaligned buffer", k);
+            }
+            end += o.seg_cols[k];
+        }
+        if (end != W->n_out) return fail(NXG_EINVAL, "linear_split: segments cover %d columns, the weight has %d", end, W->n_out);
+    } else if (!q || (!o.sums && !sx) || (!o.sums && !o.qo && !o.out) || (o.qo && !o.sxo)) {
         return fail(NXG_EINVAL, "linear: null buffer");
     }
-    const bool k256 = W->KS % 4 == 0;
+    if (!q || (!o.sums && !sx)) return fail(NXG_EINVAL, "linear: null buffer");
     if (o.qo) {
         if (!k256 || W->n_out % 32 != 0) {
             return fail(NXG_EINVAL, "linear_relu2_q8: needs n_in %% 256 == 0 and n_out %% 32 == 0 (n_in=%d n_out=%d)",
@@ -3156,6 +3207,12 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     p.NP = W->NP;
     p.KS = W->KS;
     p.KSo = ceil_div(p.N, 64);
+    p.n_seg = o.n_seg;
+    for (int k = 0, end = 0; k < 4; ++k) {
+        if (k < o.n_seg) end += o.seg_cols[k];
+        p.seg_end[k] = end;
+        p.seg_out[k] = k < o.n_seg ? o.seg_out[k] : nullptr;
+    }
     p.n_blk = W->n_blk;
     p.MF = ceil_div(T, 16);
     p.n_mt = ceil_div(T, BM);
@@ -3248,6 +3305,16 @@ int32_t nxg_linear_i8_rows(const nxg_weight * W, const int8_t * q, const float *
     gemm_out o;
     o.residual = residual;
     o.out = out;
+    return launch_gemm(W, q, sx, T, o, stream);
+}
+
+int32_t nxg_linear_i8_rows_split(const nxg_weight * W, const int8_t * q, const float * sx, int32_t T,
+                                 int32_t n_seg, const int32_t * cols, float * const * outs, void * stream) {
+    gemm_out o;
+    if (n_seg < 1) return fail(NXG_EINVAL, "linear_split: n_seg=%d", n_seg);
+    o.n_seg = n_seg;
+    o.seg_cols = cols;
+    o.seg_out = outs;
     return launch_gemm(W, q, sx, T, o, stream);
 }
 
