@@ -211,6 +211,17 @@ NXG_API int32_t nxg_qk_prep(const float * x, const float * alpha, const float * 
 NXG_API int32_t nxg_head_major(const float * x, int32_t T, int32_t n_head, int32_t head_dim, float * out,
                                void * stream);
 
+/* The three ops builder::attention applies to one layer's projections (src/nexterabert.cpp:
+ * 1186-1188) in one launch, each element as by the separate calls: nxg_qk_prep of the
+ * queries q [T][n_head * head_dim] (q_alpha / q_beta, row-major into q_out), nxg_qk_prep of
+ * the keys k [T][n_kv_head * head_dim] (k_alpha / k_beta, head-major into k_out) and
+ * nxg_head_major of the values v into v_out. */
+NXG_API int32_t nxg_qkv_prep(const float * q, const float * k, const float * v, const float * q_alpha,
+                             const float * q_beta, const float * k_alpha, const float * k_beta, const float * cos_t,
+                             const float * sin_t, int32_t n_pos, const int32_t * cu_offsets, int32_t n_seqs,
+                             int32_t T, int32_t n_head, int32_t n_kv_head, int32_t head_dim, float * q_out,
+                             float * k_out, float * v_out, void * stream);
+
 /* op_dwconv writing fp32 rows (src/nexterabert.cpp:524-543, row_op(..., false): HRA's qkv_conv
  * and c_o, :1252, :1265): out = r (or 0 with r null), then out = fma(taps[j], x[t + j - k/2], out)
  * for the taps j whose row lies in t's document, in order of j.

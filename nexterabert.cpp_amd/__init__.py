@@ -84,6 +84,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_attention_scales": ([P, i32, i32, i32, ctypes.c_float, ctypes.c_float, ctypes.c_float, P], i32),
         "nxg_qk_prep": ([P, P, P, P, P, i32, P, i32, i32, i32, i32, i32, P, P], i32),
         "nxg_head_major": ([P, i32, i32, i32, P, P], i32),
+        "nxg_qkv_prep": ([P, P, P, P, P, P, P, P, P, i32, P, i32, i32, i32, i32, i32, P, P, P, P], i32),
         "nxg_dwconv_rows": ([P, P, P, i32, P, i32, i32, i32, P, P], i32),
         "nxg_upsample_add": ([P, P, P, P, i32, i32, i32, i32, i32, P, P], i32),
         "nxg_embed_rows": ([P, i32, P, P, i32, P, i32, i32, P, P], i32),
@@ -529,6 +530,36 @@ def head_major(x, n_head: int, out=None, stream=None):
         out = torch.empty((n_head, T, D), dtype=torch.float32, device=x.device)
     _check(load_library().nxg_head_major(x.data_ptr(), T, n_head, D, out.data_ptr(), _stream_ptr(stream)), "head_major")
     return out
+
+
+def qkv_prep(q, k, v, q_alpha, q_beta, k_alpha, k_beta, cos_t, sin_t, cu_offsets: Sequence[int], n_head: int,
+             n_kv_head: int, stream=None):
+    """qk_prep(q) (row-major), qk_prep(k) (head-major) and head_major(v) in one launch, each
+    element as by the separate calls. Returns (q_out [T][n_head*D], k_out and v_out
+    [n_kv_head][T][D])."""
+    torch = _torch()
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _rows_arg(t, name)
+    T, width = q.shape
+    D = width // n_head
+    if D * n_head != width or D % 2 or tuple(k.shape) != (T, n_kv_head * D) or tuple(v.shape) != (T, n_kv_head * D):
+        raise ValueError("q must be [T][n_head * D], k and v [T][n_kv_head * D], D even")
+    for name, t in (("q_alpha", q_alpha), ("q_beta", q_beta), ("k_alpha", k_alpha), ("k_beta", k_beta)):
+        if t.dtype != torch.float32 or tuple(t.shape) != (D,) or not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 device tensor [{D}]")
+    _rows_arg(cos_t, "cos_t")
+    _rows_arg(sin_t, "sin_t", cos_t.shape)
+    if cos_t.shape[1] != D // 2:
+        raise ValueError(f"cos_t / sin_t must be [n_pos][{D // 2}]")
+    cu = _device_offsets(cu_offsets, q.device)
+    qo = torch.empty((T, width), dtype=torch.float32, device=q.device)
+    ko = torch.empty((n_kv_head, T, D), dtype=torch.float32, device=q.device)
+    vo = torch.empty((n_kv_head, T, D), dtype=torch.float32, device=q.device)
+    _check(load_library().nxg_qkv_prep(q.data_ptr(), k.data_ptr(), v.data_ptr(), q_alpha.data_ptr(), q_beta.data_ptr(),
+                                       k_alpha.data_ptr(), k_beta.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(),
+                                       cos_t.shape[0], cu.data_ptr(), cu.numel() - 1, T, n_head, n_kv_head, D,
+                                       qo.data_ptr(), ko.data_ptr(), vo.data_ptr(), _stream_ptr(stream)), "qkv_prep")
+    return qo, ko, vo
 
 
 def dwconv_rows(x, taps, cu_offsets, r=None, out=None, stream=None):

@@ -409,11 +409,9 @@ int32_t nxg_encoder::attention(const std::string & pre, const qact & h, int32_t 
     const int32_t H = hp.n_head, G = hp.n_kv_head, D = hp.head_dim;
     NXG_TRY(project(pre + "qkv", { pre + "c_q.weight", pre + "c_k.weight", pre + "c_v.weight" }, h, rows,
                     { F[0], K[0], K[2] }, s));
-    NXG_TRY(nxg_qk_prep(F[0], w(pre + "q_norm.alpha"), w(pre + "q_norm.beta"), r.cos, r.sin, r.n_pos, cu_dev, n_seqs,
-                        rows, H, D, 0, F[1], s));
-    NXG_TRY(nxg_qk_prep(K[0], w(pre + "k_norm.alpha"), w(pre + "k_norm.beta"), r.cos, r.sin, r.n_pos, cu_dev, n_seqs,
-                        rows, G, D, 1, K[1], s));
-    NXG_TRY(nxg_head_major(K[2], rows, G, D, K[3], s));
+    NXG_TRY(nxg_qkv_prep(F[0], K[0], K[2], w(pre + "q_norm.alpha"), w(pre + "q_norm.beta"), w(pre + "k_norm.alpha"),
+                         w(pre + "k_norm.beta"), r.cos, r.sin, r.n_pos, cu_dev, n_seqs, rows, H, G, D, F[1], K[1], K[3],
+                         s));
     return nxg_attention(F[1], K[1], K[3], cu_dev, n_seqs, scale, rows, H, G, half, max_keys, out, s);
 }
 

@@ -1353,14 +1353,12 @@ __device__ __forceinline__ float tanh_ref(float x) {
 // head, i < D/2): a = beta[i] tanh(alpha[i] x1[i]), b = beta[D/2+i] tanh(alpha[D/2+i] x2[i]),
 // y1 = fma(a, cos, b sin), y2 = fma(-a, sin, b cos) at the row's position in its document.
 // Output row-major [T][H*D] or head-major [H][T][D].
-__global__ __launch_bounds__(256) void qk_prep_kernel(const float * __restrict__ x, const float * __restrict__ alpha,
-                                                      const float * __restrict__ beta, const float * __restrict__ cos_t,
-                                                      const float * __restrict__ sin_t, const int32_t * __restrict__ cu,
-                                                      int n_seqs, int T, int H, int D, int n_pos, int head_major,
-                                                      float * __restrict__ out) {
+__device__ __forceinline__ void qk_prep_elem(const float * __restrict__ x, const float * __restrict__ alpha,
+                                             const float * __restrict__ beta, const float * __restrict__ cos_t,
+                                             const float * __restrict__ sin_t, const int32_t * __restrict__ cu,
+                                             int n_seqs, int T, int H, int D, int n_pos, int head_major,
+                                             float * __restrict__ out, size_t idx) {
     const int half = D / 2;
-    const size_t idx = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t) T * H * half) return;
     const int i = (int) (idx % half);
     const int h = (int) ((idx / half) % H);
     const int t = (int) (idx / ((size_t) half * H));
@@ -1375,15 +1373,63 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const float * __restrict__
     y[half + i] = __builtin_fmaf(-a, s, b * c);
 }
 
-// op_head_major (src/nexterabert.cpp:620-632): [T][H*D] -> [H][T][D].
-__global__ __launch_bounds__(256) void head_major_kernel(const float * __restrict__ x, int T, int H, int D,
-                                                         float * __restrict__ out) {
+__global__ __launch_bounds__(256) void qk_prep_kernel(const float * __restrict__ x, const float * __restrict__ alpha,
+                                                      const float * __restrict__ beta, const float * __restrict__ cos_t,
+                                                      const float * __restrict__ sin_t, const int32_t * __restrict__ cu,
+                                                      int n_seqs, int T, int H, int D, int n_pos, int head_major,
+                                                      float * __restrict__ out) {
     const size_t idx = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t) T * H * D) return;
+    if (idx >= (size_t) T * H * (D / 2)) return;
+    qk_prep_elem(x, alpha, beta, cos_t, sin_t, cu, n_seqs, T, H, D, n_pos, head_major, out, idx);
+}
+
+// op_head_major (src/nexterabert.cpp:620-632): [T][H*D] -> [H][T][D].
+__device__ __forceinline__ void head_major_elem(const float * __restrict__ x, int T, int H, int D,
+                                                float * __restrict__ out, size_t idx) {
     const int e = (int) (idx % D);
     const int h = (int) ((idx / D) % H);
     const int t = (int) (idx / ((size_t) D * H));
     out[((size_t) h * T + t) * D + e] = x[idx];
+}
+
+__global__ __launch_bounds__(256) void head_major_kernel(const float * __restrict__ x, int T, int H, int D,
+                                                         float * __restrict__ out) {
+    const size_t idx = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t) T * H * D) return;
+    head_major_elem(x, T, H, D, out, idx);
+}
+
+// builder::attention's three ops on one layer's projections (src/nexterabert.cpp:1186-1188) in
+// one launch: qk_prep of the queries (row-major), qk_prep of the keys (head-major) and the
+// values' head-major copy, each thread taking one element of one of them by index range.
+struct qkv_prep_params {
+    const float * q;
+    const float * k;
+    const float * v;
+    const float * q_alpha;
+    const float * q_beta;
+    const float * k_alpha;
+    const float * k_beta;
+    const float * cos_t;
+    const float * sin_t;
+    const int32_t * cu;
+    int n_seqs, T, H, G, D, n_pos;
+    float * q_out;
+    float * k_out;
+    float * v_out;
+};
+__global__ __launch_bounds__(256) void qkv_prep_kernel(qkv_prep_params p) {
+    const size_t idx = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t nq = (size_t) p.T * p.H * (p.D / 2), nk = (size_t) p.T * p.G * (p.D / 2);
+    const size_t nv = (size_t) p.T * p.G * p.D;
+    if (idx < nq) {
+        qk_prep_elem(p.q, p.q_alpha, p.q_beta, p.cos_t, p.sin_t, p.cu, p.n_seqs, p.T, p.H, p.D, p.n_pos, 0, p.q_out, idx);
+    } else if (idx < nq + nk) {
+        qk_prep_elem(p.k, p.k_alpha, p.k_beta, p.cos_t, p.sin_t, p.cu, p.n_seqs, p.T, p.G, p.D, p.n_pos, 1, p.k_out,
+                     idx - nq);
+    } else if (idx < nq + nk + nv) {
+        head_major_elem(p.v, p.T, p.G, p.D, p.v_out, idx - nq - nk);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -2998,6 +3044,29 @@ int32_t nxg_head_major(const float * x, int32_t T, int32_t n_head, int32_t head_
     if (rc) return rc;
     head_major_kernel<<<(unsigned) ((n + 255) / 256), 256, 0, (hipStream_t) stream>>>(x, T, n_head, head_dim, out);
     return launch_check("head_major_kernel");
+}
+
+int32_t nxg_qkv_prep(const float * q, const float * k, const float * v, const float * q_alpha, const float * q_beta,
+                     const float * k_alpha, const float * k_beta, const float * cos_t, const float * sin_t, int32_t n_pos,
+                     const int32_t * cu_offsets, int32_t n_seqs, int32_t T, int32_t n_head, int32_t n_kv_head,
+                     int32_t head_dim, float * q_out, float * k_out, float * v_out, void * stream) {
+    if (T < 0 || n_head < 1 || n_kv_head < 1 || head_dim < 2 || head_dim % 2 != 0 || n_pos < 1 || n_seqs < 1) {
+        return fail(NXG_EINVAL, "qkv_prep: T=%d n_head=%d n_kv_head=%d head_dim=%d n_pos=%d n_seqs=%d", T, n_head,
+                    n_kv_head, head_dim, n_pos, n_seqs);
+    }
+    if (T == 0) return NXG_OK;
+    if (!q || !k || !v || !q_alpha || !q_beta || !k_alpha || !k_beta || !cos_t || !sin_t || !cu_offsets || !q_out ||
+        !k_out || !v_out) {
+        return fail(NXG_EINVAL, "qkv_prep: null buffer");
+    }
+    const size_t n = (size_t) T * (n_head + n_kv_head) * (head_dim / 2) + (size_t) T * n_kv_head * head_dim;
+    if (n / 256 + 1 > (size_t) INT32_MAX) return fail(NXG_EINVAL, "qkv_prep: too large");
+    int rc = check_device();
+    if (rc) return rc;
+    const qkv_prep_params p{ q, k, v, q_alpha, q_beta, k_alpha, k_beta, cos_t, sin_t, cu_offsets, n_seqs, T,
+                             n_head, n_kv_head, head_dim, n_pos, q_out, k_out, v_out };
+    qkv_prep_kernel<<<(unsigned) ((n + 255) / 256), 256, 0, (hipStream_t) stream>>>(p);
+    return launch_check("qkv_prep_kernel");
 }
 
 int32_t nxg_dwconv_rows(const float * x, const float * r, const float * taps, int32_t k, const int32_t * cu_offsets,

@@ -154,6 +154,27 @@ def test_qk_prep_matches_oracle(nxg, orc, torch, dev, head_major):
     assert (bits(y) == bits(orc.qk_prep(x, alpha, beta, c, s, cu, H, head_major=head_major))).all()
 
 
+@pytest.mark.parametrize("H,G", [(16, 8), (2, 1), (4, 4)])
+def test_qkv_prep_equals_separate_calls(nxg, torch, dev, H, G):
+    """nxg_qkv_prep: the queries' and keys' qk_prep and the values' head-major copy in one
+    launch give the separate calls' bits (test_qk_prep_matches_oracle pins those)."""
+    say(f"qkv_prep H={H} G={G}")
+    rng = np.random.default_rng(H + G)
+    D = 64
+    cu = nxg.cu_offsets_of([1, 7, 100, 33])
+    T = int(cu[-1])
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    q, k, v = (t(rng.standard_normal((T, n * D)) * 3) for n in (H, G, G))
+    qa, qb, ka, kb = (t(rng.uniform(0.2, 2.0, D)) for _ in range(4))
+    c, s = nxg.rope_table(128, 10000.0, D)
+    c, s = t(c), t(s)
+    qo, ko, vo = nxg.qkv_prep(q, k, v, qa, qb, ka, kb, c, s, cu, H, G)
+    refs = (nxg.qk_prep(q, qa, qb, c, s, cu, H), nxg.qk_prep(k, ka, kb, c, s, cu, G, head_major=True),
+            nxg.head_major(v, G))
+    for got, ref in zip((qo, ko, vo), refs):
+        assert (bits(got.cpu().numpy()) == bits(ref.cpu().numpy())).all()
+
+
 def test_head_major(nxg, torch, dev):
     say("head_major")
     x = torch.randn(77, 8 * 64, device="cuda")
