@@ -134,7 +134,8 @@ NXG_API int32_t nxg_quantize_rows_relu2(const float * x, int32_t T, int32_t n_in
  * :414-438; chosen by rms_norm(..., int8_only(...)), e.g. :1285): each row becomes
  * (x * inv) * gain with inv = 1 / sqrt(dot / n_in + eps), dot = dot_f32(x, x) in the
  * reference's AVX2 accumulation order (:124-149), then quantize_row as nxg_quantize_rows.
- *   gain  device float [n_in] (the norm's weight);  eps  the model's rms_norm_epsilon */
+ *   x     device float [T][n_in], 16-byte aligned
+ *   gain  device float [n_in] (the norm's weight), 16-byte aligned;  eps  the model's rms_norm_epsilon */
 NXG_API int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps, int32_t T, int32_t n_in,
                                           int32_t act_max, int8_t * q, float * sx, void * stream);
 

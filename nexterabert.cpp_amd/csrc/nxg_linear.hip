@@ -2912,6 +2912,7 @@ int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps
     if (act_max != 127 && act_max != 63) return fail(NXG_EINVAL, "rmsnorm_quantize: act_max must be 127 or 63, got %d", act_max);
     if (T == 0) return NXG_OK;
     if (!x || !gain || !q || !sx) return fail(NXG_EINVAL, "rmsnorm_quantize: null buffer");
+    if (!aligned16(x) || !aligned16(gain)) return fail(NXG_EINVAL, "rmsnorm_quantize: x and gain must be 16-byte aligned");
     int rc = check_device();
     if (rc) return rc;
     hipStream_t s = (hipStream_t) stream;

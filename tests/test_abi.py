@@ -71,6 +71,15 @@ def test_arguments_checked_before_device_work(nxg):
     h = ctypes.c_void_p()
     assert L.nxg_weight_create(w.ctypes.data, s.ctypes.data, 48, 4, ctypes.byref(h)) == nxg.NXG_EINVAL
     assert h.value is None
+    # the split GEMM and the fused q/k/v preparation check their arguments first too
+    cols = (ctypes.c_int32 * 2)(64, 64)
+    assert L.nxg_linear_i8_rows_split(None, None, None, 4, 2, cols, None, None) == nxg.NXG_EINVAL
+    assert L.nxg_linear_i8_rows_split(None, None, None, 4, 0, cols, None, None) == nxg.NXG_EINVAL
+    assert L.nxg_qkv_prep(*([None] * 9), 1, None, 1, 4, 16, 8, 63, None, None, None, None) == nxg.NXG_EINVAL
+    assert b"head_dim=63" in L.nxg_last_error()
+    # RMSNorm's vector loads: x and gain must be 16-byte aligned (no pointer is dereferenced)
+    assert L.nxg_rmsnorm_quantize_rows(4, 16, ctypes.c_float(1e-6), 16, 256, 127, 16, 16, None) == nxg.NXG_EINVAL
+    assert b"aligned" in L.nxg_last_error()
 
 
 def test_device_calls_fail_loudly_without_gpu(nxg):
