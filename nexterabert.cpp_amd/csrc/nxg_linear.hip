@@ -343,13 +343,17 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(const float * __r
 // kq % 16, kq = 32 (m' % 2) + 2c + e), then each wave stores whole 1 KiB fragments. A
 // NaN anywhere in the group's normalized values sends the group through quantize_block,
 // whose fold gives the reference's MAXPS result; without NaN that fold is the plain max.
-template <int ACT_MAX, int NB>
+// SPLIT (few rows): one workgroup per (row group, block), the dot still over the whole row
+// from registers, only block blockIdx % NB quantized and stored -- NB times the workgroups
+// for launches too small to fill the device.
+template <int ACT_MAX, int NB, bool SPLIT>
 __global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float * __restrict__ x, const float * __restrict__ gain,
                                                          float eps, int T, int8_t * __restrict__ q,
                                                          float * __restrict__ sx) {
     constexpr int n_in = NB * BLK, M = n_in / 32, KS = 4 * NB;
     __shared__ __attribute__((aligned(16))) int stage[KS * FRAG / 4];
-    const int g = (int) blockIdx.x;
+    const int g = SPLIT ? (int) (blockIdx.x / NB) : (int) blockIdx.x;
+    const int Bs = SPLIT ? (int) (blockIdx.x % NB) : 0;       // SPLIT: the block of this workgroup
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rl = wave * 4 + (lane >> 4), t = g * 16 + rl, c = lane & 15;
     float2 v[M];
@@ -380,6 +384,7 @@ __global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float * __restric
     if (__syncthreads_or(nan)) {
         const src_rms src{src_rows{x, n_in}, gain, inv};
         for (int B = 0; B < NB; ++B) {
+            if (SPLIT && B != Bs) continue;
             quantize_block<ACT_MAX>(src, T, n_in, KS, NB, q, sx, g, B, stage);
             __syncthreads();
         }
@@ -388,6 +393,7 @@ __global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float * __restric
     unsigned short * st16 = reinterpret_cast<unsigned short *>(stage);
 #pragma unroll
     for (int B = 0; B < NB; ++B) {
+        if (SPLIT && B != Bs) continue;
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fmaxf(abs_bits(v[8 * B + i].x), abs_bits(v[8 * B + i].y)));
@@ -404,6 +410,12 @@ __global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float * __restric
         if (c == 0) sx[((size_t) (t >> 2) * NB + B) * 4 + (t & 3)] = t < T ? scale : 0.0f;
     }
     __syncthreads();
+    if (SPLIT) {
+        const int f = 4 * Bs + wave;                       // wave w stores fragment w of the block
+        const int4 w = reinterpret_cast<const int4 *>(stage)[f * 64 + lane];
+        *reinterpret_cast<int4 *>(q + ((size_t) g * KS + f) * FRAG + lane * 16) = w;
+        return;
+    }
 #pragma unroll
     for (int f = wave; f < KS; f += 4) {
         const int4 w = reinterpret_cast<const int4 *>(stage)[f * 64 + lane];
@@ -2918,11 +2930,18 @@ int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps
     hipStream_t s = (hipStream_t) stream;
     if (n_in % BLK == 0) {
         // the whole row group in registers: n_in = 256, 512, 1024 or 2048
-        const dim3 grid((unsigned) (d.MP / 16));
+        // fewer row groups than twice the CUs: one workgroup per (row group, block)
+        const bool split = (long long) (d.MP / 16) < 2LL * device_cus();
+        const dim3 grid((unsigned) (d.MP / 16)), grid_s((unsigned) (d.MP / 16 * d.n_blk));
 #define NXG_RMS_Q8(NB)                                                                                        \
         case NB:                                                                                              \
-            if (act_max == 127) rmsnorm_q8_kernel<127, NB><<<grid, 256, 0, s>>>(x, gain, eps, T, q, sx);       \
-            else                rmsnorm_q8_kernel<63, NB><<<grid, 256, 0, s>>>(x, gain, eps, T, q, sx);        \
+            if (split) {                                                                                      \
+                if (act_max == 127) rmsnorm_q8_kernel<127, NB, true><<<grid_s, 256, 0, s>>>(x, gain, eps, T, q, sx); \
+                else                rmsnorm_q8_kernel<63, NB, true><<<grid_s, 256, 0, s>>>(x, gain, eps, T, q, sx);  \
+            } else {                                                                                          \
+                if (act_max == 127) rmsnorm_q8_kernel<127, NB, false><<<grid, 256, 0, s>>>(x, gain, eps, T, q, sx); \
+                else                rmsnorm_q8_kernel<63, NB, false><<<grid, 256, 0, s>>>(x, gain, eps, T, q, sx);  \
+            }                                                                                                 \
             return launch_check("rmsnorm_q8_kernel");
         switch (d.n_blk) {
             NXG_RMS_Q8(1)

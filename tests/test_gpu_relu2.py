@@ -186,11 +186,13 @@ def test_relu2_q8_bad_shapes_raise(nxg, torch, dev):
 
 
 @pytest.mark.parametrize("T,n_in", [(333, 1024), (100, 2304), (17, 32), (50, 96), (1, 4096),
-                                    (1000, 256), (45, 512), (70, 2048), (4111, 1024)])
+                                    (1000, 256), (45, 512), (70, 2048), (4111, 1024), (8200, 1024)])
 @pytest.mark.parametrize("act_max", [127, 63])
 def test_rmsnorm_quantize_matches_oracle(nxg, orc, torch, dev, T, n_in, act_max):
     """op_rms_norm feeding an int8 linear: the oracle's RMSNorm (AVX2 dot order), then
-    quantize_row; rows of very different scales, eps 1e-8 and 0, NaN/Inf/zero rows."""
+    quantize_row; rows of very different scales, eps 1e-8 and 0, NaN/Inf/zero rows. n_in of
+    whole 256-blocks up to 2,048 take the register-resident kernel, one workgroup per (16 rows,
+    block) below 2 row groups per CU and one per 16 rows from there (8,200 rows on 256 CUs)."""
     say(f"rmsnorm_quantize T={T} n_in={n_in} act_max={act_max}")
     rng = np.random.default_rng(T + n_in + act_max)
     x = (rng.standard_normal((T, n_in)) * 10.0 ** rng.integers(-6, 6, (T, 1))).astype(np.float32)
