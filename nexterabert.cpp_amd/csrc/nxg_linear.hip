@@ -491,6 +491,9 @@ __device__ __forceinline__ doc_rows doc_of(const int32_t * cu, int n, int t, int
 // op_dwconv (src/nexterabert.cpp:524-543): out = r (or 0), then for every tap j whose
 // row t + j - k/2 lies in t's document, out = fma(taps[j], x[t + j - k/2], out) in order
 // of j (addmul_f32, :166-176). taps [k][C].
+// taps whose rows a convolution source loads before any of its fmas (the models' kernels: 3, 5)
+constexpr int TAPS_HOIST = 5;
+
 struct src_dwconv {
     const float * x;
     const float * r;                           // may be null
@@ -504,6 +507,28 @@ struct src_dwconv {
             v[0] = rv.x; v[1] = rv.y; v[2] = rv.z; v[3] = rv.w;
         } else {
             v[0] = v[1] = v[2] = v[3] = 0.0f;
+        }
+        if (k <= TAPS_HOIST) {
+            // every tap's row loaded first (rows clamped into the batch, so always in bounds),
+            // then the fmas of the taps inside the document in tap order
+            v4f w[TAPS_HOIST], xv[TAPS_HOIST];
+#pragma unroll
+            for (int j = 0; j < TAPS_HOIST; ++j) {
+                if (j >= k) break;
+                const int tt = min(max(t + j - k / 2, 0), T - 1);
+                w[j] = *reinterpret_cast<const v4f *>(taps + (size_t) j * C + col);
+                xv[j] = *reinterpret_cast<const v4f *>(x + (size_t) tt * C + col);
+            }
+#pragma unroll
+            for (int j = 0; j < TAPS_HOIST; ++j) {
+                const int tt = t + j - k / 2;
+                if (j >= k || tt < dr.lo || tt >= dr.hi) continue;
+                v[0] = __builtin_fmaf(w[j].x, xv[j].x, v[0]);
+                v[1] = __builtin_fmaf(w[j].y, xv[j].y, v[1]);
+                v[2] = __builtin_fmaf(w[j].z, xv[j].z, v[2]);
+                v[3] = __builtin_fmaf(w[j].w, xv[j].w, v[3]);
+            }
+            return;
         }
         for (int j = 0; j < k; ++j) {
             const int tt = t + j - k / 2;
@@ -532,6 +557,29 @@ struct src_lily_state {
     __device__ void load(const doc_rows & dr, int t, int col, float (&v)[4]) const {
         const int j0 = max(0, dr.lo - (t - k / 2)), j1 = min(k, dr.hi - (t - k / 2));
         float acc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+        if (k <= TAPS_HOIST) {
+            // every tap's rows loaded first (clamped into the batch), then the fmas of taps j0..j1-1
+            v4f w[TAPS_HOIST], av[TAPS_HOIST], xv[TAPS_HOIST];
+#pragma unroll
+            for (int j = 0; j < TAPS_HOIST; ++j) {
+                if (j >= k) break;
+                const size_t o = (size_t) min(max(t + j - k / 2, 0), T - 1) * C + col;
+                w[j] = *reinterpret_cast<const v4f *>(taps + (size_t) j * C + col);
+                av[j] = *reinterpret_cast<const v4f *>(a + o);
+                xv[j] = *reinterpret_cast<const v4f *>(x + o);
+            }
+#pragma unroll
+            for (int j = 0; j < TAPS_HOIST; ++j) {
+                if (j >= k || j < j0 || j >= j1) continue;
+                acc[0] = __builtin_fmaf(w[j].x, av[j].x * xv[j].x, acc[0]);
+                acc[1] = __builtin_fmaf(w[j].y, av[j].y * xv[j].y, acc[1]);
+                acc[2] = __builtin_fmaf(w[j].z, av[j].z * xv[j].z, acc[2]);
+                acc[3] = __builtin_fmaf(w[j].w, av[j].w * xv[j].w, acc[3]);
+            }
+            const v4f bv = *reinterpret_cast<const v4f *>(b + (size_t) t * C + col);
+            v[0] = acc[0] * bv.x; v[1] = acc[1] * bv.y; v[2] = acc[2] * bv.z; v[3] = acc[3] * bv.w;
+            return;
+        }
         for (int j = j0; j < j1; ++j) {
             const size_t o = (size_t) (t + j - k / 2) * C + col;
             const v4f w = *reinterpret_cast<const v4f *>(taps + (size_t) j * C + col);
