@@ -196,6 +196,25 @@ NXG_API int32_t nxg_attention(const float * q, const float * k, const float * v,
                               int32_t n_seqs, const float * scale, int32_t T, int32_t n_head, int32_t n_kv_head,
                               int32_t half, int32_t max_keys, float * out, void * stream);
 
+/* op_attention (src/nexterabert.cpp:785-852) as nxg_attention, with a device workspace for documents whose scores do not fit in LDS (more than
+ * ~2,400 keys per query with n_head / n_kv_head dividing 16): each score is computed once and
+ * kept in the workspace for the softmax and the values, instead of being recomputed in each of
+ * three passes; the outputs are the same bits. The workspace holds one slot of
+ * 16 * max_keys floats per resident workgroup; a smaller one (at least one slot) runs fewer
+ * workgroups at a time, and none (NULL, 0) the recomputing kernel. Other launches ignore it.
+ * Calls that share a workspace must not overlap.
+ *   workspace        device memory, 4-byte aligned, or NULL
+ *   workspace_bytes  its size (nxg_attention_workspace_bytes gives the size for every slot) */
+NXG_API int32_t nxg_attention_ws(const float * q, const float * k, const float * v, const int32_t * cu_offsets,
+                                 int32_t n_seqs, const float * scale, int32_t T, int32_t n_head, int32_t n_kv_head,
+                                 int32_t half, int32_t max_keys, float * out, void * workspace,
+                                 int64_t workspace_bytes, void * stream);
+
+/* Sizing for nxg_attention_ws (no counterpart in the reference, whose op_attention keeps a
+ * document's scores in host memory): the workspace it uses for these sizes: 0 when the launch does not need one,
+ * else one slot per resident workgroup (a negative NXG_E* code for invalid sizes). */
+NXG_API int64_t nxg_attention_workspace_bytes(int32_t T, int32_t n_head, int32_t n_kv_head, int32_t max_keys);
+
 /* op_qk_prep (src/nexterabert.cpp:590-632): the separable DyT (beta * tanh(alpha * x), with
  * tanh256's arithmetic) then RoPE at each row's position in its document:
  *   x          device float [T][n_head * head_dim]

@@ -81,6 +81,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_lily_state_quantize_rows": ([P, P, P, P, i32, P, i32, i32, i32, i32, P, P, P], i32),
         "nxg_block_mean_quantize_rows": ([P, P, P, P, i32, i32, i32, i32, i32, i32, P, P, P], i32),
         "nxg_attention": ([P, P, P, P, i32, P, i32, i32, i32, i32, i32, P, P], i32),
+        "nxg_attention_ws": ([P, P, P, P, i32, P, i32, i32, i32, i32, i32, P, P, i64, P], i32),
+        "nxg_attention_workspace_bytes": ([i32, i32, i32, i32], i64),
         "nxg_attention_scales": ([P, i32, i32, i32, ctypes.c_float, ctypes.c_float, ctypes.c_float, P], i32),
         "nxg_qk_prep": ([P, P, P, P, P, i32, P, i32, i32, i32, i32, i32, P, P], i32),
         "nxg_head_major": ([P, i32, i32, i32, P, P], i32),
@@ -457,10 +459,22 @@ def attention_scales(cu_offsets: Sequence[int], head_dim: int = 64, mode: int = 
     return out
 
 
+def attention_workspace_bytes(T: int, n_head: int, n_kv_head: int, max_keys: int) -> int:
+    """nxg_attention_workspace_bytes: the workspace attention(..., workspace="auto") allocates
+    (0 when the launch keeps its scores in LDS)."""
+    n = int(load_library().nxg_attention_workspace_bytes(T, n_head, n_kv_head, max_keys))
+    if n < 0:
+        _check(n, "attention_workspace_bytes")
+    return n
+
+
 def attention(q, k, v, cu_offsets: Sequence[int], scale, n_head: int, n_kv_head: int, half: int = -1,
-              out=None, stream=None):
+              out=None, stream=None, workspace=None):
     """op_attention with head_dim 64 inside each document: q [T][n_head*64], k / v
-    [n_kv_head][T][64] head-major, scale per document (host or device floats)."""
+    [n_kv_head][T][64] head-major, scale per document (host or device floats).
+    workspace: None (nxg_attention), a uint8 device tensor, or "auto" (one of
+    attention_workspace_bytes) for nxg_attention_ws, which keeps the scores of documents too
+    long for LDS in it instead of recomputing them."""
     torch = _torch()
     _rows_arg(q, "q")
     T = q.shape[0]
@@ -479,9 +493,22 @@ def attention(q, k, v, cu_offsets: Sequence[int], scale, n_head: int, n_kv_head:
     sc = sc.to(device=q.device, dtype=torch.float32).contiguous()
     if out is None:
         out = torch.empty_like(q)
-    _check(load_library().nxg_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), cu.data_ptr(), cu.numel() - 1,
-                                        sc.data_ptr(), T, n_head, n_kv_head, half, max(1, max_keys), out.data_ptr(),
-                                        _stream_ptr(stream)), "attention")
+    if workspace is None:
+        _check(load_library().nxg_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), cu.data_ptr(), cu.numel() - 1,
+                                            sc.data_ptr(), T, n_head, n_kv_head, half, max(1, max_keys),
+                                            out.data_ptr(), _stream_ptr(stream)), "attention")
+        return out
+    if isinstance(workspace, str):
+        if workspace != "auto":
+            raise ValueError('workspace must be None, "auto" or a uint8 device tensor')
+        workspace = torch.empty(attention_workspace_bytes(T, n_head, n_kv_head, max(1, max_keys)),
+                                dtype=torch.uint8, device=q.device)
+    if workspace.dtype != torch.uint8 or not workspace.is_cuda or not workspace.is_contiguous():
+        raise ValueError("workspace must be a contiguous uint8 device tensor")
+    _check(load_library().nxg_attention_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), cu.data_ptr(), cu.numel() - 1,
+                                           sc.data_ptr(), T, n_head, n_kv_head, half, max(1, max_keys),
+                                           out.data_ptr(), workspace.data_ptr() if workspace.numel() else None,
+                                           workspace.numel(), _stream_ptr(stream)), "attention")
     return out
 
 

@@ -143,10 +143,11 @@ struct nxg_encoder {
     hipStream_t stream = nullptr;
     double last_ms = 0.0;
 
-    // work area, sized for cap_T rows, cap_TB block rows and cap_seqs sequences
+    // work area, sized for cap_T rows, cap_TB block rows, cap_seqs sequences and cap_keys tokens
+    // in the longest one
     void * work = nullptr;
     size_t work_bytes = 0;
-    int64_t cap_T = -1, cap_TB = -1, cap_seqs = -1;
+    int64_t cap_T = -1, cap_TB = -1, cap_seqs = -1, cap_keys = -1;
     float * x[2] = {};
     float * F[8] = {};                         // [T][C]
     float * K[4] = {};                         // [T][KV]
@@ -157,6 +158,8 @@ struct nxg_encoder {
     qact qa_h, qa_y, qa_g, qa_I, qa_R, qa_hb;
     int32_t * ids = nullptr, * types = nullptr, * cu = nullptr, * cub = nullptr;
     float * scales = nullptr;                  // [n_layer][n_seqs]
+    void * attn_ws = nullptr;                  // nxg_attention_ws's scores of long documents
+    int64_t attn_ws_bytes = 0;
 
     // the batch layout the device buffers hold (prepare_batch, :1341-1371)
     std::vector<int32_t> lengths, cu_h, cub_h;
@@ -167,7 +170,7 @@ struct nxg_encoder {
 
     ~nxg_encoder();
     const float * w(const std::string & name) const { return f32.at(name).dev; }
-    int32_t ensure_work(int64_t T, int64_t TB, int64_t n_seqs);
+    int32_t ensure_work(int64_t T, int64_t TB, int64_t n_seqs, int64_t n_keys);
     int32_t prepare(const int32_t * lengths, int32_t n_seqs, hipStream_t s);
     int32_t run(const int32_t * ids, const int32_t * types, int32_t n_seqs, float * hidden, float * pooled,
                 int32_t normalize, hipStream_t s);
@@ -212,9 +215,13 @@ struct carver {
 
 } // namespace
 
-int32_t nxg_encoder::ensure_work(int64_t nT, int64_t nTB, int64_t n_seqs) {
-    if (work && nT <= cap_T && nTB <= cap_TB && n_seqs <= cap_seqs) return NXG_OK;
+int32_t nxg_encoder::ensure_work(int64_t nT, int64_t nTB, int64_t n_seqs, int64_t n_keys) {
+    if (work && nT <= cap_T && nTB <= cap_TB && n_seqs <= cap_seqs && n_keys <= cap_keys) return NXG_OK;
     const int64_t T_ = std::max(nT, cap_T), TB_ = std::max(nTB, cap_TB), S_ = std::max(n_seqs, cap_seqs);
+    const int64_t K_ = std::max(n_keys, cap_keys);
+    // attention over at most K_ keys on T_ rows (HRA's block rows: fewer rows and keys, less space)
+    const int64_t ws = nxg_attention_workspace_bytes((int32_t) T_, hp.n_head, hp.n_kv_head, (int32_t) K_);
+    if (ws < 0) return (int32_t) ws;
     const int C = hp.n_embd, KV = hp.n_kv_head * hp.head_dim, R = std::max(hp.lily_rank, 32), I = hp.n_inter;
     auto layout = [&](char * base) {
         carver c{base};
@@ -241,6 +248,7 @@ int32_t nxg_encoder::ensure_work(int64_t nT, int64_t nTB, int64_t n_seqs) {
         c.take(cu, (size_t) (S_ + 1) * sizeof(int32_t));
         c.take(cub, (size_t) (S_ + 1) * sizeof(int32_t));
         c.take(scales, (size_t) std::max(hp.n_layer, 1) * S_ * sizeof(float));
+        c.take(attn_ws, (size_t) ws);
         return c.off;
     };
     const size_t bytes = layout(nullptr);
@@ -253,7 +261,8 @@ int32_t nxg_encoder::ensure_work(int64_t nT, int64_t nTB, int64_t n_seqs) {
     void * p = nullptr;
     const hipError_t e = hipMalloc(&p, bytes);
     if (e != hipSuccess) {
-        cap_T = cap_TB = cap_seqs = -1;
+        cap_T = cap_TB = cap_seqs = cap_keys = -1;
+        attn_ws_bytes = 0;
         return fail(NXG_ENOMEM, "encoder: %zu bytes of work memory for %lld rows: %s", bytes, (long long) T_,
                     hipGetErrorString(e));
     }
@@ -263,6 +272,8 @@ int32_t nxg_encoder::ensure_work(int64_t nT, int64_t nTB, int64_t n_seqs) {
     cap_T = T_;
     cap_TB = TB_;
     cap_seqs = S_;
+    cap_keys = K_;
+    attn_ws_bytes = ws;
     lengths.clear();                           // device offsets and scales must be uploaded again
     return NXG_OK;
 }
@@ -298,7 +309,7 @@ int32_t nxg_encoder::prepare(const int32_t * lens, int32_t n_seqs, hipStream_t s
     }
     // the previous forward may still read the offsets, scales and tables being replaced
     NXG_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
-    NXG_TRY(ensure_work(total, total_b, n_seqs));
+    NXG_TRY(ensure_work(total, total_b, n_seqs, mx));
     lengths.clear();                           // recorded again once every upload below has succeeded
     T = (int32_t) total;
     TB = (int32_t) total_b;
@@ -412,7 +423,8 @@ int32_t nxg_encoder::attention(const std::string & pre, const qact & h, int32_t 
     NXG_TRY(nxg_qkv_prep(F[0], K[0], K[2], w(pre + "q_norm.alpha"), w(pre + "q_norm.beta"), w(pre + "k_norm.alpha"),
                          w(pre + "k_norm.beta"), r.cos, r.sin, r.n_pos, cu_dev, n_seqs, rows, H, G, D, F[1], K[1], K[3],
                          s));
-    return nxg_attention(F[1], K[1], K[3], cu_dev, n_seqs, scale, rows, H, G, half, max_keys, out, s);
+    return nxg_attention_ws(F[1], K[1], K[3], cu_dev, n_seqs, scale, rows, H, G, half, max_keys, out,
+                            attn_ws_bytes ? attn_ws : nullptr, attn_ws_bytes, s);
 }
 
 // builder::gated_out (:1206-1213): x + c_proj(sigmoid(c_gate(y)) * z), the gate quantized

@@ -1188,7 +1188,13 @@ __device__ __forceinline__ float score_d64(const float (&qv)[64], const float * 
 //           v[d], acc) over the keys in order, as attention_tile_kernel (the tile's weights
 //           read once per lane and broadcast per key by DPP row_newbcast or readlane)
 // Keys and values are staged ATT_KT at a time ([key][ATT_KS]).
-__global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
+// STORED: pass 1 also writes each score to the workgroup's slot of the workspace sc
+// ([gridDim.x][ATT_P][max_keys] floats, pair-relative key index), and passes 2 and 3 read the
+// scores back instead of recomputing them, the same bits; pass 2 then needs no staged keys
+// (lane l < 8 of a pair adds keys 16b + l and 16b + 8 + l, the second taken from lane l + 8),
+// pass 3 stages only the values. One call is the tile bt = (KV head, query block).
+template <bool STORED>
+__device__ __forceinline__ void attention_long_tile(const attn_params & p, float * __restrict__ sc, int bt) {
     __shared__ __attribute__((aligned(16))) float tile[ATT_KT * ATT_KS];
     __shared__ float E[ATT_P][ATT_KT + 1];                 // one tile's e (pass 2) or w (pass 3)
     __shared__ float tail_e[ATT_P][8];
@@ -1197,7 +1203,7 @@ __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
     const int tid = (int) threadIdx.x;
     const int rep = p.H / p.G, nq = ATT_P / rep;
     const int n_qblk = (p.T + nq - 1) / nq;
-    const int g = (int) blockIdx.x / n_qblk, t0 = ((int) blockIdx.x - g * n_qblk) * nq;
+    const int g = bt / n_qblk, t0 = (bt - g * n_qblk) * nq;
 
     if (tid < ATT_P) {
         const int t = t0 + tid / rep;
@@ -1232,6 +1238,7 @@ __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
     const int sp = tid >> 4, sk = tid & 15;
     const int plo = lo_s[sp], n_p = hi_s[sp] - plo, ng_p = n_p & ~7;
     const bool valid = n_p > 0 && n_p <= p.max_keys;     // more keys than max_keys: NaN, as the other kernels
+    float * const scp = STORED ? sc + ((size_t) blockIdx.x * ATT_P + sp) * (size_t) p.max_keys : nullptr;
     float qv[64];
     {
         const int t = t0 + sp / rep, h = g * rep + sp % rep;
@@ -1273,6 +1280,7 @@ __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
                 const float s = score_d64(qv, tile + (sk + 16 * r) * ATT_KS, jr < ng_p) * scale;
                 mx = fmaxf(mx, s);
                 if (jr == 0) s0_s[sp] = s;
+                if constexpr (STORED) scp[jr] = s;
             }
         }
 #pragma unroll
@@ -1284,7 +1292,45 @@ __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
     const float m = m_s[sp];
 
     // pass 2: the ordered sum of the exponentials
-    {
+    if constexpr (STORED) {
+        float ls = 0.0f;
+        const int ng = valid ? ng_p : 0;                   // the same for the 16 lanes of a pair
+        constexpr int U = 8;                               // 16-key steps per batch of loads
+        float cur[U], nxt[U];
+        auto load = [&](float (&dst)[U], int b) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int jr = b + 16 * u + sk;
+                dst[u] = jr < ng ? scp[jr] : 0.0f;
+            }
+        };
+        if (ng > 0) load(cur, 0);
+        for (int b = 0; b < ng; b += 16 * U) {
+            if (b + 16 * U < ng) load(nxt, b + 16 * U);    // the next batch in flight meanwhile
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (b + 16 * u >= ng) break;               // uniform over the pair's 16 lanes
+                const int jr = b + 16 * u + sk;
+                const float e = jr < ng ? exp_cephes(cur[u] - m) : 0.0f;
+                const float e8 = __shfl_down(e, 8, 16);    // key jr + 8, from lane sk + 8
+                if (sk < 8) {
+                    ls = ls + e;
+                    if (jr + 8 < ng) ls = ls + e8;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) cur[u] = nxt[u];
+        }
+        ls = ls + __shfl_xor(ls, 4);                       // lanes 8..15 hold 0 and stay among themselves
+        ls = ls + __shfl_xor(ls, 2);
+        ls = ls + __shfl_xor(ls, 1);
+        if (valid && sk == 0) {
+            float sum = ls;
+            for (int jr = ng_p; jr < n_p; ++jr) sum = sum + expf_libm(scp[jr] - m);
+            inv_s[sp] = 1.0f / sum;
+        }
+        __syncthreads();
+    } else {
         float ls = 0.0f;
         if (kl < kh) fetch(kg, kl);
         for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
@@ -1335,23 +1381,49 @@ __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
         vn[i] = __builtin_amdgcn_readfirstlane(n <= p.max_keys ? n : 0);
         acc[i] = 0.0f;
     }
-    if (kl < kh) fetch(kg, kl);
+    float snx[2] = { 0.0f, 0.0f };                          // STORED: the next tile's scores of this thread
+    auto sfetch = [&](int j0) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int jr = j0 + sk + 16 * r - plo;
+            snx[r] = valid && jr >= 0 && jr < n_p ? scp[jr] : 0.0f;
+        }
+    };
+    if (kl < kh) {
+        fetch(STORED ? vg : kg, kl);
+        if constexpr (STORED) sfetch(kl);
+    }
     for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
         __syncthreads();                                   // E and the tile are free
         stage();
-        __syncthreads();
-        fetch(vg, j0);                                     // this tile's values, staged after the weights
+        if constexpr (STORED) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int kt = sk + 16 * r, jr = j0 + kt - plo;
-            if (!valid || jr < 0 || jr >= n_p) continue;
-            const float s = score_d64(qv, tile + kt * ATT_KS, jr < ng_p) * scale;
-            E[sp][kt] = (jr < ng_p ? exp_cephes(s - m) : expf_libm(s - m)) * inv;
+            for (int r = 0; r < 2; ++r) {
+                const int kt = sk + 16 * r, jr = j0 + kt - plo;
+                if (!valid || jr < 0 || jr >= n_p) continue;
+                const float s = snx[r];
+                E[sp][kt] = (jr < ng_p ? exp_cephes(s - m) : expf_libm(s - m)) * inv;
+            }
+            __syncthreads();                               // the values and the weights are in LDS
+            if (j0 + ATT_KT < kh) {
+                fetch(vg, j0 + ATT_KT);
+                sfetch(j0 + ATT_KT);
+            }
+        } else {
+            __syncthreads();
+            fetch(vg, j0);                                 // this tile's values, staged after the weights
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int kt = sk + 16 * r, jr = j0 + kt - plo;
+                if (!valid || jr < 0 || jr >= n_p) continue;
+                const float s = score_d64(qv, tile + kt * ATT_KS, jr < ng_p) * scale;
+                E[sp][kt] = (jr < ng_p ? exp_cephes(s - m) : expf_libm(s - m)) * inv;
+            }
+            __syncthreads();                               // the keys have been read
+            stage();
+            __syncthreads();
+            if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
         }
-        __syncthreads();                                   // the keys have been read
-        stage();
-        __syncthreads();
-        if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
         const int jn = min(ATT_KT, kh - j0);
         // pair i's weights of the tile: lane l holds key j0 + l (l < 32), broadcast per key
         int a[4], b[4];
@@ -1389,6 +1461,21 @@ __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
         if (t >= p.T) continue;
         const int n = hi_s[pp] - lo_s[pp];
         p.out[(size_t) t * p.H * 64 + (size_t) h * 64 + d] = (n > 0 && n <= p.max_keys) ? acc[i] : __uint_as_float(0x7fc00000u);
+    }
+}
+
+__global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
+    attention_long_tile<false>(p, nullptr, (int) blockIdx.x);
+}
+
+// The scores kept in the workspace: a persistent grid, one slot of sc per workgroup, which
+// takes tiles blockIdx.x, blockIdx.x + gridDim.x, ...
+__global__ __launch_bounds__(256) void attention_stored_kernel(attn_params p, float * __restrict__ sc) {
+    const int nq = ATT_P / (p.H / p.G);
+    const int n_tiles = p.G * ((p.T + nq - 1) / nq);
+    for (int bt = (int) blockIdx.x; bt < n_tiles; bt += (int) gridDim.x) {
+        __syncthreads();                                   // the previous tile's shared reads are done
+        attention_long_tile<true>(p, sc, bt);
     }
 }
 
@@ -3044,13 +3131,76 @@ int32_t nxg_block_mean_quantize_rows(const float * h, const float * g, const int
                           n_blocks, n_in, act_max, q, sx, stream);
 }
 
+// Resident workgroups of attention_stored_kernel on the device (its persistent grid and
+// the workspace slots), queried once.
+static long long attention_long_slots() {
+    static long long slots = 0;
+    static bool done = false;
+    if (!done) {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attention_stored_kernel, 256, 0) == hipSuccess &&
+            cus > 0 && per_cu > 0) {
+            slots = (long long) cus * per_cu;
+        } else {
+            (void) hipGetLastError();
+            slots = 256;
+        }
+        done = true;
+    }
+    return slots;
+}
+
+// The launch nxg_attention_ws makes for (T, heads, max_keys): 0 tile kernel, 1 long kernel,
+// 2 row kernel; for the long kernel, its tiles and the workspace bytes of one slot.
+struct attn_plan {
+    int kind;
+    long long n_tiles;
+    long long slot_bytes;
+};
+
+static attn_plan plan_attention(int32_t T, int32_t n_head, int32_t n_kv_head, int32_t max_keys) {
+    const int rep = n_head / n_kv_head;
+    if (ATT_P % rep != 0) return {2, 0, 0};
+    const long long n_tiles = (long long) n_kv_head * ((T + ATT_P / rep - 1) / (ATT_P / rep));
+    const int smax = (max_keys + 3) & ~3;
+    const size_t tile_lds = ((size_t) ATT_P * smax + (size_t) ATT_KT * ATT_KS) * sizeof(float);
+    if (tile_lds <= attention_tile_lds_limit()) return {0, n_tiles, 0};
+    return {1, n_tiles, (long long) ATT_P * max_keys * (long long) sizeof(float)};
+}
+
+int64_t nxg_attention_workspace_bytes(int32_t T, int32_t n_head, int32_t n_kv_head, int32_t max_keys) {
+    if (T < 0 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head != 0 || max_keys < 1) {
+        return fail(NXG_EINVAL, "attention_workspace_bytes: T=%d n_head=%d n_kv_head=%d max_keys=%d", T, n_head,
+                    n_kv_head, max_keys);
+    }
+    if (T == 0) return 0;
+    int rc = check_device();
+    if (rc) return rc;
+    const attn_plan pl = plan_attention(T, n_head, n_kv_head, max_keys);
+    if (pl.kind != 1) return 0;
+    return std::min(pl.n_tiles, attention_long_slots()) * pl.slot_bytes;
+}
+
 int32_t nxg_attention(const float * q, const float * k, const float * v, const int32_t * cu_offsets,
                       int32_t n_seqs, const float * scale, int32_t T, int32_t n_head, int32_t n_kv_head,
                       int32_t half, int32_t max_keys, float * out, void * stream) {
+    return nxg_attention_ws(q, k, v, cu_offsets, n_seqs, scale, T, n_head, n_kv_head, half, max_keys, out, nullptr,
+                            0, stream);
+}
+
+int32_t nxg_attention_ws(const float * q, const float * k, const float * v, const int32_t * cu_offsets,
+                         int32_t n_seqs, const float * scale, int32_t T, int32_t n_head, int32_t n_kv_head,
+                         int32_t half, int32_t max_keys, float * out, void * workspace, int64_t workspace_bytes,
+                         void * stream) {
     if (T < 0 || n_seqs < 1 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head != 0) {
         return fail(NXG_EINVAL, "attention: T=%d n_seqs=%d n_head=%d n_kv_head=%d", T, n_seqs, n_head, n_kv_head);
     }
     if (max_keys < 1) return fail(NXG_EINVAL, "attention: max_keys=%d (must be >= 1)", max_keys);
+    if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace) || ((uintptr_t) workspace & 3)) {
+        return fail(NXG_EINVAL, "attention: workspace %p of %lld bytes", workspace, (long long) workspace_bytes);
+    }
     if (T == 0) return NXG_OK;
     if (!q || !k || !v || !cu_offsets || !scale || !out) return fail(NXG_EINVAL, "attention: null buffer");
     const long long n_wg = (long long) T * n_head;
@@ -3073,6 +3223,13 @@ int32_t nxg_attention(const float * q, const float * k, const float * v, const i
                 attention_tile_kernel<false><<<dim3((unsigned) n_tiles), dim3(256), tile_lds, (hipStream_t) stream>>>(p, smax);
             }
             return launch_check("attention_tile_kernel");
+        }
+        // scores written once into the workspace: as many slots as it holds, up to the resident workgroups
+        const attn_plan pl = plan_attention(T, n_head, n_kv_head, max_keys);
+        const long long n_slots = std::min({n_tiles, attention_long_slots(), (long long) (workspace_bytes / pl.slot_bytes)});
+        if (n_slots >= 1) {
+            attention_stored_kernel<<<dim3((unsigned) n_slots), dim3(256), 0, (hipStream_t) stream>>>(p, (float *) workspace);
+            return launch_check("attention_stored_kernel");
         }
         attention_long_kernel<<<dim3((unsigned) n_tiles), dim3(256), 0, (hipStream_t) stream>>>(p);
         return launch_check("attention_long_kernel");

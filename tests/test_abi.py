@@ -80,6 +80,14 @@ def test_arguments_checked_before_device_work(nxg):
     # RMSNorm's vector loads: x and gain must be 16-byte aligned (no pointer is dereferenced)
     assert L.nxg_rmsnorm_quantize_rows(4, 16, ctypes.c_float(1e-6), 16, 256, 127, 16, 16, None) == nxg.NXG_EINVAL
     assert b"aligned" in L.nxg_last_error()
+    # attention's workspace: a size without memory, a negative size or a misaligned one is refused
+    args = (None, None, None, None, 1, None, 8, 2, 1, -1, 8, None)
+    assert L.nxg_attention_ws(*args, None, 64, None) == nxg.NXG_EINVAL
+    assert L.nxg_attention_ws(*args, 16, -1, None) == nxg.NXG_EINVAL
+    assert L.nxg_attention_ws(*args, 18, 64, None) == nxg.NXG_EINVAL
+    assert b"workspace" in L.nxg_last_error()
+    assert L.nxg_attention_workspace_bytes(8, 3, 2, 8) == nxg.NXG_EINVAL
+    assert L.nxg_attention_workspace_bytes(0, 2, 1, 8) == 0
 
 
 def test_device_calls_fail_loudly_without_gpu(nxg):

@@ -33,9 +33,9 @@ def dev(torch, nxg):
     return torch.device("cuda:0")
 
 
-def run(nxg, torch, q, k, v, cu, scale, H, G, half):
+def run(nxg, torch, q, k, v, cu, scale, H, G, half, workspace=None):
     c = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
-    return nxg.attention(c(q), c(k), c(v), cu, scale, H, G, half).cpu().numpy()
+    return nxg.attention(c(q), c(k), c(v), cu, scale, H, G, half, workspace=workspace).cpu().numpy()
 
 
 CASES = [
@@ -88,6 +88,46 @@ def test_attention_long_documents(nxg, orc, torch, dev, lengths, half):
     scale = rng.uniform(0.05, 0.2, len(lengths)).astype(np.float32)
     y = run(nxg, torch, q, k, v, cu, scale, H, G, half)
     assert (bits(y) == bits(orc.attention(q, k, v, cu, scale, H, G, half))).all()
+
+
+@pytest.mark.parametrize("lengths,half,H,G", [([4000], 1500, 2, 1), ([3000, 5, 700], -1, 2, 1),
+                                              ([2600, 1, 9], -1, 4, 2), ([2500], 1300, 1, 1)])
+def test_attention_stored_scores(nxg, orc, torch, dev, lengths, half, H, G):
+    """nxg_attention_ws past the tile kernel's LDS: the scores written once to the workspace and
+    read back by the softmax and the values give the oracle's bits, with a slot for every
+    resident workgroup and with 3 slots (each workgroup then takes many tiles in turn)."""
+    say(f"attention stored scores lengths={lengths} half={half} H={H} G={G}")
+    rng = np.random.default_rng(len(lengths) + 11 * H + half)
+    cu = nxg.cu_offsets_of(lengths)
+    T = int(cu[-1])
+    q = rng.standard_normal((T, H * 64)).astype(np.float32)
+    k, v = (rng.standard_normal((G, T, 64)).astype(np.float32) for _ in range(2))
+    scale = rng.uniform(0.05, 0.2, len(lengths)).astype(np.float32)
+    ref = orc.attention(q, k, v, cu, scale, H, G, half)
+    lens = np.diff(cu)
+    max_keys = int(lens.max()) if half < 0 else int(min(lens.max(), 2 * half + 1))
+    full = nxg.attention_workspace_bytes(T, H, G, max_keys)
+    slot = 16 * max_keys * 4
+    assert full >= slot and full % slot == 0
+    for ws in ("auto", torch.empty(3 * slot + 100, dtype=torch.uint8, device="cuda")):
+        y = run(nxg, torch, q, k, v, cu, scale, H, G, half, workspace=ws)
+        assert (bits(y) == bits(ref)).all()
+
+
+def test_attention_workspace_ignored_when_scores_fit(nxg, orc, torch, dev):
+    """Short documents keep their scores in LDS: no workspace is asked for, and one given is unused."""
+    say("attention workspace with short documents")
+    assert nxg.attention_workspace_bytes(1024, 16, 8, 1024) == 0
+    rng = np.random.default_rng(12)
+    H, G = 4, 2
+    cu = nxg.cu_offsets_of([100, 30])
+    T = int(cu[-1])
+    q = rng.standard_normal((T, H * 64)).astype(np.float32)
+    k, v = (rng.standard_normal((G, T, 64)).astype(np.float32) for _ in range(2))
+    scale = np.array([0.1, 0.2], np.float32)
+    ws = torch.empty(4096, dtype=torch.uint8, device="cuda")
+    y = run(nxg, torch, q, k, v, cu, scale, H, G, -1, workspace=ws)
+    assert (bits(y) == bits(orc.attention(q, k, v, cu, scale, H, G))).all()
 
 
 def test_attention_head_ratio_3(nxg, orc, torch, dev):

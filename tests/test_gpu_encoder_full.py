@@ -89,6 +89,19 @@ def test_encoder_matches_oracle(nxg, enc, torch, small_models, key, lengths):
                 assert (bits(p) == bits(pr)).all(), f"pooled differs: normalize={normalize}"
 
 
+def test_encoder_long_document_matches_oracle(nxg, enc, torch, small_models):
+    """One 2,700-token document: its full-attention layer has more keys per query than the tile
+    kernel's LDS holds, so the encoder's attention keeps the scores in its workspace."""
+    path, d, m = small_models["c128_q4km"]
+    say("encoder c128_q4km one 2,700-token document")
+    tok = np.random.default_rng(27).integers(0, d.n_vocab, 2700).astype(np.int32)
+    with nxg.Encoder(path) as e:
+        h, p = e.encode(tok, [2700], pooled=True)
+    hr, pr = enc.encode(m, tok, [2700])
+    assert (bits(h) == bits(hr)).all()
+    assert (bits(p) == bits(pr)).all()
+
+
 def test_encoder_batch_invariance_and_layers(nxg, enc, torch, small_models):
     path, d, m = small_models["c256_q8"]
     say("encoder batch invariance, set_layers, device entry point")
