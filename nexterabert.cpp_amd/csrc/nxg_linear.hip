@@ -1295,7 +1295,7 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
     if constexpr (STORED) {
         float ls = 0.0f;
         const int ng = valid ? ng_p : 0;                   // the same for the 16 lanes of a pair
-        constexpr int U = 8;                               // 16-key steps per batch of loads
+        constexpr int U = 16;                              // 16-key steps per batch of loads
         float cur[U], nxt[U];
         auto load = [&](float (&dst)[U], int b) {
 #pragma unroll
