@@ -90,6 +90,33 @@ NXG_API int32_t nxg_encoder_forward(nxg_encoder * e, const int32_t * tokens, con
 /* nextera_last_ms (nexterabert.h:121-122): wall time of the last nxg_encoder_encode, in ms. */
 NXG_API double nxg_encoder_last_ms(const nxg_encoder * e);
 
+/* The number of int8 linears the file's encoder has (before projections sharing an input are
+ * fused): the count nextera_load reports in its system info (src/nexterabert.cpp:1735-1752). */
+NXG_API int32_t nxg_encoder_n_int8(const nxg_encoder * e);
+
+/* Kinds of launch the profiler tells apart, the reference's prof_kind (src/nexterabert.cpp:
+ * 262-266): int8 linears (every GEMM, the MLP's fused c_fc -> relu^2 -> int8 included),
+ * attention, the row ops (norms, convolutions, gates, DyT/RoPE, block means, quantizations,
+ * pooling); OTHER is what the reference leaves to ggml (embedding rows, out_norm, copies). */
+#define NXG_PROF_LINEAR 0
+#define NXG_PROF_ATTN   1
+#define NXG_PROF_ROWS   2
+#define NXG_PROF_OTHER  3
+#define NXG_PROF_COUNT  4
+
+/* nextera_debug_profile (src/nexterabert.cpp:1823-1826): clears the profile and turns it on or
+ * off. While it is on, every forward pass records a HIP event after each launch on its stream
+ * and adds the device time of each launch to its kind; nxg_encoder_forward then waits for its
+ * pass to end (so a profiled pass cannot be captured into a graph: NXG_EINVAL). */
+NXG_API void nxg_encoder_profile(nxg_encoder * e, int32_t enable);
+
+/* The profile so far: kind_ms [NXG_PROF_COUNT] device ms per kind, summed over the passes;
+ * device_ms their total; wall_ms the host wall time of the nxg_encoder_encode calls (the
+ * device time for nxg_encoder_forward passes); passes the number of profiled passes. Any
+ * output may be NULL. */
+NXG_API int32_t nxg_encoder_profile_read(const nxg_encoder * e, double * kind_ms, double * device_ms,
+                                         double * wall_ms, int64_t * passes);
+
 #ifdef __cplusplus
 }
 #endif

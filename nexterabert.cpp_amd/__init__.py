@@ -241,6 +241,24 @@ def _stream_ptr(stream=None) -> Optional[int]:
     return s.cuda_stream or None
 
 
+def _order_on(stream, *tensors) -> None:
+    """Before a launch on `stream` that reads or writes tensors allocated here, on torch's
+    current stream: the launch waits for the current stream's work (host-to-device copies
+    of offsets and scales), and the caching allocator may not hand those tensors' memory to
+    anything else before `stream` has finished with them. A no-op when `stream` is the
+    current stream (or None)."""
+    if stream is None:
+        return
+    torch = _torch()
+    cur = torch.cuda.current_stream()
+    if stream.cuda_stream == cur.cuda_stream:
+        return
+    stream.wait_stream(cur)
+    for t in tensors:
+        if t is not None:
+            t.record_stream(stream)
+
+
 def init() -> None:
     """Checks that the current device is a gfx950 GPU (raises otherwise)."""
     _check(load_library().nxg_init(), "init")
@@ -307,6 +325,7 @@ def _quantize(fn_name: str, x, act_max: int, out: Optional[QAct], stream) -> QAc
     qa = out if out is not None else qact_alloc(T, n_in, act_max, x.device)
     qa.T, qa.n_in, qa.act_max = T, n_in, act_max
     fn = getattr(load_library(), fn_name)
+    _order_on(stream, qa.q, qa.sx)
     _check(fn(x.data_ptr(), T, n_in, act_max, qa.q.data_ptr(), qa.sx.data_ptr(), _stream_ptr(stream)), fn_name)
     return qa
 
@@ -332,6 +351,7 @@ def rmsnorm_quantize_rows(x, gain, eps: float, act_max: int = 127, out: Optional
         raise ValueError(f"gain must be a contiguous float32 device tensor of shape ({n_in},)")
     qa = out if out is not None else qact_alloc(T, n_in, act_max, x.device)
     qa.T, qa.n_in, qa.act_max = T, n_in, act_max
+    _order_on(stream, qa.q, qa.sx)
     _check(load_library().nxg_rmsnorm_quantize_rows(x.data_ptr(), gain.data_ptr(), float(eps), T, n_in, act_max,
                                                      qa.q.data_ptr(), qa.sx.data_ptr(), _stream_ptr(stream)),
            "rmsnorm_quantize_rows")
@@ -372,6 +392,7 @@ def gate_quantize_rows(g, y, act_max: int = 127, out: Optional[QAct] = None, str
     T, n_in = g.shape
     _rows_arg(y, "y", (T, n_in))
     qa = _produce_out(T, n_in, act_max, out, g.device)
+    _order_on(stream, qa.q, qa.sx)
     _check(load_library().nxg_gate_quantize_rows(g.data_ptr(), y.data_ptr(), T, n_in, act_max, qa.q.data_ptr(),
                                                  qa.sx.data_ptr(), _stream_ptr(stream)), "gate_quantize_rows")
     return qa
@@ -390,6 +411,7 @@ def dwconv_quantize_rows(x, taps, cu_offsets, r=None, act_max: int = 127, out: O
         _rows_arg(r, "r", (T, n_in))
     cu = _device_offsets(cu_offsets, x.device)
     qa = _produce_out(T, n_in, act_max, out, x.device)
+    _order_on(stream, cu, qa.q, qa.sx)
     _check(load_library().nxg_dwconv_quantize_rows(x.data_ptr(), r.data_ptr() if r is not None else None,
                                                    taps.data_ptr(), taps.shape[0], cu.data_ptr(), cu.numel() - 1,
                                                    T, n_in, act_max, qa.q.data_ptr(), qa.sx.data_ptr(),
@@ -410,6 +432,7 @@ def lily_state_quantize_rows(a, x, b, taps, cu_offsets, act_max: int = 127, out:
         raise ValueError(f"taps must be [k][{n_in}]")
     cu = _device_offsets(cu_offsets, x.device)
     qa = _produce_out(T, n_in, act_max, out, x.device)
+    _order_on(stream, cu, qa.q, qa.sx)
     _check(load_library().nxg_lily_state_quantize_rows(a.data_ptr(), x.data_ptr(), b.data_ptr(), taps.data_ptr(),
                                                        taps.shape[0], cu.data_ptr(), cu.numel() - 1, T, n_in,
                                                        act_max, qa.q.data_ptr(), qa.sx.data_ptr(),
@@ -438,6 +461,7 @@ def block_mean_quantize_rows(h, cu_offsets: Sequence[int], block: int, g=None, a
     n_blocks = int(cub_host[-1])
     cu, cub = _device_offsets(cu_host, h.device), _device_offsets(cub_host, h.device)
     qa = _produce_out(n_blocks, n_in, act_max, out, h.device)
+    _order_on(stream, cu, cub, qa.q, qa.sx)
     _check(load_library().nxg_block_mean_quantize_rows(h.data_ptr(), g.data_ptr() if g is not None else None,
                                                        cu.data_ptr(), cub.data_ptr(), cu.numel() - 1, T, n_blocks,
                                                        block, n_in, act_max, qa.q.data_ptr(), qa.sx.data_ptr(),
@@ -494,6 +518,7 @@ def attention(q, k, v, cu_offsets: Sequence[int], scale, n_head: int, n_kv_head:
     if out is None:
         out = torch.empty_like(q)
     if workspace is None:
+        _order_on(stream, cu, sc, out)
         _check(load_library().nxg_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), cu.data_ptr(), cu.numel() - 1,
                                             sc.data_ptr(), T, n_head, n_kv_head, half, max(1, max_keys),
                                             out.data_ptr(), _stream_ptr(stream)), "attention")
@@ -505,6 +530,7 @@ def attention(q, k, v, cu_offsets: Sequence[int], scale, n_head: int, n_kv_head:
                                 dtype=torch.uint8, device=q.device)
     if workspace.dtype != torch.uint8 or not workspace.is_cuda or not workspace.is_contiguous():
         raise ValueError("workspace must be a contiguous uint8 device tensor")
+    _order_on(stream, cu, sc, out, workspace)
     _check(load_library().nxg_attention_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), cu.data_ptr(), cu.numel() - 1,
                                            sc.data_ptr(), T, n_head, n_kv_head, half, max(1, max_keys),
                                            out.data_ptr(), workspace.data_ptr() if workspace.numel() else None,
@@ -541,6 +567,7 @@ def qk_prep(x, alpha, beta, cos_t, sin_t, cu_offsets: Sequence[int], n_head: int
     cu = _device_offsets(cu_offsets, x.device)
     if out is None:
         out = torch.empty((n_head, T, D) if head_major else (T, width), dtype=torch.float32, device=x.device)
+    _order_on(stream, cu, out)
     _check(load_library().nxg_qk_prep(x.data_ptr(), alpha.data_ptr(), beta.data_ptr(), cos_t.data_ptr(),
                                       sin_t.data_ptr(), cos_t.shape[0], cu.data_ptr(), cu.numel() - 1, T, n_head, D,
                                       1 if head_major else 0, out.data_ptr(), _stream_ptr(stream)), "qk_prep")
@@ -555,6 +582,7 @@ def head_major(x, n_head: int, out=None, stream=None):
     D = width // n_head
     if out is None:
         out = torch.empty((n_head, T, D), dtype=torch.float32, device=x.device)
+    _order_on(stream, out)
     _check(load_library().nxg_head_major(x.data_ptr(), T, n_head, D, out.data_ptr(), _stream_ptr(stream)), "head_major")
     return out
 
@@ -582,6 +610,7 @@ def qkv_prep(q, k, v, q_alpha, q_beta, k_alpha, k_beta, cos_t, sin_t, cu_offsets
     qo = torch.empty((T, width), dtype=torch.float32, device=q.device)
     ko = torch.empty((n_kv_head, T, D), dtype=torch.float32, device=q.device)
     vo = torch.empty((n_kv_head, T, D), dtype=torch.float32, device=q.device)
+    _order_on(stream, cu, qo, ko, vo)
     _check(load_library().nxg_qkv_prep(q.data_ptr(), k.data_ptr(), v.data_ptr(), q_alpha.data_ptr(), q_beta.data_ptr(),
                                        k_alpha.data_ptr(), k_beta.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(),
                                        cos_t.shape[0], cu.data_ptr(), cu.numel() - 1, T, n_head, n_kv_head, D,
@@ -603,6 +632,7 @@ def dwconv_rows(x, taps, cu_offsets, r=None, out=None, stream=None):
     cu = _device_offsets(cu_offsets, x.device)
     if out is None:
         out = torch.empty_like(x)
+    _order_on(stream, cu, out)
     _check(load_library().nxg_dwconv_rows(x.data_ptr(), r.data_ptr() if r is not None else None, taps.data_ptr(),
                                           taps.shape[0], cu.data_ptr(), cu.numel() - 1, T, C, out.data_ptr(),
                                           _stream_ptr(stream)), "dwconv_rows")
@@ -623,6 +653,7 @@ def upsample_add(yb, r, cu_offsets, block: int, out=None, stream=None):
     cu, cub = _device_offsets(cu_host, r.device), _device_offsets(cub_host, r.device)
     if out is None:
         out = torch.empty_like(r)
+    _order_on(stream, cu, cub, out)
     _check(load_library().nxg_upsample_add(yb.data_ptr(), r.data_ptr(), cu.data_ptr(), cub.data_ptr(), cu.numel() - 1,
                                            T, yb.shape[0], block, C, out.data_ptr(), _stream_ptr(stream)),
            "upsample_add")
@@ -646,6 +677,7 @@ def embed_rows(table, ids, type_table=None, types=None, out=None, stream=None):
             raise ValueError("type_table must be [n_types][C] with int32 types [T]")
     if out is None:
         out = torch.empty((T, C), dtype=torch.float32, device=table.device)
+    _order_on(stream, out)
     _check(load_library().nxg_embed_rows(table.data_ptr(), n_vocab, ids.data_ptr(),
                                          type_table.data_ptr() if type_table is not None else None, n_types,
                                          types.data_ptr() if type_table is not None else None, T, C, out.data_ptr(),
@@ -663,6 +695,7 @@ def layer_norm(x, w=None, b=None, eps: float = 1e-5, out=None, stream=None):
             raise ValueError(f"{name} must be a contiguous float32 device tensor [{C}]")
     if out is None:
         out = torch.empty_like(x)
+    _order_on(stream, out)
     _check(load_library().nxg_layer_norm(x.data_ptr(), w.data_ptr() if w is not None else None,
                                          b.data_ptr() if b is not None else None, eps, T, C, out.data_ptr(),
                                          _stream_ptr(stream)), "layer_norm")
@@ -679,6 +712,7 @@ def doc_mean(x, cu_offsets, normalize: bool = False, out=None, stream=None):
     n = cu.numel() - 1
     if out is None:
         out = torch.empty((n, C), dtype=torch.float32, device=x.device)
+    _order_on(stream, cu, out)
     _check(load_library().nxg_doc_mean(x.data_ptr(), cu.data_ptr(), n, T, C, 1 if normalize else 0, out.data_ptr(),
                                        _stream_ptr(stream)), "doc_mean")
     return out
@@ -690,6 +724,7 @@ def export_qact(qa: QAct, stream=None):
     nb = (qa.n_in + BLOCK - 1) // BLOCK
     u8 = torch.empty((qa.T, qa.n_in), dtype=torch.uint8, device=qa.q.device)
     sx = torch.empty(((qa.T + 3) // 4) * nb * 4, dtype=torch.float32, device=qa.q.device)
+    _order_on(stream, u8, sx)
     _check(load_library().nxg_qact_export(qa.q.data_ptr(), qa.sx.data_ptr(), qa.T, qa.n_in, qa.act_max,
                                           u8.data_ptr(), sx.data_ptr(), _stream_ptr(stream)), "qact_export")
     return u8, sx
@@ -720,9 +755,11 @@ def linear_i8(weight: DeviceWeight, qa: QAct, residual=None, cu_offsets: Optiona
         cu = np.ascontiguousarray(cu_offsets, dtype=np.int32)
         if cu.size < 2 or int(cu[-1]) != T:
             raise ValueError(f"cu_offsets must end at T={T}")
+        _order_on(stream, out)
         rc = L.nxg_linear_i8(weight.handle, qa.q.data_ptr(), qa.sx.data_ptr(), _np_ptr(cu), cu.size - 1,
                              res_ptr, out.data_ptr(), _stream_ptr(stream))
     else:
+        _order_on(stream, out)
         rc = L.nxg_linear_i8_rows(weight.handle, qa.q.data_ptr(), qa.sx.data_ptr(), T, res_ptr,
                                   out.data_ptr(), _stream_ptr(stream))
     _check(rc, "linear_i8")
@@ -746,6 +783,7 @@ def linear_i8_split(weight: DeviceWeight, qa: QAct, cols: Sequence[int], outs=No
         _check_rows(o, T, c, "out")
     cols_a = np.ascontiguousarray(cols, dtype=np.int32)
     ptrs = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    _order_on(stream, *outs)
     _check(load_library().nxg_linear_i8_rows_split(weight.handle, qa.q.data_ptr(), qa.sx.data_ptr(), T, len(cols),
                                                    _np_ptr(cols_a), ctypes.cast(ptrs, ctypes.c_void_p),
                                                    _stream_ptr(stream)), "linear_i8_split")
@@ -767,9 +805,11 @@ def linear_i8_relu2_q8(weight: DeviceWeight, qa: QAct, act_max: int = 127,
         cu = np.ascontiguousarray(cu_offsets, dtype=np.int32)
         if cu.size < 2 or int(cu[-1]) != T:
             raise ValueError(f"cu_offsets must end at T={T}")
+        _order_on(stream, res.q, res.sx)
         rc = L.nxg_linear_i8_relu2_q8(weight.handle, qa.q.data_ptr(), qa.sx.data_ptr(), _np_ptr(cu), cu.size - 1,
                                       act_max, res.q.data_ptr(), res.sx.data_ptr(), _stream_ptr(stream))
     else:
+        _order_on(stream, res.q, res.sx)
         rc = L.nxg_linear_i8_relu2_q8_rows(weight.handle, qa.q.data_ptr(), qa.sx.data_ptr(), T, act_max,
                                            res.q.data_ptr(), res.sx.data_ptr(), _stream_ptr(stream))
     _check(rc, "linear_i8_relu2_q8")
@@ -780,6 +820,7 @@ def block_sums(weight: DeviceWeight, qa: QAct, stream=None):
     """int32 [n_blk][T][n_out]: the exact per-block sums of the GEMM."""
     torch = _torch()
     s = torch.empty((weight.n_blk, qa.T, weight.n_out), dtype=torch.int32, device=qa.q.device)
+    _order_on(stream, s)
     _check(load_library().nxg_linear_i8_block_sums(weight.handle, qa.q.data_ptr(), qa.T, s.data_ptr(),
                                                    _stream_ptr(stream)), "block_sums")
     return s

@@ -27,6 +27,9 @@ CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 OBJ = PKG / "_build"
 LIB = PKG / "libnxg.so"
+# the reference's public C API (include/nexterabert.h) over libnxg.so, under the library name the
+# reference's binding and CLI link against
+API_LIB = PKG / "libnexterabert.so"
 CLI = PKG / "nxg-cli"
 ARCH = "gfx950"
 
@@ -94,6 +97,12 @@ def build(verbose: bool = False) -> Path:
     _run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread",
           OBJ / "nxg_linear.o", OBJ / "nxg_host.o", OBJ / "nxg_gguf.o", OBJ / "nxg_encoder.o", "-o", tmp], verbose)
     os.replace(tmp, LIB)
+    tmp = API_LIB.with_suffix(".so.tmp")
+    _run(["g++", "-O2", "-fPIC", "-std=c++17", "-Wall", "-fvisibility=hidden", "-DNEXTERA_SHARED", "-DNEXTERA_BUILD",
+          "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}", f"-I{rocm / 'include'}", "-shared", CSRC / "nexterabert_api.cpp",
+          "-o", tmp, f"-L{PKG}", "-lnxg", f"-L{rocm / 'lib'}", "-lamdhip64", "-Wl,-rpath,$ORIGIN",
+          f"-Wl,-rpath,{rocm / 'lib'}"], verbose)
+    os.replace(tmp, API_LIB)
     # the C++ driver over the C ABI (nxg-cli: --info, --bench), linked against libnxg.so
     _run(["g++", "-O2", "-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}", f"-I{rocm / 'include'}",
           CSRC / "nxg_cli.cpp", "-o", CLI, f"-L{PKG}", "-lnxg", f"-L{rocm / 'lib'}", "-lamdhip64",

@@ -54,6 +54,13 @@ int hip_fail(hipError_t e, const char * what) {
         if (e_ != hipSuccess) return hip_fail(e_, what);  \
     } while (0)
 
+// One launch of the forward pass, then the profiler's mark for its kind (nxg_encoder_profile).
+#define NXG_OP(kind, x)                     \
+    do {                                    \
+        NXG_TRY(x);                         \
+        NXG_TRY(mark(kind, s));             \
+    } while (0)
+
 // Frees device memory where no error can be reported (destructors, replaced buffers).
 void release(void * p) {
     if (p) (void) hipFree(p);
@@ -167,6 +174,20 @@ struct nxg_encoder {
     int32_t T = 0, TB = 0, max_len = 0, max_blocks = 0;
     rope_dev rope[2];                          // [0]: full attention and HRA, [1]: swa
     bool fuse_mlp = true;
+    int32_t n_int8 = 0;                        // int8 linears of the file's encoder, before fusing
+
+    // Device time per kind of launch (the reference's per-op-kind profiler, src/nexterabert.cpp:
+    // 262-283): an event after every launch of a pass, on the launching stream; the interval
+    // that ends at an event is the time of the launch before it (its dispatch gap included).
+    struct profiler {
+        bool enabled = false;
+        std::vector<hipEvent_t> ev;            // reused from pass to pass
+        std::vector<int> kind;                 // kind[i]: the launch ending at ev[i]; ev[0] opens the pass
+        size_t used = 0;
+        double ms[NXG_PROF_COUNT] = {};
+        double device_ms = 0.0, wall_ms = 0.0;
+        int64_t passes = 0;
+    } prof;
 
     ~nxg_encoder();
     const float * w(const std::string & name) const { return f32.at(name).dev; }
@@ -184,6 +205,9 @@ struct nxg_encoder {
                       hipStream_t s);
     int32_t gated_out(const std::string & pre, const float * y, const float * z, const float * x_in, float * x_out,
                       int32_t n_seqs, hipStream_t s);
+    int32_t mark(int kind, hipStream_t s);
+    // waits for the last pass's events and adds their intervals (wall_ms: the caller's clock, or < 0)
+    int32_t collect(double wall_ms);
 };
 
 nxg_encoder::~nxg_encoder() {
@@ -195,7 +219,38 @@ nxg_encoder::~nxg_encoder() {
         release(r.sin);
     }
     release(work);
+    for (hipEvent_t ev : prof.ev) (void) hipEventDestroy(ev);
     if (stream) (void) hipStreamDestroy(stream);
+}
+
+int32_t nxg_encoder::mark(int k, hipStream_t s) {
+    if (!prof.enabled) return NXG_OK;
+    if (prof.used == prof.ev.size()) {
+        hipEvent_t ev = nullptr;
+        NXG_HIP(hipEventCreate(&ev), "hipEventCreate(profile)");
+        prof.ev.push_back(ev);
+        prof.kind.push_back(0);
+    }
+    NXG_HIP(hipEventRecord(prof.ev[prof.used], s), "hipEventRecord(profile)");
+    prof.kind[prof.used++] = k;
+    return NXG_OK;
+}
+
+int32_t nxg_encoder::collect(double wall_ms) {
+    if (!prof.enabled || prof.used < 2) return NXG_OK;
+    NXG_HIP(hipEventSynchronize(prof.ev[prof.used - 1]), "hipEventSynchronize(profile)");
+    double pass = 0.0;
+    for (size_t i = 1; i < prof.used; ++i) {
+        float ms = 0.0f;
+        NXG_HIP(hipEventElapsedTime(&ms, prof.ev[i - 1], prof.ev[i]), "hipEventElapsedTime(profile)");
+        prof.ms[prof.kind[i]] += ms;
+        pass += ms;
+    }
+    prof.device_ms += pass;
+    prof.wall_ms += wall_ms >= 0.0 ? wall_ms : pass;
+    prof.passes += 1;
+    prof.used = 0;
+    return NXG_OK;
 }
 
 namespace {
@@ -418,13 +473,14 @@ int32_t nxg_encoder::attention(const std::string & pre, const qact & h, int32_t 
                                int32_t n_seqs, const rope_dev & r, int32_t half, const float * scale,
                                int32_t max_keys, float * out, hipStream_t s) {
     const int32_t H = hp.n_head, G = hp.n_kv_head, D = hp.head_dim;
-    NXG_TRY(project(pre + "qkv", { pre + "c_q.weight", pre + "c_k.weight", pre + "c_v.weight" }, h, rows,
+    NXG_OP(NXG_PROF_LINEAR, project(pre + "qkv", { pre + "c_q.weight", pre + "c_k.weight", pre + "c_v.weight" }, h, rows,
                     { F[0], K[0], K[2] }, s));
-    NXG_TRY(nxg_qkv_prep(F[0], K[0], K[2], w(pre + "q_norm.alpha"), w(pre + "q_norm.beta"), w(pre + "k_norm.alpha"),
+    NXG_OP(NXG_PROF_ROWS, nxg_qkv_prep(F[0], K[0], K[2], w(pre + "q_norm.alpha"), w(pre + "q_norm.beta"), w(pre + "k_norm.alpha"),
                          w(pre + "k_norm.beta"), r.cos, r.sin, r.n_pos, cu_dev, n_seqs, rows, H, G, D, F[1], K[1], K[3],
                          s));
-    return nxg_attention_ws(F[1], K[1], K[3], cu_dev, n_seqs, scale, rows, H, G, half, max_keys, out,
-                            attn_ws_bytes ? attn_ws : nullptr, attn_ws_bytes, s);
+    NXG_OP(NXG_PROF_ATTN, nxg_attention_ws(F[1], K[1], K[3], cu_dev, n_seqs, scale, rows, H, G, half, max_keys, out,
+                                           attn_ws_bytes ? attn_ws : nullptr, attn_ws_bytes, s));
+    return NXG_OK;
 }
 
 // builder::gated_out (:1206-1213): x + c_proj(sigmoid(c_gate(y)) * z), the gate quantized
@@ -433,10 +489,11 @@ int32_t nxg_encoder::gated_out(const std::string & pre, const float * y, const f
                                float * x_out, int32_t n_seqs, hipStream_t s) {
     (void) n_seqs;
     const int32_t C = hp.n_embd;
-    NXG_TRY(nxg_quantize_rows(y, T, C, act_max, qa_y.q, qa_y.sx, s));
-    NXG_TRY(linear(pre + "c_gate.weight", qa_y, T, nullptr, F[3], s));
-    NXG_TRY(nxg_gate_quantize_rows(F[3], z, T, C, act_max, qa_g.q, qa_g.sx, s));
-    return linear(pre + "c_proj.weight", qa_g, T, x_in, x_out, s);
+    NXG_OP(NXG_PROF_ROWS, nxg_quantize_rows(y, T, C, act_max, qa_y.q, qa_y.sx, s));
+    NXG_OP(NXG_PROF_LINEAR, linear(pre + "c_gate.weight", qa_y, T, nullptr, F[3], s));
+    NXG_OP(NXG_PROF_ROWS, nxg_gate_quantize_rows(F[3], z, T, C, act_max, qa_g.q, qa_g.sx, s));
+    NXG_OP(NXG_PROF_LINEAR, linear(pre + "c_proj.weight", qa_g, T, x_in, x_out, s));
+    return NXG_OK;
 }
 
 // builder::encoder (src/nexterabert.cpp:1270-1292) and run_forward's pooling (:1913-1925).
@@ -445,7 +502,9 @@ int32_t nxg_encoder::run(const int32_t * ids_dev, const int32_t * types_dev, int
     const int32_t C = hp.n_embd, R = hp.lily_rank, I = hp.n_inter;
     const f32_tensor & emb = f32.at("embedding.weight");
     const bool seg = hp.n_types > 0 && types_dev;
-    NXG_TRY(nxg_embed_rows(emb.dev, emb.rows, ids_dev, seg ? w("token_type_embeddings.weight") : nullptr,
+    prof.used = 0;
+    NXG_TRY(mark(NXG_PROF_OTHER, s));          // opens the pass
+    NXG_OP(NXG_PROF_OTHER, nxg_embed_rows(emb.dev, emb.rows, ids_dev, seg ? w("token_type_embeddings.weight") : nullptr,
                            hp.n_types, seg ? types_dev : nullptr, T, C, x[0], s));
     int cur = 0;
     const int32_t n_layer = n_layers_run >= 0 ? std::min(n_layers_run, hp.n_layer) : hp.n_layer;
@@ -455,7 +514,7 @@ int32_t nxg_encoder::run(const int32_t * ids_dev, const int32_t * types_dev, int
         float * xi = x[cur];
         float * xo = x[cur ^ 1];
         const float * scale = scales + (size_t) l * n_seqs;
-        NXG_TRY(nxg_rmsnorm_quantize_rows(xi, w(blk + "attn_norm.weight"), hp.rms_eps, T, C, act_max, qa_h.q, qa_h.sx, s));
+        NXG_OP(NXG_PROF_ROWS, nxg_rmsnorm_quantize_rows(xi, w(blk + "attn_norm.weight"), hp.rms_eps, T, C, act_max, qa_h.q, qa_h.sx, s));
         switch (hp.block_types[l]) {
             case MIX_SWA:
             case MIX_ATTN: {                   // mix_attn (:1215-1222)
@@ -467,30 +526,30 @@ int32_t nxg_encoder::run(const int32_t * ids_dev, const int32_t * types_dev, int
                 break;
             }
             case MIX_LILY: {                   // mix_lily (:1224-1244)
-                NXG_TRY(project(pre + "lily_in", { pre + "ltc_conv.in_proj.weight", pre + "ltc_conv.A.weight",
+                NXG_OP(NXG_PROF_LINEAR, project(pre + "lily_in", { pre + "ltc_conv.in_proj.weight", pre + "ltc_conv.A.weight",
                                                    pre + "x_proj.weight", pre + "B_proj.weight" },
                                 qa_h, T, { Z[0], Z[1], F[1], F[2] }, s));
                 const f32_tensor & ltc = f32.at(pre + "ltc_conv.kernel");
-                NXG_TRY(nxg_dwconv_quantize_rows(Z[0], Z[1], ltc.dev, ltc.rows, cu, n_seqs, T, R, act_max, qa_R.q,
+                NXG_OP(NXG_PROF_ROWS, nxg_dwconv_quantize_rows(Z[0], Z[1], ltc.dev, ltc.rows, cu, n_seqs, T, R, act_max, qa_R.q,
                                                  qa_R.sx, s));
-                NXG_TRY(linear(pre + "ltc_conv.out_proj.weight", qa_R, T, nullptr, F[0], s));
+                NXG_OP(NXG_PROF_LINEAR, linear(pre + "ltc_conv.out_proj.weight", qa_R, T, nullptr, F[0], s));
                 const f32_tensor & st = f32.at(pre + "state_conv.depthwise.weight");
-                NXG_TRY(nxg_lily_state_quantize_rows(F[0], F[1], F[2], st.dev, st.rows, cu, n_seqs, T, C, act_max,
+                NXG_OP(NXG_PROF_ROWS, nxg_lily_state_quantize_rows(F[0], F[1], F[2], st.dev, st.rows, cu, n_seqs, T, C, act_max,
                                                      qa_g.q, qa_g.sx, s));
-                NXG_TRY(linear(pre + "c_proj.weight", qa_g, T, xi, xo, s));
+                NXG_OP(NXG_PROF_LINEAR, linear(pre + "c_proj.weight", qa_g, T, xi, xo, s));
                 break;
             }
             case MIX_HRA: {                    // mix_hra (:1246-1268)
-                NXG_TRY(project(pre + "hra_in", { pre + "qkv_in.weight", pre + "qkv_gate.weight", pre + "c_C.weight" },
+                NXG_OP(NXG_PROF_LINEAR, project(pre + "hra_in", { pre + "qkv_in.weight", pre + "qkv_gate.weight", pre + "c_C.weight" },
                                 qa_h, T, { F[4], F[6], F[7] }, s));
                 const f32_tensor & qc = f32.at(pre + "qkv_conv.depthwise.weight");
-                NXG_TRY(nxg_dwconv_rows(F[4], nullptr, qc.dev, qc.rows, cu, n_seqs, T, C, F[5], s));
-                NXG_TRY(nxg_block_mean_quantize_rows(F[5], F[6], cu, cub, n_seqs, T, TB, hp.hra_block, C, act_max,
+                NXG_OP(NXG_PROF_ROWS, nxg_dwconv_rows(F[4], nullptr, qc.dev, qc.rows, cu, n_seqs, T, C, F[5], s));
+                NXG_OP(NXG_PROF_ROWS, nxg_block_mean_quantize_rows(F[5], F[6], cu, cub, n_seqs, T, TB, hp.hra_block, C, act_max,
                                                      qa_hb.q, qa_hb.sx, s));
                 NXG_TRY(attention(pre, qa_hb, TB, cub, n_seqs, rope[0], -1, scale, max_blocks, F[2], s));
-                NXG_TRY(nxg_upsample_add(F[2], F[7], cu, cub, n_seqs, T, TB, hp.hra_block, C, F[4], s));
+                NXG_OP(NXG_PROF_ROWS, nxg_upsample_add(F[2], F[7], cu, cub, n_seqs, T, TB, hp.hra_block, C, F[4], s));
                 const f32_tensor & co = f32.at(pre + "c_o.depthwise.weight");
-                NXG_TRY(nxg_dwconv_rows(F[4], nullptr, co.dev, co.rows, cu, n_seqs, T, C, F[5], s));
+                NXG_OP(NXG_PROF_ROWS, nxg_dwconv_rows(F[4], nullptr, co.dev, co.rows, cu, n_seqs, T, C, F[5], s));
                 NXG_TRY(gated_out(pre, F[4], F[5], xi, xo, n_seqs, s));
                 break;
             }
@@ -499,27 +558,28 @@ int32_t nxg_encoder::run(const int32_t * ids_dev, const int32_t * types_dev, int
         // x + c_proj(relu(c_fc(norm(x)))^2) (:1284-1289)
         xi = x[cur];
         xo = x[cur ^ 1];
-        NXG_TRY(nxg_rmsnorm_quantize_rows(xi, w(blk + "mlp_norm.weight"), hp.rms_eps, T, C, act_max, qa_h.q, qa_h.sx, s));
+        NXG_OP(NXG_PROF_ROWS, nxg_rmsnorm_quantize_rows(xi, w(blk + "mlp_norm.weight"), hp.rms_eps, T, C, act_max, qa_h.q, qa_h.sx, s));
         if (fuse_mlp) {
-            NXG_TRY(nxg_linear_i8_relu2_q8_rows(i8.at(blk + "mlp.c_fc.weight"), qa_h.q, qa_h.sx, T, act_max, qa_I.q,
+            NXG_OP(NXG_PROF_LINEAR, nxg_linear_i8_relu2_q8_rows(i8.at(blk + "mlp.c_fc.weight"), qa_h.q, qa_h.sx, T, act_max, qa_I.q,
                                                 qa_I.sx, s));
         } else {
-            NXG_TRY(linear(blk + "mlp.c_fc.weight", qa_h, T, nullptr, U, s));
-            NXG_TRY(nxg_quantize_rows_relu2(U, T, I, act_max, qa_I.q, qa_I.sx, s));
+            NXG_OP(NXG_PROF_LINEAR, linear(blk + "mlp.c_fc.weight", qa_h, T, nullptr, U, s));
+            NXG_OP(NXG_PROF_ROWS, nxg_quantize_rows_relu2(U, T, I, act_max, qa_I.q, qa_I.sx, s));
         }
-        NXG_TRY(linear(blk + "mlp.c_proj.weight", qa_I, T, xi, xo, s));
+        NXG_OP(NXG_PROF_LINEAR, linear(blk + "mlp.c_proj.weight", qa_I, T, xi, xo, s));
         cur ^= 1;
     }
     const float * out = x[cur];
     if (n_layers_run < 0) {                    // out_norm (:1290-1291)
         float * dst = hidden_out ? hidden_out : x[cur ^ 1];
-        NXG_TRY(nxg_layer_norm(out, w("out_norm.weight"), w("out_norm.bias"), hp.ln_eps, T, C, dst, s));
+        NXG_OP(NXG_PROF_OTHER, nxg_layer_norm(out, w("out_norm.weight"), w("out_norm.bias"), hp.ln_eps, T, C, dst, s));
         out = dst;
     } else if (hidden_out) {
         NXG_HIP(hipMemcpyAsync(hidden_out, out, (size_t) T * C * sizeof(float), hipMemcpyDeviceToDevice, s),
                 "hipMemcpyAsync(hidden)");
+        NXG_TRY(mark(NXG_PROF_OTHER, s));
     }
-    if (pooled_out) NXG_TRY(nxg_doc_mean(out, cu, n_seqs, T, C, normalize, pooled_out, s));
+    if (pooled_out) NXG_OP(NXG_PROF_ROWS, nxg_doc_mean(out, cu, n_seqs, T, C, normalize, pooled_out, s));
     return NXG_OK;
 }
 
@@ -709,6 +769,7 @@ int32_t load_into(nxg_encoder & e, const char * path, const nxg_encoder_params &
             nxg_weight * wt = nullptr;
             NXG_TRY(nxg_gguf_weight_create(g, i, params.load_threads, &wt));
             e.i8[name] = wt;
+            e.n_int8 += 1;
             e.weight_bytes += nxg_weight_device_bytes(wt);
             continue;
         }
@@ -860,15 +921,40 @@ void nxg_encoder_set_layers(nxg_encoder * e, int32_t n_layers) {
     if (e) e->n_layers_run = n_layers;
 }
 double nxg_encoder_last_ms(const nxg_encoder * e) { return e ? e->last_ms : 0.0; }
+int32_t nxg_encoder_n_int8(const nxg_encoder * e) { return e ? e->n_int8 : 0; }
+
+void nxg_encoder_profile(nxg_encoder * e, int32_t enable) {
+    if (!e) return;
+    const std::vector<hipEvent_t> ev = std::move(e->prof.ev);   // the events are kept for reuse
+    e->prof = nxg_encoder::profiler();
+    e->prof.ev = ev;
+    e->prof.kind.assign(ev.size(), 0);
+    e->prof.enabled = enable != 0;
+}
+
+int32_t nxg_encoder_profile_read(const nxg_encoder * e, double * kind_ms, double * device_ms, double * wall_ms,
+                                 int64_t * passes) {
+    if (!e) return fail(NXG_EINVAL, "encoder_profile_read: null context");
+    for (int k = 0; kind_ms && k < NXG_PROF_COUNT; ++k) kind_ms[k] = e->prof.ms[k];
+    if (device_ms) *device_ms = e->prof.device_ms;
+    if (wall_ms) *wall_ms = e->prof.wall_ms;
+    if (passes) *passes = e->prof.passes;
+    return NXG_OK;
+}
 
 int32_t nxg_encoder_forward(nxg_encoder * e, const int32_t * tokens, const int32_t * token_types,
                             const int32_t * lengths, int32_t n_seqs, float * hidden, float * pooled,
                             int32_t normalize, void * stream) {
     if (!e || !tokens) return fail(NXG_EINVAL, "encoder_forward: null context or tokens");
     hipStream_t s = (hipStream_t) stream;
+    if (e->prof.enabled) {
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        NXG_HIP(hipStreamIsCapturing(s, &st), "hipStreamIsCapturing");
+        if (st != hipStreamCaptureStatusNone) return fail(NXG_EINVAL, "encoder_forward: a profiled pass cannot be captured");
+    }
     NXG_TRY(e->prepare(lengths, n_seqs, s));
     NXG_TRY(e->run(tokens, token_types, n_seqs, hidden, pooled, normalize, s));
-    return NXG_OK;
+    return e->collect(-1.0);
 }
 
 int32_t nxg_encoder_encode(nxg_encoder * e, const int32_t * tokens, const int32_t * token_types,
@@ -905,7 +991,7 @@ int32_t nxg_encoder_encode(nxg_encoder * e, const int32_t * tokens, const int32_
     }
     NXG_HIP(hipStreamSynchronize(s), "compute");
     e->last_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    return NXG_OK;
+    return e->collect(e->last_ms);
 }
 
 } // extern "C"

@@ -176,14 +176,23 @@ def metadata(d: Dims, preset: str) -> list:
 
 
 def write_random_model(nxg, path, preset: str = "Q4_K_M", seed: int = 0, dims: Optional[Dims] = None,
-                       tensors: Optional[Dict[str, np.ndarray]] = None) -> dict:
+                       tensors: Optional[Dict[str, np.ndarray]] = None, extra_metadata: Optional[list] = None,
+                       extra_tensors: Optional[Dict[str, np.ndarray]] = None) -> dict:
     """Writes a random-init model file (or the given tensors, model_tensors' layout);
-    returns {"n_params", "types": {name: block type}}."""
+    returns {"n_params", "types": {name: block type}}. extra_metadata: (key, type, value)
+    entries added to the converter's keys (replacing one of the same key); extra_tensors:
+    more tensors (heads, for instance), typed by the same rule."""
     d = dims or Dims()
     if preset not in PRESETS:
         raise ValueError(f"preset must be one of {sorted(PRESETS)}")
     if tensors is None:
         tensors = model_tensors(d, seed)
+    if extra_tensors:
+        tensors = {**tensors, **extra_tensors}
+    meta = metadata(d, preset)
+    if extra_metadata:
+        keys = {k for k, _, _ in extra_metadata}
+        meta = [m for m in meta if m[0] not in keys] + list(extra_metadata)
     entries, types = [], {}
     for name in sorted(tensors):                 # the converter writes tensors sorted by name
         arr = tensors[name]
@@ -191,5 +200,5 @@ def write_random_model(nxg, path, preset: str = "Q4_K_M", seed: int = 0, dims: O
         ne = tuple(reversed(arr.shape)) if arr.ndim == 2 else (arr.size,)
         entries.append((name, t, ne, encode_tensor(nxg, arr, t)))
         types[name] = t
-    W.write_gguf(path, metadata(d, preset), entries)
+    W.write_gguf(path, meta, entries)
     return {"n_params": int(sum(a.size for a in tensors.values())), "types": types}

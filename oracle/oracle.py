@@ -18,6 +18,8 @@ import os
 import subprocess
 from pathlib import Path
 
+from typing import Optional
+
 import numpy as np
 
 _HERE = Path(__file__).resolve().parent
@@ -32,6 +34,20 @@ def build(force: bool = False) -> Path:
     if force or not _LIB_PATH.exists():
         subprocess.run(["make", "-s", "-B" if force else "liboracle.so"], cwd=_HERE, check=True)
     return _LIB_PATH
+
+
+REFERENCE = Path("/root/reference")
+REF_CLI = _HERE / "_ref" / "nexterabert-cli"
+
+
+def build_reference_cli() -> Optional[Path]:
+    """The reference's command-line client (tools/cli.cpp), compiled unchanged where it lies
+    against include/nexterabert.h and linked to libnexterabert.so (the Makefile's
+    _ref/nexterabert-cli). Only where the reference's tree is present; None otherwise."""
+    if not (REFERENCE / "tools" / "cli.cpp").is_file():
+        return None
+    subprocess.run(["make", "-s", "-B", "_ref/nexterabert-cli", f"REF={REFERENCE}"], cwd=_HERE, check=True)
+    return REF_CLI
 
 
 def lib() -> ctypes.CDLL:

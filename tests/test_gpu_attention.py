@@ -220,3 +220,46 @@ def test_head_major(nxg, torch, dev):
     x = torch.randn(77, 8 * 64, device="cuda")
     y = nxg.head_major(x, 8)
     assert torch.equal(y, x.view(77, 8, 64).permute(1, 0, 2).contiguous())
+
+
+def test_attention_workspace_16384_keys(nxg, torch, dev):
+    """One 16,384-token document: nxg_attention_ws with a 3-slot workspace (few workgroups at a
+    time, each over many query tiles) equals the recomputing kernel (no workspace) bit for bit."""
+    say("attention 16,384 keys: 3-slot workspace vs recomputing kernel")
+    H, G, T = 2, 1, 16384
+    g = torch.Generator("cuda").manual_seed(16)
+    q = torch.randn(T, H * 64, device="cuda", generator=g)
+    k = torch.randn(G, T, 64, device="cuda", generator=g)
+    v = torch.randn(G, T, 64, device="cuda", generator=g)
+    cu = [0, T]
+    scale = np.array([0.125], np.float32)
+    slot = 16 * T * 4
+    y_rec = nxg.attention(q, k, v, cu, scale, H, G)
+    y_ws = nxg.attention(q, k, v, cu, scale, H, G, workspace=torch.empty(3 * slot, dtype=torch.uint8, device="cuda"))
+    torch.cuda.synchronize()
+    assert torch.isfinite(y_rec).all()
+    assert torch.equal(y_rec.view(torch.int32), y_ws.view(torch.int32))
+
+
+def test_attention_auto_workspace_on_a_side_stream(nxg, orc, torch, dev):
+    """workspace="auto" with a caller's stream: the wrapper's temporaries (offsets, scales,
+    workspace) allocated on torch's current stream stay reserved until the side stream's
+    kernel is done, although the caller reuses memory on the current stream right away."""
+    say("attention auto workspace on a side stream")
+    rng = np.random.default_rng(31)
+    H, G, T = 2, 1, 2600
+    cu = nxg.cu_offsets_of([T])
+    q = rng.standard_normal((T, H * 64)).astype(np.float32)
+    k, v = (rng.standard_normal((G, T, 64)).astype(np.float32) for _ in range(2))
+    scale = np.array([0.1], np.float32)
+    ref = orc.attention(q, k, v, cu, scale, H, G)
+    c = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    qd, kd, vd = c(q), c(k), c(v)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    y = nxg.attention(qd, kd, vd, cu, scale, H, G, stream=side, workspace="auto")
+    junk = torch.full((nxg.attention_workspace_bytes(T, H, G, T) // 4 + 4096,), float("nan"), device="cuda")
+    side.synchronize()
+    torch.cuda.synchronize()
+    assert (bits(y.cpu().numpy()) == bits(ref)).all()
+    del junk

@@ -172,3 +172,48 @@ def test_cli_encode_bench(nxg, torch, small_models, capsys):
     assert r.returncode == 0, r.stderr
     line = next(l for l in r.stdout.splitlines() if l.startswith("bench: "))
     assert line.startswith("bench: Q8_0  T=48  batch=2  encoder  median") and "tokens/s" in line
+
+
+BRANCH_BLOCKS = ["lily", "swa", "attn", "hra"]
+
+
+@pytest.mark.parametrize("variant", ["ntk", "ssmax_none", "ssmax", "act63"])
+def test_encoder_branches_match_oracle(nxg, synth, enc, torch, tmp_path, variant):
+    """Branches of the forward pass the default synthetic file does not take, each against the
+    oracle bit for bit: dynamic-NTK RoPE for a single sequence longer than
+    rope.ntk_train_length (src/nexterabert.cpp:1356-1366; a batch of such sequences is refused,
+    one of shorter sequences keeps the base), Scalable-Softmax modes "none" and "ssmax"
+    (:1196-1201), and the AVX2-only build's 7-bit activations (ACT_MAX 63, :53-70)."""
+    say(f"encoder branch {variant}")
+    kw = dict(n_vocab=300, n_embd=256, n_inter=512, n_head=4, n_kv_head=2, lily_rank=64, swa_window=8,
+              block_types=BRANCH_BLOCKS)
+    if variant == "ntk":
+        kw["ntk_train_len"] = 24
+    elif variant.startswith("ssmax"):
+        kw["ssmax_mode"] = {"ssmax_none": "none", "ssmax": "ssmax"}[variant]
+    d = synth.Dims(**kw)
+    path = tmp_path / f"{variant}.gguf"
+    synth.write_random_model(nxg, path, "Q8_0", seed=7, dims=d)
+    act_max = 63 if variant == "act63" else 127
+    m = enc.from_gguf(nxg, path, act_max=act_max)
+    rng = np.random.default_rng(3)
+    cases = [[61]] if variant == "ntk" else [[61], [19, 1, 40]]
+    if variant == "ntk":
+        cases.append([24, 9])                      # every sequence within the trained length: no NTK
+    with nxg.Encoder(path, act_max=act_max) as e:
+        for lengths in cases:
+            tok = rng.integers(0, d.n_vocab, sum(lengths)).astype(np.int32)
+            h, p = e.encode(tok, lengths, pooled=True, normalize=True)
+            hr, pr = enc.encode(m, tok, lengths, normalize=True)
+            assert (bits(h) == bits(hr)).all(), f"hidden differs, lengths={lengths}"
+            assert (bits(p) == bits(pr)).all(), f"pooled differs, lengths={lengths}"
+        if variant == "ntk":
+            with pytest.raises(ValueError, match="one at a time"):
+                e.encode(rng.integers(0, d.n_vocab, 70).astype(np.int32), [30, 40])
+    if variant == "ntk":                           # the stretched base is in use: the bits differ without it
+        d0 = synth.Dims(**{**kw, "ntk_train_len": 0})
+        p0 = tmp_path / "ntk0.gguf"
+        synth.write_random_model(nxg, p0, "Q8_0", seed=7, dims=d0)
+        tok = np.random.default_rng(3).integers(0, d.n_vocab, 61).astype(np.int32)
+        with nxg.Encoder(p0) as e0, nxg.Encoder(path) as e1:
+            assert not (bits(e0.encode(tok, [61])[0]) == bits(e1.encode(tok, [61])[0])).all()
