@@ -222,12 +222,11 @@ def cpu_baseline(path, rows: int, reps: int):
     orc.build()
     if not orc.vnni_flavour():
         return None
-    try:
-        hw = len(os.sched_getaffinity(0))
-    except AttributeError:
-        hw = os.cpu_count() or 1
-    n_threads = min(16, hw)
-    n_threads = max(1, n_threads - n_threads // 10)
+    host = host_cpu()
+    # the reference's default pool, hw - hw/10 (src/nexterabert.cpp:1519-1524), of the cores this
+    # process may use: its affinity, capped at the 16-core share a one-GPU lease grants
+    share = min(CPU_SHARE, host["affinity"])
+    n_threads = max(1, share - share // 10)
     rng = np.random.default_rng(1)
     rb = (rows + 3) // 4
     xs = {}
@@ -264,6 +263,7 @@ def cpu_baseline(path, rows: int, reps: int):
         one_pass()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
+    limited = host["affinity"] > CPU_SHARE
     return {
         "value": round(ops / med / 1e12, 4),
         "unit": "TOPS",
@@ -274,7 +274,34 @@ def cpu_baseline(path, rows: int, reps: int):
                    f"(HRA q/k/v at {rb}), CPU oracle on {orc.vnni_flavour()}, median of {reps} passes "
                    f"after 1 warm-up, {med:.2f} s per pass"),
         "tokens_per_s": round(rows / med, 1),
+        "cpu": host["model"],
+        "nproc": host["nproc"],
+        "affinity": host["affinity"],
+        "threads_rule": (f"hw - hw/10 of {share} cores (the reference's default pool size)"
+                         + (f"; the lease grants a {CPU_SHARE}-core share of the {host['affinity']} CPUs "
+                            "in this process's affinity" if limited else "")),
+        "vnni": orc.vnni_flavour(),
     }
+
+
+CPU_SHARE = 16   # host cores a one-GPU lease grants
+
+
+def host_cpu() -> dict:
+    """The host CPU: model name, logical CPUs, CPUs in this process's affinity."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count() or 1
+    return {"model": model, "nproc": os.cpu_count() or 1, "affinity": aff}
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "gemm_traffic_config5.json"
@@ -330,7 +357,7 @@ def main() -> int:
     ap.add_argument("--no-fuse-mlp", action="store_true",
                     help="c_fc writes fp32 rows, then relu^2 + quantize (instead of the int8 epilogue)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-rows", type=int, default=2048)
+    ap.add_argument("--cpu-rows", type=int, default=8192)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-encoder1024", action="store_true")
     ap.add_argument("--no-encoder", action="store_true", help="skip the whole-encoder timing")

@@ -103,6 +103,9 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_encoder_encode": ([P, P, P, P, i32, P, P, i32], i32),
         "nxg_encoder_forward": ([P, P, P, P, i32, P, P, i32, P], i32),
         "nxg_encoder_last_ms": ([P], ctypes.c_double),
+        "nxg_encoder_n_int8": ([P], i32),
+        "nxg_encoder_profile": ([P, i32], None),
+        "nxg_encoder_profile_read": ([P, P, P, P, P], i32),
         "nxg_rope_table": ([i32, ctypes.c_float, i32, P, P], i32),
         "nxg_qact_export": ([P, P, i32, i32, i32, P, P, P], i32),
         "nxg_weight_create": ([P, P, i32, i32, ctypes.POINTER(P)], i32),
@@ -1014,6 +1017,25 @@ class Encoder:
     @property
     def last_ms(self) -> float:
         return float(load_library().nxg_encoder_last_ms(self._h))
+
+    @property
+    def n_int8(self) -> int:
+        return int(load_library().nxg_encoder_n_int8(self._h))
+
+    PROFILE_KINDS = ("int8 linear", "attention", "norm / conv / gate / quantize", "other device work")
+
+    def profile(self, enable: bool = True) -> None:
+        """nxg_encoder_profile: clear the per-kind device times and turn profiling on or off."""
+        load_library().nxg_encoder_profile(self._h, 1 if enable else 0)
+
+    def profile_read(self) -> dict:
+        """{"passes", "wall_ms", "device_ms", "kinds": {kind: ms}} summed over the profiled passes."""
+        kinds = (ctypes.c_double * 4)()
+        dev, wall, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+        _check(load_library().nxg_encoder_profile_read(self._h, kinds, ctypes.byref(dev), ctypes.byref(wall),
+                                                       ctypes.byref(n)), "encoder_profile_read")
+        return {"passes": int(n.value), "wall_ms": wall.value, "device_ms": dev.value,
+                "kinds": dict(zip(self.PROFILE_KINDS, list(kinds)))}
 
     def set_layers(self, n_layers: int) -> None:
         """Run only the first n_layers blocks, returning the residual stream (-1: all)."""

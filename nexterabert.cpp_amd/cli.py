@@ -14,14 +14,16 @@ rows (see encoder.py). Weights are random Q8_0 unless -m names a GGUF file holdi
 encoder's tensors. --graph replays the pass from a HIP graph instead of launching it.
 --profile adds the device time per kind of launch from HIP events on one extra pass.
 
-    python nexterabert.cpp_amd/cli.py --bench T --encode [--batch B] [--reps R] [-m model.gguf]
+    python nexterabert.cpp_amd/cli.py --bench T --encode [--batch B] [--reps R] [--profile] [-m model.gguf]
 
 --encode times the whole encoder instead (nxg_encoder_encode, the counterpart of
 nextera_encode, on host buffers), exactly as tools/cli.cpp:177-204 times nextera_encode:
 ids uniform in [1000, min(vocab, 40000)) from a fixed seed with CLS first and SEP last in
 each sequence, the pooled vectors L2-normalised as the only output. Without -m the model
 is the 213M-parameter architecture with random-init weights, written as Q4_K_M to a
-temporary file.
+temporary file. With --profile the timed passes are profiled (nxg_encoder_profile) and the
+reference's --profile report follows: ms per pass of the int8 linears, attention and row
+ops (device time from HIP events), everything else, and the total wall time.
 """
 from __future__ import annotations
 
@@ -166,12 +168,34 @@ def bench_encoder(nxg, args) -> str:
             t1 = time.perf_counter()
             if r >= 3:
                 ms.append((t1 - t0) * 1e3)
+            if r == 2 and args.profile:          # the reference CLI profiles the timed passes (tools/cli.cpp:196)
+                enc.profile(True)
+        prof = enc.profile_read() if args.profile else None
     finally:
         enc.close()
     ms.sort()
     med = ms[len(ms) // 2]
-    return (f"bench: {ftype}  T={T}  batch={B}  encoder  median {med:.3f} ms  min {ms[0]:.3f} ms  "
-            f"({1000.0 * T * B / med:.0f} tokens/s)")
+    lines = [f"bench: {ftype}  T={T}  batch={B}  encoder  median {med:.3f} ms  min {ms[0]:.3f} ms  "
+             f"({1000.0 * T * B / med:.0f} tokens/s)"]
+    if prof:
+        lines += profile_lines(prof)
+    return "\n".join(lines)
+
+
+def profile_lines(prof: dict) -> List[str]:
+    """nextera_debug_profile_print's report (src/nexterabert.cpp:1828-1841) from an encoder
+    profile: ms per pass and share of the wall time of the three kinds, the rest, the total."""
+    n, total = max(prof["passes"], 1), max(prof["wall_ms"], 1e-9)
+    out = [f"profile over {prof['passes']} forward passes (ms per pass, GPU time from HIP events):"]
+    done = 0.0
+    for k in ("int8 linear", "attention", "norm / conv / gate / quantize"):
+        t = prof["kinds"][k]
+        done += t
+        out.append(f"  {k:22s} {t / n:8.3f}  {100 * t / total:5.1f}%")
+    out.append(f"  {'everything else':22s} {(total - done) / n:8.3f}  {100 * (total - done) / total:5.1f}%"
+               "   (embedding rows, out_norm, copies, launch gaps, host)")
+    out.append(f"  {'total':22s} {total / n:8.3f}")
+    return out
 
 
 def main(argv: Optional[List[str]] = None) -> int:

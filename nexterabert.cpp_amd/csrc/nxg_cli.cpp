@@ -7,12 +7,14 @@
 //
 //   nxg-cli --info [-m model.gguf]
 //   nxg-cli --bench T [--batch B] [--reps R] [--graph] [--profile] [-m model.gguf]
-//   nxg-cli --bench T --encode -m model.gguf [--batch B] [--reps R]
+//   nxg-cli --bench T --encode -m model.gguf [--batch B] [--reps R] [--profile]
 //
 // --encode times the whole encoder instead (include/nxg_encoder.h: nxg_encoder_encode on
 // host buffers, the counterpart of nextera_encode) with the reference CLI's inputs: ids
 // uniform in [1000, min(vocab, 40000)) from mt19937(0), CLS first and SEP last in each
-// sequence, L2-normalised pooled vectors as the only output.
+// sequence, L2-normalised pooled vectors as the only output. --profile profiles the timed
+// passes (nxg_encoder_profile) and prints the reference's --profile report
+// (src/nexterabert.cpp:1828-1841): int8 linear, attention, row ops, everything else, total.
 //
 // A pass runs every int8 projection of the 18 layers (src/nexterabert.cpp:1185-1289) over B
 // packed sequences of T tokens: per layer each distinct activation is quantized once
@@ -432,11 +434,28 @@ int main(int argc, char ** argv) {
                   "encoder_encode");
             const auto t1 = std::chrono::steady_clock::now();
             if (r >= 3) ms.push_back(std::chrono::duration<double, std::milli>(t1 - t0).count());
+            if (r == 2 && profile) nxg_encoder_profile(enc, 1);   // the timed passes, as tools/cli.cpp:196
         }
         std::sort(ms.begin(), ms.end());
         const double med = ms[ms.size() / 2];
         printf("bench: %s  T=%d  batch=%d  encoder  median %.3f ms  min %.3f ms  (%.0f tokens/s)\n", ftype_of(g).c_str(),
                bench_t, batch, med, ms.front(), 1000.0 * bench_t * batch / med);
+        if (profile) {
+            double kind[NXG_PROF_COUNT] = {}, dev_ms = 0.0, wall = 0.0;
+            int64_t passes = 0;
+            check(nxg_encoder_profile_read(enc, kind, &dev_ms, &wall, &passes), "encoder_profile_read");
+            const char * names[3] = { "int8 linear", "attention", "norm / conv / gate / quantize" };
+            const double n = (double) std::max<int64_t>(passes, 1), total = std::max(wall, 1e-9);
+            double sum = 0.0;
+            printf("profile over %lld forward passes (ms per pass, GPU time from HIP events):\n", (long long) passes);
+            for (int k = 0; k < 3; ++k) {
+                sum += kind[k];
+                printf("  %-22s %8.3f  %5.1f%%\n", names[k], kind[k] / n, 100.0 * kind[k] / total);
+            }
+            printf("  %-22s %8.3f  %5.1f%%   (embedding rows, out_norm, copies, launch gaps, host)\n", "everything else",
+                   (total - sum) / n, 100.0 * (total - sum) / total);
+            printf("  %-22s %8.3f\n", "total", total / n);
+        }
         nxg_encoder_free(enc);
         nxg_gguf_close(g);
         return 0;

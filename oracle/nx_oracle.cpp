@@ -983,6 +983,51 @@ void tanh_avx2(const float * x, int64_t n, float * out) {
 
 } // namespace
 
+namespace {
+
+// softmax_exp (src/nexterabert.cpp:177-197) on the instructions the reference uses: the
+// running std::max, exp256 of each whole 8-group added into one 256-bit lane sum, hsum256
+// (VEXTRACTF128 / ADDPS / MOVHLPS / ADDPS / MOVSHDUP / ADDSS), then the tail with the C
+// library's expf added one by one. The scalar statement softmax_exp_lanes is checked
+// against it.
+__attribute__((target("avx2,fma")))
+float softmax_exp_avx2(float * s, int n) {
+    float m = s[0];
+    for (int i = 1; i < n; ++i) m = std::max(m, s[i]);
+    int i = 0;
+    float sum = 0.0f;
+    const __m256 vm = _mm256_set1_ps(m);
+    __m256 vs = _mm256_setzero_ps();
+    for (; i + 8 <= n; i += 8) {
+        const __m256 e = exp256_avx2(_mm256_sub_ps(_mm256_loadu_ps(s + i), vm));
+        _mm256_storeu_ps(s + i, e);
+        vs = _mm256_add_ps(vs, e);
+    }
+    __m128 h = _mm_add_ps(_mm256_castps256_ps128(vs), _mm256_extractf128_ps(vs, 1));
+    h = _mm_add_ps(h, _mm_movehl_ps(h, h));
+    h = _mm_add_ss(h, _mm_movehdup_ps(h));
+    sum = _mm_cvtss_f32(h);
+    for (; i < n; ++i) {
+        s[i] = std::exp(s[i] - m);
+        sum += s[i];
+    }
+    return sum;
+}
+
+} // namespace
+
+// softmax_exp on s[0..n): the weights in place, the sum in *sum; simd != 0: on AVX2 + FMA
+// (returns -1 without them), else the scalar statement the attention oracle uses.
+extern "C" int orc_softmax_exp(float * s, int n, int simd, float * sum) {
+    if (simd) {
+        if (!__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma")) return -1;
+        *sum = softmax_exp_avx2(s, n);
+        return 0;
+    }
+    *sum = softmax_exp_lanes(s, n);
+    return 0;
+}
+
 extern "C" int orc_tanh_simd(const float * x, int64_t n, float * out) {
     if (n % 8 != 0 || !__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma")) return -1;
     tanh_avx2(x, n, out);

@@ -94,6 +94,7 @@ def lib() -> ctypes.CDLL:
         L.orc_expf_restated_check.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, P, i32]
         L.orc_expf_restated_check.restype = i64
         L.orc_scores_d64.argtypes, L.orc_scores_d64.restype = [P, P, i32, ctypes.c_float, P], None
+        L.orc_softmax_exp.argtypes, L.orc_softmax_exp.restype = [P, i32, i32, P], i32
         L.orc_scores_d64_simd.argtypes, L.orc_scores_d64_simd.restype = [P, P, i32, ctypes.c_float, P], i32
         L.orc_dequant_q8_0.argtypes = [P, ctypes.c_int64, P]
         L.orc_dequant_q8_0.restype = None
@@ -356,6 +357,16 @@ def scores_d64(q: np.ndarray, k: np.ndarray, scale: float, simd: bool = False) -
     else:
         lib().orc_scores_d64(_p(q), _p(k), n, float(scale), _p(out))
     return out
+
+
+def softmax_exp(s: np.ndarray, simd: bool = False):
+    """softmax_exp (src/nexterabert.cpp:177-197) of a row of scores: (weights exp(s - max),
+    their sum in the reference's order). simd: on AVX2 + FMA, else the scalar statement."""
+    w = np.array(s, dtype=np.float32, copy=True)
+    total = ctypes.c_float()
+    if lib().orc_softmax_exp(_p(w), w.size, 1 if simd else 0, ctypes.byref(total)) != 0:
+        raise RuntimeError("AVX2/FMA not available")
+    return w, np.float32(total.value)
 
 
 def expand_rows(rows: np.ndarray, act_off: int = 128):

@@ -172,6 +172,25 @@ def test_cli_encode_bench(nxg, torch, small_models, capsys):
     assert r.returncode == 0, r.stderr
     line = next(l for l in r.stdout.splitlines() if l.startswith("bench: "))
     assert line.startswith("bench: Q8_0  T=48  batch=2  encoder  median") and "tokens/s" in line
+    # --profile: the reference's report of where the time goes, the timed passes only
+    import re
+    say("cli / nxg-cli --bench 48 --batch 2 --reps 3 --encode --profile")
+    assert cli.main(["--bench", "48", "--batch", "2", "--reps", "3", "--encode", "--profile", "-m", str(path)]) == 0
+    outs = [capsys.readouterr().out]
+    r = subprocess.run([str(root / "nexterabert.cpp_amd" / "nxg-cli"), "--bench", "48", "--batch", "2", "--reps", "3",
+                        "--encode", "--profile", "-m", str(path)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    outs.append(r.stdout)
+    for out in outs:
+        assert "profile over 3 forward passes" in out, out
+        rows = {}
+        for k in ("int8 linear", "attention", "norm / conv / gate / quantize", "everything else"):
+            m = re.search(re.escape(k) + r"\s+(-?[\d.]+)\s+(-?[\d.]+)%", out)
+            assert m, (k, out)
+            rows[k] = float(m.group(1))
+        total = float(re.search(r"\n\s+total\s+([\d.]+)", out).group(1))
+        assert all(rows[k] > 0 for k in ("int8 linear", "attention", "norm / conv / gate / quantize")), out
+        assert abs(sum(rows.values()) - total) <= 0.01 + 1e-3 * total, out
 
 
 BRANCH_BLOCKS = ["lily", "swa", "attn", "hra"]

@@ -43,6 +43,61 @@ def test_scores_lane_statement_equals_avx2(orc, n):
     assert (bits(orc.scores_d64(q, k, 0.125)) == bits(s)).all()
 
 
+def sequential_softmax(s):
+    """softmax_exp's weights (exp256 for the 8-groups, expf for the tail, as the oracle) but
+    summed one by one in index order: a plausible wrong order the pin must reject."""
+    import oracle.oracle as o
+    w, _ = o.softmax_exp(s)
+    total = np.float32(0)
+    for x in w:
+        total = np.float32(total + x)
+    return w, total
+
+
+@pytest.mark.parametrize("n", list(range(1, 101)))
+def test_softmax_exp_order_equals_avx2(orc, n):
+    """softmax_exp's lane statement (8 lane sums of the 8-groups, hsum256, then the tail one by
+    one) equals the reference's instructions on AVX2 + FMA bit for bit, weights and sum, on
+    scores spread over +-30 (so the weights span many binades)."""
+    rng = np.random.default_rng(1000 + n)
+    s = (rng.standard_normal(n) * rng.uniform(0.1, 10)).astype(np.float32)
+    try:
+        w_simd, sum_simd = orc.softmax_exp(s, simd=True)
+    except RuntimeError:
+        pytest.skip("no AVX2/FMA")
+    w, total = orc.softmax_exp(s)
+    assert (bits(w) == bits(w_simd)).all()
+    assert bits(np.float32(total)) == bits(np.float32(sum_simd))
+    assert w.max() == np.float32(1.0)                   # exp(max - max)
+
+
+def test_softmax_exp_order_is_pinned(orc):
+    """A constructed row whose sequential sum differs from the lane order's: the statement
+    follows the reference's instructions there too, so a wrong order fails the test above."""
+    try:
+        orc.softmax_exp(np.zeros(8, np.float32), simd=True)
+    except RuntimeError:
+        pytest.skip("no AVX2/FMA")
+    # one weight of 1 (the max) among weights e^-15 .. e^-18, around half an ulp of 1: summed
+    # one by one many of them round away, in 8 lanes they add up before meeting the 1
+    found = None
+    rng = np.random.default_rng(77)
+    for trial in range(2000):
+        n = int(rng.integers(9, 40))
+        s = np.concatenate([[0.0], rng.uniform(-18, -15, n - 1)]).astype(np.float32)
+        rng.shuffle(s)
+        w, total = orc.softmax_exp(s)
+        _, seq = sequential_softmax(s)
+        if bits(np.float32(total)) != bits(np.float32(seq)):
+            found = s
+            break
+    assert found is not None, "no row where the orders differ"
+    w, total = orc.softmax_exp(found)
+    w_simd, sum_simd = orc.softmax_exp(found, simd=True)
+    assert bits(np.float32(total)) == bits(np.float32(sum_simd))
+    assert bits(np.float32(sequential_softmax(found)[1])) != bits(np.float32(sum_simd))
+
+
 def rand_qkv(rng, T, H, G):
     q = rng.standard_normal((T, H * 64)).astype(np.float32)
     k = rng.standard_normal((G, T, 64)).astype(np.float32)
