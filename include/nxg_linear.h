@@ -210,6 +210,19 @@ NXG_API int32_t nxg_attention_ws(const float * q, const float * k, const float *
                                  int32_t half, int32_t max_keys, float * out, void * workspace,
                                  int64_t workspace_bytes, void * stream);
 
+/* nxg_attention_ws without a caller's workspace and without allocating: no counterpart in
+ * the reference; for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The workspace is a static
+ * device array of NXG_NOALLOC_SCRATCH_BYTES in the library, one per GPU, held until the
+ * process ends; the call uses as many of its slots (16 * max_keys floats each) as fit, and
+ * refuses (NXG_EINVAL) a max_keys whose single slot would not fit (more than 1,048,576 keys).
+ * Same arguments and results as nxg_attention. Calls that overlap on one GPU race (they
+ * share the array); calls in one stream, or synchronized, do not. */
+#define NXG_NOALLOC_SCRATCH_BYTES (64u << 20)
+NXG_API int32_t nxg_attention_noalloc(const float * q, const float * k, const float * v, const int32_t * cu_offsets,
+                                      int32_t n_seqs, const float * scale, int32_t T, int32_t n_head,
+                                      int32_t n_kv_head, int32_t half, int32_t max_keys, float * out, void * stream);
+
 /* Sizing for nxg_attention_ws (no counterpart in the reference, whose op_attention keeps a
  * document's scores in host memory): the workspace it uses for these sizes: 0 when the launch does not need one,
  * else one slot per resident workgroup (a negative NXG_E* code for invalid sizes). */

@@ -20,6 +20,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <type_traits>
 #include <vector>
@@ -3133,6 +3134,34 @@ int32_t nxg_block_mean_quantize_rows(const float * h, const float * g, const int
 
 // Resident workgroups of attention_stored_kernel on the device (its persistent grid and
 // the workspace slots), queried once.
+// The scratch of nxg_attention_noalloc: a device array of the code object, so the entry point
+// allocates nothing. Each GPU the library runs on holds its own copy at its own address (until
+// the process ends); host code uses that address, found once per device by
+// hipGetSymbolAddress, never the array's name (a host-side stand-in). Every call on a GPU
+// shares the array: the scores a workgroup writes to its slot are read back by the same
+// workgroup within the call, so nothing needs clearing, and calls that overlap on one GPU race.
+static __device__ __align__(256) float scratch[NXG_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+static constexpr int MAX_DEVICES = 64;
+static std::mutex scratch_mutex;
+static void * scratch_ptr[MAX_DEVICES] = {};
+
+static int scratch_of_device(void ** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= MAX_DEVICES) return fail(NXG_EDEVICE, "attention_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_ptr[dev]) {
+        void * p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+        scratch_ptr[dev] = p;
+    }
+    *out = scratch_ptr[dev];
+    return NXG_OK;
+}
+
 static long long attention_long_slots() {
     static long long slots = 0;
     static bool done = false;
@@ -3181,6 +3210,32 @@ int64_t nxg_attention_workspace_bytes(int32_t T, int32_t n_head, int32_t n_kv_he
     const attn_plan pl = plan_attention(T, n_head, n_kv_head, max_keys);
     if (pl.kind != 1) return 0;
     return std::min(pl.n_tiles, attention_long_slots()) * pl.slot_bytes;
+}
+
+int32_t nxg_attention_noalloc(const float * q, const float * k, const float * v, const int32_t * cu_offsets,
+                              int32_t n_seqs, const float * scale, int32_t T, int32_t n_head, int32_t n_kv_head,
+                              int32_t half, int32_t max_keys, float * out, void * stream) {
+    if (T < 0 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head != 0 || max_keys < 1) {
+        return fail(NXG_EINVAL, "attention_noalloc: T=%d n_head=%d n_kv_head=%d max_keys=%d", T, n_head, n_kv_head,
+                    max_keys);
+    }
+    if (T == 0) return NXG_OK;
+    int rc = check_device();
+    if (rc) return rc;
+    const attn_plan pl = plan_attention(T, n_head, n_kv_head, max_keys);
+    if (pl.kind == 1 && pl.slot_bytes > (long long) NXG_NOALLOC_SCRATCH_BYTES) {
+        return fail(NXG_EINVAL,
+                    "attention_noalloc: max_keys=%d needs %lld bytes per workgroup's scores; the static scratch "
+                    "holds %lld (at most %lld keys)", max_keys, pl.slot_bytes, (long long) NXG_NOALLOC_SCRATCH_BYTES,
+                    (long long) NXG_NOALLOC_SCRATCH_BYTES / (ATT_P * (long long) sizeof(float)));
+    }
+    void * ws = nullptr;
+    if (pl.kind == 1) {
+        rc = scratch_of_device(&ws);
+        if (rc) return rc;
+    }
+    return nxg_attention_ws(q, k, v, cu_offsets, n_seqs, scale, T, n_head, n_kv_head, half, max_keys, out, ws,
+                            ws ? (int64_t) NXG_NOALLOC_SCRATCH_BYTES : 0, stream);
 }
 
 int32_t nxg_attention(const float * q, const float * k, const float * v, const int32_t * cu_offsets,
