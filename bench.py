@@ -17,7 +17,9 @@ Output: one JSON line. `value` is int8 TOPS of the whole step (quantization
 included, 2 ops per MAC of the GEMMs); `roofline` describes the GEMM kernel from
 HIP events around every GEMM launch of the timed steps; `cpu_baseline` times the
 CPU oracle (the same path on VPDPBUSD, the reference's instruction) on a row
-sample on this host. The 1,024-token encoder line is the same path at M=1024,
+sample on this host; `mfma_counters` gives each GEMM kind's MFMA-busy %, counted int8
+ops and shader clock from a rocprofv3 --pmc pass over the same workload, run as a
+child process before this one touches the GPU (--no-counters skips it). The 1,024-token encoder line is the same path at M=1024,
 replayed from a HIP graph; `encoder` times the whole encoder forward (nxg_encoder:
 embedding, every block, out_norm) on the 213M-parameter model at 1x1024 and 8x1024
 tokens and on one 8,192- and one 65,536-token document, beside the reference's published CPU timings of
@@ -28,8 +30,12 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import shutil
+import signal
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -306,6 +312,123 @@ def host_cpu() -> dict:
 
 TRAFFIC_FILE = ROOT / "profiles" / "gemm_traffic_config5.json"
 
+# MFMA utilisation from hardware counters, one rocprofv3 --pmc pass (2 SQ + 1 GRBM counters).
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_I8", "GRBM_GUI_ACTIVE")
+N_XCC = 8                      # GRBM_GUI_ACTIVE is summed over the 8 XCDs
+INT8_OPS_PER_SIMD_CYCLE = 2048  # v_mfma_i32_32x32x32_i8: 65,536 ops in 32 cycles
+
+
+def gemm_class(name: str):
+    if "gemm_relu2_q8" in name or "gemm_relu2_small" in name:
+        return "relu2"
+    if "gemm_k256" in name or "gemm_kernel" in name or "gemm_small" in name:
+        return "fp32"
+    return None
+
+
+def counter_pass(args) -> int:
+    """The child of mfma_counters: the same workload, one warm-up and two steps, under the
+    profiler; prints the device's CU count for the parent."""
+    import torch
+    import __graft_entry__
+    nxg = __graft_entry__.load_package()
+    torch.cuda.set_device(0)
+    nxg.init()
+    path = LinearPath(nxg, args.rows, fuse=not args.no_fuse, fuse_mlp=not args.no_fuse_mlp)
+    for _ in range(3):
+        path.step()
+    torch.cuda.synchronize()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    print(json.dumps({"counter_pass": "done", "cus": cus, "gemms_per_step": path.n_gemm}), flush=True)
+    return 0
+
+
+def summarize_counters(csv_path: Path, cus: int, skip_first: int) -> dict:
+    """Per GEMM kind, from a counter_collection.csv of MFMA_COUNTERS: MFMA-busy % (the
+    MfmaUtil metric: busy cycles summed over all SIMDs / (GUI-active cycles of an XCD x
+    SIMDs)), the int8 ops the MFMAs counted (MOPS_I8 x 512), the shader clock (GUI-active
+    cycles of an XCD / dispatch time) and the ops rate against the peak at that clock.
+    The first skip_first dispatches of each kind (the warm-up step) are left out."""
+    import csv
+    disp = {}
+    for row in csv.DictReader(open(csv_path)):
+        kind = gemm_class(row["Kernel_Name"])
+        if kind is None:
+            continue
+        d = disp.setdefault(int(row["Dispatch_Id"]), {"kind": kind, "name": row["Kernel_Name"]})
+        d[row["Counter_Name"]] = float(row["Counter_Value"])
+        d["ns"] = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+    simds = 4 * cus
+    res = {}
+    for kind in ("fp32", "relu2"):
+        ds = [disp[k] for k in sorted(disp) if disp[k]["kind"] == kind]
+        ds = ds[skip_first * len(ds) // (skip_first + 2):] if ds else ds
+        ds = [d for d in ds if all(c in d for c in MFMA_COUNTERS) and d["ns"] > 0]
+        if not ds:
+            continue
+        busy = [100.0 * d["SQ_VALU_MFMA_BUSY_CYCLES"] / (d["GRBM_GUI_ACTIVE"] / N_XCC * simds) for d in ds]
+        ghz = [d["GRBM_GUI_ACTIVE"] / N_XCC / d["ns"] for d in ds]
+        ops = [d["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512 for d in ds]
+        tops = [o / d["ns"] / 1e3 for o, d in zip(ops, ds)]
+        at_clk = [100.0 * t * 1e12 / (simds * INT8_OPS_PER_SIMD_CYCLE * g * 1e9) for t, g in zip(tops, ghz)]
+        names = sorted({d["name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+                        for d in ds})
+        res[kind] = {"kernels": names, "dispatches": len(ds),
+                     "mfma_busy_pct": round(statistics.mean(busy), 2),
+                     "int8_ops_counted_per_launch": int(statistics.mean(ops)),
+                     "clock_ghz": round(statistics.mean(ghz), 3),
+                     "us_per_launch_profiled": round(statistics.mean(d["ns"] for d in ds) / 1e3, 2),
+                     "int8_tops_profiled": round(statistics.mean(tops), 1),
+                     "pct_of_peak_at_clock": round(statistics.mean(at_clk), 2)}
+    return res
+
+
+def mfma_counters(args, timeout_s: int = 240) -> dict:
+    """MFMA utilisation of the two GEMM kinds from hardware counters: a child process runs
+    the same workload (one warm-up and two steps) under rocprofv3 --pmc MFMA_COUNTERS.
+    Started before this process touches the GPU; on any failure the reason is returned
+    instead of figures."""
+    rocprof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not Path(rocprof).exists():
+        return {"status": "not measured: rocprofv3 not found"}
+    out = Path(tempfile.mkdtemp(prefix="nxg_pmc_", dir="/tmp"))
+    child = [sys.executable, str(ROOT / "bench.py"), "--counter-pass", "--rows", str(args.rows)]
+    if args.no_fuse:
+        child.append("--no-fuse")
+    if args.no_fuse_mlp:
+        child.append("--no-fuse-mlp")
+    cmd = [rocprof, "--pmc", *MFMA_COUNTERS, "--output-format", "csv", "-d", str(out), "-o", "pmc", "--", *child]
+    res = {"command": "rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + " --output-format csv -d DIR -o pmc -- "
+                      "python3 bench.py --counter-pass --rows " + str(args.rows)}
+    t0 = time.perf_counter()
+    try:
+        proc = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), stdout=subprocess.PIPE,
+                                stderr=subprocess.STDOUT, text=True, start_new_session=True)
+        try:
+            text, _ = proc.communicate(timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.communicate()
+            res["status"] = f"not measured: the profiled pass did not finish in {timeout_s} s"
+            return res
+        info = None
+        for line in text.splitlines():
+            if line.startswith('{"counter_pass"'):
+                info = json.loads(line)
+        files = sorted(out.rglob("*counter_collection.csv"))
+        # rocprofv3 may end with a signal after a complete run; the child's own line and
+        # the CSV say whether the results are whole
+        if info is None or not files:
+            tail = " | ".join(text.strip().splitlines()[-3:])
+            res["status"] = f"not measured: rocprofv3 exit {proc.returncode}: {tail[-300:]}"
+            return res
+        res.update(summarize_counters(files[0], info["cus"], skip_first=1))
+        res["status"] = "ok"
+        res["profiled_pass_s"] = round(time.perf_counter() - t0, 1)
+        return res
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+
 
 def pmc_summary(fetch_csv: str, write_csv: str, calib_mib: int, out_path: Path) -> dict:
     """HBM traffic per launch of the GEMM and quantize kernels from two rocprofv3 --pmc
@@ -365,6 +488,9 @@ def main() -> int:
                     help="also time the whole encoder on one document of each of these lengths ('': none)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one plain device copy of this many MiB first (PMC counter calibration)")
+    ap.add_argument("--no-counters", action="store_true",
+                    help="skip the rocprofv3 MFMA-counter pass (MFMA busy %% of both GEMM kinds)")
+    ap.add_argument("--counter-pass", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarize two rocprofv3 --pmc counter_collection.csv files of a run with "
                          "--calib-copy-mib into " + str(TRAFFIC_FILE.relative_to(ROOT)) + " and exit")
@@ -377,6 +503,13 @@ def main() -> int:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the linear path shards by rows with no exchange; see the design notes)", file=sys.stderr)
         return 2
+    if args.counter_pass:
+        return counter_pass(args)
+    counters = None
+    if not args.no_counters:
+        # before this process initialises the GPU: the profiler runs as a separate child
+        counters = mfma_counters(args)
+        log(f"MFMA counters: {counters}")
 
     import torch
     import __graft_entry__
@@ -427,6 +560,8 @@ def main() -> int:
     # The dominant kernel: the fp32-output GEMM (most launches and most of the time).
     n_fp32 = path.n_gemm - path.n_relu2
     roof = roofline(n_fp32, path.ops_fp32, path.gemm_bytes, gemm_ms["fp32"], "gemm_k256 (nxg_linear_i8)")
+    if counters and "fp32" in counters:
+        roof["mfma_busy_pct"] = counters["fp32"]["mfma_busy_pct"]
     if TRAFFIC_FILE.exists() and args.rows == 65536 and not args.no_fuse:
         tr = json.loads(TRAFFIC_FILE.read_text())
         if "gemm_fp32" in tr:
@@ -437,6 +572,8 @@ def main() -> int:
     if path.n_relu2:
         roof_relu2 = roofline(path.n_relu2, path.ops_relu2, path.relu2_bytes, gemm_ms["relu2"],
                               "gemm_relu2_q8 (nxg_linear_i8_relu2_q8)")
+        if counters and "relu2" in counters:
+            roof_relu2["mfma_busy_pct"] = counters["relu2"]["mfma_busy_pct"]
         if TRAFFIC_FILE.exists() and args.rows == 65536 and not args.no_fuse:
             tr = json.loads(TRAFFIC_FILE.read_text())
             if "gemm_relu2" in tr:
@@ -483,6 +620,7 @@ def main() -> int:
                    "mlp_relu2_int8_epilogue": path.n_relu2 > 0, "weights": "Q8_0 expanded to int8",
                    "parallelism": "single GPU"},
         "pct_of_mfma_peak": round(100 * value / PEAK_INT8_TOPS, 2),
+        "mfma_counters": counters,
         "tokens_per_s": round(args.rows / (ms * 1e-3), 1),
         "gemm_only": {"int8_tops": round(gemm_tops, 2), "pct_of_mfma_peak": round(100 * gemm_tops / PEAK_INT8_TOPS, 2),
                       "ms_per_step": round(gemm_total, 4),

@@ -27,26 +27,17 @@
 
 #include "nxg_linear.h"
 #include "nxg_internal.h"
+#include "nxg_gemm_plan.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+#define NXG_ATTN_MAX_KEYS 16384          // keys per query the attention's LDS holds (64 KiB)
+
 namespace {
 
-constexpr int BLK = NXG_BLOCK;   // inputs per scale block
-constexpr int FRAG = 1024;       // bytes of one 16-row x 64-input fragment
-constexpr int BM = 128;          // GEMM workgroup tile: rows (tokens)
-constexpr int BN = 128;          //                      columns (output features)
-constexpr int NTHREADS = 256;    // 4 waves, 2 x 2, each 64 x 64
-constexpr int WBN = 256;         // relu^2 -> int8 GEMM tile columns: one 256-input block of the next linear
-constexpr int WTHREADS = 512;    // relu^2 -> int8 GEMM: 8 waves, 2 x 4, each 64 x 64
-constexpr int N_XCD = 8;         // MI355X: 8 XCDs, workgroups dispatched round-robin
-#define NXG_ATTN_MAX_KEYS 16384          // keys per query the attention's LDS holds (64 KiB)
-#ifndef NXG_WG_PER_CU
-#define NXG_WG_PER_CU 2          // persistent GEMM workgroups per CU (0: one workgroup per tile)
-#endif
-
-__host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+// tiles, fragments, the tile walk, the operand and output addresses, the launch plan
+using namespace nxg_gemm;
 
 // ---------------------------------------------------------------------------
 // quantize
@@ -1791,49 +1782,10 @@ struct gemm_params {
 };
 
 // Where output column n of row t goes: base + t * ld + col.
-struct out_map {
-    float * base;
-    int col, ld;
-};
+typedef out_col<float *> out_map;
 __device__ __forceinline__ out_map out_of(const gemm_params & p, int n) {
-    out_map m{ p.out, n, p.N };
-    if (p.n_seg > 0) {
-        int lo = 0, hi = p.seg_end[0];
-        float * b = p.seg_out[0];
-        // the segments are kernel arguments: selected, not indexed
-        if (p.n_seg > 1 && n >= p.seg_end[0]) { b = p.seg_out[1]; lo = p.seg_end[0]; hi = p.seg_end[1]; }
-        if (p.n_seg > 2 && n >= p.seg_end[1]) { b = p.seg_out[2]; lo = p.seg_end[1]; hi = p.seg_end[2]; }
-        if (p.n_seg > 3 && n >= p.seg_end[2]) { b = p.seg_out[3]; lo = p.seg_end[2]; hi = p.seg_end[3]; }
-        m = out_map{ b, n - lo, hi - lo };
-    }
-    return m;
+    return out_col_of<float *>(n, p.N, p.n_seg, p.seg_end, p.out, p.seg_out);
 }
-
-// Tiles of one workgroup. Workgroups are dispatched to the 8 XCDs round-robin
-// (workgroup w runs on XCD w % 8). Each XCD owns a contiguous range of tile
-// numbers, dealt out round-robin to its workgroups; tiles are numbered with the
-// column tile fastest, so the workgroups of an XCD work on neighbouring row tiles
-// at the same time and share them (and the whole weight) in that XCD's L2.
-struct tile_walk {
-    int first, stride, count;
-    __device__ tile_walk(int wg, int n_wg, int G) {
-        const int xcd = wg % N_XCD, idx = wg / N_XCD;
-        const int per = n_wg / N_XCD + (xcd < n_wg % N_XCD ? 1 : 0);     // workgroups on this XCD
-        const int q = G / N_XCD, r = G % N_XCD;
-        const int lo = xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q;
-        const int n = q + (xcd < r ? 1 : 0);                              // tiles of this XCD
-        first = lo + idx;
-        stride = per;
-        count = idx < n ? (n - idx + per - 1) / per : 0;
-    }
-    __device__ int tile(int i) const { return first + i * stride; }
-};
-
-// LDS ring: four slots, one 64-input k-step each: 8 A fragments, 8 B fragments
-// and (slot 3 only) the block's scales: sx of the tile's 128 rows (as 32 groups of
-// 4), then sw of its 128 columns.
-constexpr int SLOT_AB = (BM / 16 + BN / 16) * FRAG;   // 16 KiB
-constexpr int SLOT = SLOT_AB + 1024;
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -1891,11 +1843,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
     // Scales of block B of tile (mt, nt) for lane l of wave 0: l < 32 sx of row group
     // l of the tile, l >= 32 sw of columns 4(l-32)..+3.
     auto scale_src = [&](int mt, int nt, int B) -> const float * {
-        if (lane < 32) {
-            const int grp = min(mt * (BM / 4) + lane, p.MF * 4 - 1);
-            return p.sx + ((size_t) grp * p.n_blk + B) * 4;
-        }
-        return p.sw + (size_t) B * p.NP + nt * BN + 4 * (lane - 32);
+        if (lane < 32) return p.sx + sx_group_index(mt, lane, p.MF, p.n_blk, B);
+        return p.sw + sw_index(B, p.NP, nt * BN + 4 * (lane - 32));
     };
 
     // The load stream: k-steps in order, across this workgroup's tiles. Wave w moves
@@ -1908,13 +1857,15 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
     const int8_t * ia0 = nullptr;
     const int8_t * ia1 = nullptr;
     const int8_t * ib0 = nullptr;
+    const int8_t * ib1 = nullptr;
     auto issue_tile = [&]() {            // per-lane sources of k-step 0 of tile iss_it
         const int tile = walk.tile(iss_it);
         iss_mt = tile / p.n_nt;
         iss_nt = tile - iss_mt * p.n_nt;
-        ia0 = p.a + (size_t) min(iss_mt * (BM / 16) + wave, p.MF - 1) * p.KS * FRAG + lane * 16;
-        ia1 = p.a + (size_t) min(iss_mt * (BM / 16) + wave + 4, p.MF - 1) * p.KS * FRAG + lane * 16;
-        ib0 = p.w + (size_t) (iss_nt * (BN / 16) + wave) * p.KS * FRAG + lane * 16;
+        ia0 = p.a + frag_byte(a_frag(iss_mt, wave, p.MF), p.KS, 0, lane);
+        ia1 = p.a + frag_byte(a_frag(iss_mt, wave + 4, p.MF), p.KS, 0, lane);
+        ib0 = p.w + frag_byte(w_frag(iss_nt, BN, wave), p.KS, 0, lane);
+        ib1 = p.w + frag_byte(w_frag(iss_nt, BN, wave + 4), p.KS, 0, lane);
     };
     issue_tile();
     auto issue = [&](int8_t * slot) {
@@ -1923,7 +1874,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
         dma16(ia0 + o, slot + wave * FRAG);
         dma16(ia1 + o, slot + (wave + 4) * FRAG);
         dma16(ib0 + o, slot + (8 + wave) * FRAG);
-        dma16(ib0 + o + (size_t) 4 * p.KS * FRAG, slot + (12 + wave) * FRAG);
+        dma16(ib1 + o, slot + (12 + wave) * FRAG);
         if (!SUMS && wave == 0 && (iss_ks & 3) == 3) dma16(scale_src(iss_mt, iss_nt, iss_ks >> 2), s3 + SLOT_AB);
         if (++iss_ks == p.KS) {
             iss_ks = 0;
@@ -2041,7 +1992,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
                 // lane%16, features 16ni + 4(lane/16) + 0..3), read it back as 4 rows of
                 // 256 bytes per instruction, and store whole 128-byte lines.
                 lds_barrier();
-                float * stg = reinterpret_cast<float *>(s3 + wave * 4352);
+                float * stg = reinterpret_cast<float *>(s3 + wave * STAGE_BYTES);
                 const int trow = lane & 15, tcol = 4 * (lane >> 4);
                 const int rrow = lane >> 4, rcol = 4 * (lane & 15);
                 const int tbase = mt * BM + wm * 64, nb = nt * BN + wn * 64 + rcol;
@@ -2050,13 +2001,13 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_kernel(gemm_params p) {
 #pragma unroll
                     for (int ni = 0; ni < 4; ++ni) {
                         const v4f y = { f[mi][ni][0], f[mi][ni][1], f[mi][ni][2], f[mi][ni][3] };
-                        *reinterpret_cast<v4f *>(stg + trow * 68 + 16 * ni + tcol) = y;
+                        *reinterpret_cast<v4f *>(stg + trow * STAGE_PITCH + 16 * ni + tcol) = y;
                     }
                     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const int row = 4 * q + rrow;
-                        v4f y = *reinterpret_cast<const v4f *>(stg + row * 68 + rcol);
+                        v4f y = *reinterpret_cast<const v4f *>(stg + row * STAGE_PITCH + rcol);
                         const int t = tbase + mi * 16 + row;
                         if (t < p.T && nb < p.N) {
                             const size_t o = (size_t) t * p.N + nb;
@@ -2147,13 +2098,13 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
     // Tile i of the walk (clamped to the last one). A fragment rows past the last
     // row of A re-read its last fragment row; those output rows are never stored.
     auto rows_of = [&](int i) {
-        const int tile = walk.tile(min(i, walk.count - 1));
+        const int tile = walk.tile_clamped(i);
         const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
         frag_rows r;
-        r.a0 = uniform_ptr(p.a + (size_t) min(mt * (BM / 16) + wave, p.MF - 1) * frow);
-        r.a1 = uniform_ptr(p.a + (size_t) min(mt * (BM / 16) + wave + 4, p.MF - 1) * frow);
-        r.w0 = uniform_ptr(p.w + (size_t) (nt * (BN / 16) + wave) * frow);
-        r.w1 = uniform_ptr(p.w + (size_t) (nt * (BN / 16) + wave + 4) * frow);
+        r.a0 = uniform_ptr(p.a + (size_t) a_frag(mt, wave, p.MF) * frow);
+        r.a1 = uniform_ptr(p.a + (size_t) a_frag(mt, wave + 4, p.MF) * frow);
+        r.w0 = uniform_ptr(p.w + (size_t) w_frag(nt, BN, wave) * frow);
+        r.w1 = uniform_ptr(p.w + (size_t) w_frag(nt, BN, wave + 4) * frow);
         return r;
     };
     // k-step ks of a tile into ring slot j: A fragments w and w + 4 of the slot,
@@ -2204,15 +2155,21 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
         const int tile = walk.tile(it);
         const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
         const frag_rows cur = rows_of(it), nxt = rows_of(it + 1);
+        // the load that k-step j of block B issues (ring_prefetch: this tile's k-step
+        // 4B + 3 + j, or in the last block the next tile's k-step j - 1)
+        auto prefetch = [&](int B, int j, auto last_tag) {
+            const ring_load l = ring_prefetch(it, B, j, decltype(last_tag)::value);
+            issue(l.pos == it ? cur : nxt, l.ks, l.slot);
+        };
         // wave 0's scale loads: lane l < 32 the sx of row group l of the tile, lane
         // l >= 32 the sw of columns 4(l-32)..+3; block B adds B * sstep bytes.
         const float * ssrc;
         size_t sstep;
         if (lane < 32) {
-            ssrc = p.sx + (size_t) min(mt * (BM / 4) + lane, p.MF * 4 - 1) * p.n_blk * 4;
-            sstep = 16;
+            ssrc = p.sx + sx_group_index(mt, lane, p.MF, p.n_blk, 0);
+            sstep = 4 * sizeof(float);
         } else {
-            ssrc = p.sw + (size_t) nt * BN + 4 * (lane - 32);
+            ssrc = p.sw + sw_index(0, p.NP, nt * BN + 4 * (lane - 32));
             sstep = (size_t) p.NP * sizeof(float);
         }
         v4f rv[4][4];                                // residual rows (RES)
@@ -2225,7 +2182,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
         // (never stored). Columns past N read the last 4 columns (never stored).
         auto load_res = [&](int m0) {
             const int row0 = mt * BM + wm * 64;
-            const uint32_t col = (uint32_t) min(ncol, p.N - 4);
+            const uint32_t col = (uint32_t) clamp_col4(ncol, p.N);
             if (row0 + 64 <= p.T) {
                 const uint32_t lo = (uint32_t) rrow * (uint32_t) p.N + col;
 #pragma unroll
@@ -2238,7 +2195,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
                 for (int mi = m0; mi < m0 + 2; ++mi)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const int t = min(row0 + mi * 16 + 4 * q + rrow, p.T - 1);
+                        const int t = clamp_row(row0 + mi * 16 + 4 * q + rrow, p.T);
                         rv[mi][q] = *reinterpret_cast<const v4f *>(p.res + (size_t) t * p.N + col);
                     }
             }
@@ -2252,20 +2209,20 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
             // block 0: the tile's first three k-steps were loaded under the previous tile; the
             // previous tile's output stores went out after them, so wait for everything
             if (B > 0) arrive(0); else { wait_vm<0>(); lds_barrier(); }
-            issue(cur, 4 * B + 3, 3);
+            prefetch(B, 0, last_tag);
             if (wave == 0) dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, ring + 3 * SLOT + SLOT_AB);
             mma(0, true);
             // k-step 4B + 1 (slot 1)
             if (B > 0) arrive(1); else lds_barrier();
-            if (last) issue(nxt, 0, 0); else issue(cur, 4 * B + 4, 0);
+            prefetch(B, 1, last_tag);
             mma(1, false);
             // k-step 4B + 2 (slot 2)
             if (B > 0) arrive(2); else lds_barrier();
-            if (last) issue(nxt, 1, 1); else issue(cur, 4 * B + 5, 1);
+            prefetch(B, 2, last_tag);
             mma(2, false);
             // k-step 4B + 3 (slot 3, with the block's scales)
             arrive(3);
-            if (last) issue(nxt, 2, 2); else issue(cur, 4 * B + 6, 2);
+            prefetch(B, 3, last_tag);
             mma(3, false);
             if (RES && last) load_res(0);
 
@@ -2300,20 +2257,20 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
         // rows of 256 bytes per instruction and store whole lines.
         lds_barrier();
         const out_map om = out_of(p, ncol);
-        float * stg = reinterpret_cast<float *>(ring + 3 * SLOT + wave * 4352);
+        float * stg = reinterpret_cast<float *>(ring + 3 * SLOT + wave * STAGE_BYTES);
         const int trow = lane & 15, tcol = 4 * (lane >> 4);
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni) {
                 const v4f y = { f[mi][ni][0], f[mi][ni][1], f[mi][ni][2], f[mi][ni][3] };
-                *reinterpret_cast<v4f *>(stg + trow * 68 + 16 * ni + tcol) = y;
+                *reinterpret_cast<v4f *>(stg + trow * STAGE_PITCH + 16 * ni + tcol) = y;
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int row = 4 * q + rrow;
-                v4f y = *reinterpret_cast<const v4f *>(stg + row * 68 + rcol);
+                v4f y = *reinterpret_cast<const v4f *>(stg + row * STAGE_PITCH + rcol);
                 const int t = tbase + mi * 16 + row;
                 if (t < p.T && col_ok) {
                     if (RES) y = rv[mi][q] + y;
@@ -2330,41 +2287,23 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
 // GEMMs for few rows: latency-bound, so operands go straight to registers
 // ---------------------------------------------------------------------------
 
-constexpr int SDT = 2;                     // activation fragments (16 tokens each) per wave
-#ifndef NXG_SMALL_DEPTH4
-#define NXG_SMALL_DEPTH4 4                 // k-steps in flight per wave of the 32 x 64 pieces
-#endif
-// k-steps in flight per wave: two 256-input blocks for 32 x 32 pieces, one for 32 x 64
-// pieces (whose 6 fragments per k-step would otherwise need more than 256 registers)
-template <int FN> constexpr int small_depth() { return FN == 2 ? 8 : NXG_SMALL_DEPTH4; }
-constexpr int SNB_MAX = 16;                // 256-input blocks (n_in <= 4096): sw kept in LDS
-#ifndef NXG_SMALL_MAX_WAVES_PER_CU
-#define NXG_SMALL_MAX_WAVES_PER_CU 4       // gemm_small while its waves number at most this many per CU
-#endif
-#ifndef NXG_RELU2_SMALL_MAX_WAVES_PER_CU
-#define NXG_RELU2_SMALL_MAX_WAVES_PER_CU 6 // gemm_relu2_small likewise
-#endif
-#ifndef NXG_SMALL_FN
-#define NXG_SMALL_FN 0                     // weight fragments per wave of gemm_small (0: chosen per launch)
-#endif
-
 // sw of blocks 0 .. n_blk - 1 for the nw features n0 .. n0 + nw - 1 into LDS, sl[B * nw + c].
 // nw divides 256 and n0 is a multiple of nw, so the rows exist (NP is a multiple of 256).
 template <int NW>
 __device__ __forceinline__ void small_sw_fill(const gemm_params & p, int n0, float * sl) {
     for (int i = threadIdx.x; i < p.n_blk * (NW / 4); i += blockDim.x) {
         const int B = i / (NW / 4), c = (i - B * (NW / 4)) * 4;
-        *reinterpret_cast<v4f *>(sl + B * NW + c) = *reinterpret_cast<const v4f *>(p.sw + (size_t) B * p.NP + n0 + c);
+        *reinterpret_cast<v4f *>(sl + B * NW + c) = *reinterpret_cast<const v4f *>(p.sw + sw_index(B, p.NP, n0 + c));
     }
 }
 
-// One wave's 32 x 16FN piece: tokens of fragment rows fr0, fr0 + 1, features of weight
+// One wave's 32 x 16FN piece: tokens of fragment rows 2mt, 2mt + 1, features of weight
 // fragment rows nr0 .. nr0 + FN - 1. Per k-step the wave loads its 2 + FN fragments
 // (1 KiB each, one dwordx4 per lane, already in MFMA operand order) from global memory
 // straight into registers, D k-steps ahead, so that it keeps that many k-steps of
 // loads in flight however little it computes per k-step. The MFMA operands, the lane
 // layout of the accumulators and the per-block epilogue f = fma((float) s * sx[t], sw[n], f)
-// are those of gemm_kernel: f[j][i][r] is token 16(fr0 + j) + lane % 16, feature
+// are those of gemm_kernel: f[j][i][r] is token 16(2mt + j) + lane % 16, feature
 // 16(nr0 + i) + 4(lane / 16) + r. sx is loaded one block ahead; sw comes from LDS,
 // swl[B * PITCH + 16 i + 4(lane / 16)], written by fill() once the first k-steps' loads
 // are in flight (so that its wait for its own loads costs no extra round trip) and
@@ -2373,10 +2312,10 @@ __device__ __forceinline__ void small_sw_fill(const gemm_params & p, int n0, flo
 // (n_in % 256 == 0) no k-step is loaded twice; otherwise the last block has fewer than
 // 4 k-steps and refills past the last k-step re-read it.
 template <int FN, bool K256, int PITCH, typename Fill, typename Last>
-__device__ __forceinline__ void small_piece(const gemm_params & p, int fr0, int nr0, const float * swl,
+__device__ __forceinline__ void small_piece(const gemm_params & p, int mt, int nr0, const float * swl,
                                             float (&f)[SDT][FN][4], Fill fill, Last last) {
     constexpr int NF = SDT + FN;           // fragments per k-step
-    constexpr int D = small_depth<FN>();
+    constexpr int D = small_depth(FN);
     static_assert(D == 4 || D == 8, "k-steps in flight: one or two blocks");
     const int lane = threadIdx.x & 63;
     const int nb = p.n_blk;
@@ -2389,7 +2328,7 @@ __device__ __forceinline__ void small_piece(const gemm_params & p, int fr0, int 
     const int8_t * base[NF];               // fragment rows, uniform
 #pragma unroll
     for (int j = 0; j < SDT; ++j) {
-        fr[j] = min(fr0 + j, p.MF - 1);
+        fr[j] = small_a_frag(mt, j, p.MF);
         base[j] = p.a + fr[j] * frow;
     }
 #pragma unroll
@@ -2411,7 +2350,7 @@ __device__ __forceinline__ void small_piece(const gemm_params & p, int fr0, int 
 #pragma unroll
         for (int j = 0; j < SDT; ++j) {
             const int t = fr[j] * 16 + (lane & 15);
-            d[j] = p.sx[((size_t) (t >> 2) * nb + B) * 4 + (t & 3)];
+            d[j] = p.sx[sx_index(t, nb, B)];
         }
     };
 
@@ -2521,7 +2460,7 @@ __global__ __launch_bounds__(64) void gemm_small(gemm_params p) {
     __shared__ __attribute__((aligned(16))) float swl[SNB_MAX * 16 * FN];
     const int lane = threadIdx.x;
     const int mt = blockIdx.x / p.n_nt, nt = blockIdx.x - mt * p.n_nt;
-    const int fr0 = mt * SDT, nr0 = nt * FN;
+    const int fr0 = mt * SDT, nr0 = w_frag(nt, 16 * FN, 0);
     float f[SDT][FN][4];
     // The residual of this lane's outputs, loaded at the start of the last block; rows
     // and features past the output read row T - 1 / feature N - 4 (never stored).
@@ -2532,13 +2471,13 @@ __global__ __launch_bounds__(64) void gemm_small(gemm_params p) {
             for (int j = 0; j < SDT; ++j)
 #pragma unroll
                 for (int i = 0; i < FN; ++i) {
-                    const int t = min((fr0 + j) * 16 + (lane & 15), p.T - 1);
-                    const int n = min((nr0 + i) * 16 + 4 * (lane >> 4), p.N - 4);
+                    const int t = clamp_row((fr0 + j) * 16 + (lane & 15), p.T);
+                    const int n = clamp_col4((nr0 + i) * 16 + 4 * (lane >> 4), p.N);
                     rv[j][i] = *reinterpret_cast<const v4f *>(p.res + (size_t) t * p.N + n);
                 }
         }
     };
-    small_piece<FN, K256, 16 * FN>(p, fr0, nr0, swl, f, [&] { small_sw_fill<16 * FN>(p, nr0 * 16, swl); }, load_res);
+    small_piece<FN, K256, 16 * FN>(p, mt, nr0, swl, f, [&] { small_sw_fill<16 * FN>(p, nr0 * 16, swl); }, load_res);
 
     // out[t][n .. n + 3] = (res +) f: 16 bytes per lane and fragment pair.
 #pragma unroll
@@ -2560,9 +2499,6 @@ __global__ __launch_bounds__(64) void gemm_small(gemm_params p) {
 // ---------------------------------------------------------------------------
 // Wide GEMM with the relu^2 -> int8 output: 128 x 256 tiles, n_in % 256 == 0
 // ---------------------------------------------------------------------------
-
-constexpr int WSLOT = (BM / 16 + WBN / 16) * FRAG;   // 24 KiB: 8 A + 16 B fragments
-constexpr int WSCALE = 4 * (BM + WBN);               // sx of 128 rows, then sw of 256 columns
 
 // Across the four 16-lane rows of a wave: lane l gets the maximum of lanes
 // l % 16 + 16 r, r = 0..3 (values without NaN).
@@ -2621,12 +2557,12 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
         const int8_t * w1;
     };
     auto rows_of = [&](int i) {                      // tile i of the walk (clamped)
-        const int tile = walk.tile(min(i, walk.count - 1));
+        const int tile = walk.tile_clamped(i);
         const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
         frag_rows r;
-        r.a = uniform_ptr(p.a + (size_t) min(mt * (BM / 16) + wave, p.MF - 1) * frow);
-        r.w0 = uniform_ptr(p.w + (size_t) (nt * (WBN / 16) + wave) * frow);
-        r.w1 = uniform_ptr(p.w + (size_t) (nt * (WBN / 16) + wave + 8) * frow);
+        r.a = uniform_ptr(p.a + (size_t) a_frag(mt, wave, p.MF) * frow);
+        r.w0 = uniform_ptr(p.w + (size_t) w_frag(nt, WBN, wave) * frow);
+        r.w1 = uniform_ptr(p.w + (size_t) w_frag(nt, WBN, wave + 8) * frow);
         return r;
     };
     // k-step ks of a tile into ring slot j: A fragment w, B fragments w and w + 8.
@@ -2673,16 +2609,22 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
         const int tile = walk.tile(it);
         const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
         const frag_rows cur = rows_of(it), nxt = rows_of(it + 1);
+        // the load that k-step j of block B issues (ring_prefetch: this tile's k-step
+        // 4B + 3 + j, or in the last block the next tile's k-step j - 1)
+        auto prefetch = [&](int B, int j, auto last_tag) {
+            const ring_load l = ring_prefetch(it, B, j, decltype(last_tag)::value);
+            issue(l.pos == it ? cur : nxt, l.ks, l.slot);
+        };
         // Scale loads of block B (B * sstep bytes on): wave 0 lane l < 32 the sx of row
         // group l, wave 0 lane l >= 32 the sw of columns 4(l-32)..+3, wave 1 lane l < 32
         // the sw of columns 128 + 4l..+3; lane l lands at scl + 16 l (+ 1024 on wave 1).
         const float * ssrc;
         size_t sstep;
         if (wave == 0 && lane < 32) {
-            ssrc = p.sx + (size_t) min(mt * (BM / 4) + lane, p.MF * 4 - 1) * p.n_blk * 4;
-            sstep = 16;
+            ssrc = p.sx + sx_group_index(mt, lane, p.MF, p.n_blk, 0);
+            sstep = 4 * sizeof(float);
         } else {
-            ssrc = p.sw + (size_t) nt * WBN + (wave == 0 ? 4 * (lane - 32) : 128 + 4 * lane);
+            ssrc = p.sw + sw_index(0, p.NP, nt * WBN + (wave == 0 ? 4 * (lane - 32) : 128 + 4 * lane));
             sstep = (size_t) p.NP * sizeof(float);
         }
         const int tbase = mt * BM + wm * 64;
@@ -2691,7 +2633,7 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
             constexpr bool last = decltype(last_tag)::value;
             // k-step 4B (slot 0). In block 0 k-steps 0..2 are already in LDS.
             if (B > 0) arrive(0); else lds_barrier();
-            issue(cur, 4 * B + 3, 3);
+            prefetch(B, 0, last_tag);
             if (wave == 0) {
                 dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl);
             } else if (wave == 1 && lane < 32) {
@@ -2700,15 +2642,15 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
             mma(0, true);
             // k-step 4B + 1 (slot 1)
             if (B > 0) arrive(1); else lds_barrier();
-            if (last) issue(nxt, 0, 0); else issue(cur, 4 * B + 4, 0);
+            prefetch(B, 1, last_tag);
             mma(1, false);
             // k-step 4B + 2 (slot 2)
             if (B > 0) arrive(2); else lds_barrier();
-            if (last) issue(nxt, 1, 1); else issue(cur, 4 * B + 5, 1);
+            prefetch(B, 2, last_tag);
             mma(2, false);
             // k-step 4B + 3 (slot 3); the block's scales arrive with it
             arrive(3);
-            if (last) issue(nxt, 2, 2); else issue(cur, 4 * B + 6, 2);
+            prefetch(B, 3, last_tag);
             mma(3, false);
 
             // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
@@ -2786,9 +2728,9 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                 const int rf = mt * (BM / 16) + wm * 4 + mi, kf = nt * (WBN / 64) + wn;
                 if (rf < p.MF) {
                     if (kf < p.KSo) {
-                        *reinterpret_cast<v4i *>(p.qo + ((size_t) rf * p.KSo + kf) * FRAG + lane * 16) = v4i{d[0], d[1], d[2], d[3]};
+                        *reinterpret_cast<v4i *>(p.qo + qo_byte(rf, p.KSo, kf, lane)) = v4i{d[0], d[1], d[2], d[3]};
                     }
-                    if (wn == 0 && lane < 16) p.sxo[((size_t) (t >> 2) * p.n_nt + nt) * 4 + (t & 3)] = scale;
+                    if (wn == 0 && lane < 16) p.sxo[sxo_index(t, p.n_nt, nt)] = scale;
                 }
             }
         }
@@ -2809,9 +2751,9 @@ __global__ __launch_bounds__(256) void gemm_relu2_small(gemm_params p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int mt = blockIdx.x / p.n_nt, nt = blockIdx.x - mt * p.n_nt;
-    const int fr0 = mt * SDT, nr0 = nt * (WBN / 16) + wave * 4;
+    const int fr0 = mt * SDT, nr0 = w_frag(nt, WBN, 4 * wave);
     float f[SDT][4][4];
-    small_piece<4, true, WBN>(p, fr0, nr0, swl + wave * 64, f, [&] { small_sw_fill<WBN>(p, nt * WBN, swl); }, [] {});
+    small_piece<4, true, WBN>(p, mt, nr0, swl + wave * 64, f, [&] { small_sw_fill<WBN>(p, nt * WBN, swl); }, [] {});
 
     // relu(f)^2 in place: f > 0 ? f : 0 (a NaN gives 0), then r * r.
 #pragma unroll
@@ -2861,9 +2803,9 @@ __global__ __launch_bounds__(256) void gemm_relu2_small(gemm_params p) {
         const int rf = fr0 + j, kf = nt * (WBN / 64) + wave;
         if (rf < p.MF) {
             if (kf < p.KSo) {
-                *reinterpret_cast<v4i *>(p.qo + ((size_t) rf * p.KSo + kf) * FRAG + lane * 16) = v4i{d[0], d[1], d[2], d[3]};
+                *reinterpret_cast<v4i *>(p.qo + qo_byte(rf, p.KSo, kf, lane)) = v4i{d[0], d[1], d[2], d[3]};
             }
-            if (wave == 0 && lane < 16) p.sxo[((size_t) (t >> 2) * p.n_nt + nt) * 4 + (t & 3)] = scale;
+            if (wave == 0 && lane < 16) p.sxo[sxo_index(t, p.n_nt, nt)] = scale;
         }
     }
 }
@@ -3541,6 +3483,10 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     }
     int rc = check_device();
     if (rc) return rc;
+    gemm_plan pl;
+    if (!plan_gemm(T, W->n_in, W->n_out, o.sums != nullptr, o.qo != nullptr, device_cus(), pl)) {
+        return fail(NXG_EINVAL, "linear: T=%d too large", T);
+    }
     gemm_params p;
     p.a = q;
     p.sx = sx;
@@ -3551,86 +3497,61 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     p.sums = o.sums;
     p.qo = o.qo;
     p.sxo = o.sxo;
-    p.T = T;
-    p.N = W->n_out;
-    p.NP = W->NP;
-    p.KS = W->KS;
-    p.KSo = ceil_div(p.N, 64);
+    p.T = pl.T;
+    p.N = pl.N;
+    p.NP = pl.NP;
+    p.KS = pl.KS;
+    p.KSo = pl.KSo;
+    p.n_blk = pl.n_blk;
+    p.MF = pl.MF;
+    p.n_mt = pl.n_mt;
+    p.n_nt = pl.n_nt;
+    p.G = pl.G;
     p.n_seg = o.n_seg;
     for (int k = 0, end = 0; k < 4; ++k) {
         if (k < o.n_seg) end += o.seg_cols[k];
         p.seg_end[k] = end;
         p.seg_out[k] = k < o.n_seg ? o.seg_out[k] : nullptr;
     }
-    p.n_blk = W->n_blk;
-    p.MF = ceil_div(T, 16);
-    p.n_mt = ceil_div(T, BM);
+    if (p.NP != W->NP || p.KS != W->KS || p.n_blk != W->n_blk) return fail(NXG_EINVAL, "linear: weight layout mismatch");
     hipStream_t s = (hipStream_t) stream;
-    if (o.qo) {
-        // relu^2 -> int8: 128 x 256 tiles (a whole 256-column block), one workgroup per CU
-        p.n_nt = ceil_div(p.N, WBN);
-        const long long G = (long long) p.n_mt * p.n_nt;
-        if (G > INT32_MAX / 2) return fail(NXG_EINVAL, "linear: T=%d too large", T);
-        p.G = (int) G;
-        const long long G_small = (long long) ceil_div(p.MF, SDT) * p.n_nt;   // 4 waves each
-        if (p.n_blk <= SNB_MAX && 4 * G_small <= (long long) NXG_RELU2_SMALL_MAX_WAVES_PER_CU * device_cus()) {
-            p.n_mt = ceil_div(p.MF, SDT);
-            p.G = (int) G_small;
-            const dim3 grid((unsigned) p.G), block(256);
-            if (o.act_max == 127) gemm_relu2_small<127><<<grid, block, 0, s>>>(p);
-            else                  gemm_relu2_small<63><<<grid, block, 0, s>>>(p);
-            return launch_check("gemm_relu2_small");
-        }
-        const dim3 grid((unsigned) std::min<long long>(G, device_cus())), block(WTHREADS);
+    const dim3 grid((unsigned) pl.grid), block((unsigned) pl.block);
+    const bool res = o.residual != nullptr;
+    switch (pl.kind) {
+    case GEMM_RELU2_SMALL:
+        if (o.act_max == 127) gemm_relu2_small<127><<<grid, block, 0, s>>>(p);
+        else                  gemm_relu2_small<63><<<grid, block, 0, s>>>(p);
+        return launch_check("gemm_relu2_small");
+    case GEMM_RELU2_Q8:
         if (o.act_max == 127) gemm_relu2_q8<127><<<grid, block, 0, s>>>(p);
         else                  gemm_relu2_q8<63><<<grid, block, 0, s>>>(p);
         return launch_check("gemm_relu2_q8");
-    }
-    p.n_nt = ceil_div(p.N, BN);
-    const long long G = (long long) p.n_mt * p.n_nt;
-    if (G > INT32_MAX / 2) return fail(NXG_EINVAL, "linear: T=%d too large", T);
-    p.G = (int) G;
-    // Few rows, one wave per piece: 32 x 32 pieces while they number at most
-    // NXG_SMALL_MAX_WAVES_PER_CU per CU, else 32 x 64 pieces (fewer bytes per output
-    // through each CU) while those do; beyond that the 128 x 128 tiles above, which
-    // read each operand fragment once per tile. (Measured on MI355X at 128..4096 rows.)
-    const long long W2 = (long long) ceil_div(p.MF, SDT) * ceil_div(p.N, 32);
-    const long long W4 = (long long) ceil_div(p.MF, SDT) * ceil_div(p.N, 64);
-    const long long w_max = (long long) NXG_SMALL_MAX_WAVES_PER_CU * device_cus();
-    const int fn = NXG_SMALL_FN ? NXG_SMALL_FN : (W2 <= w_max ? 2 : 4);
-    const long long n_waves = fn == 2 ? W2 : W4;
-    if (!o.sums && p.N % 4 == 0 && p.n_blk <= SNB_MAX && n_waves <= w_max) {
-        p.n_mt = ceil_div(p.MF, SDT);
-        p.n_nt = ceil_div(p.N, 16 * fn);
-        p.G = (int) n_waves;
-        const dim3 grid((unsigned) p.G), block(64);
-        const bool res = o.residual != nullptr;
-        if (fn == 2) {
-            if (res) { if (k256) gemm_small<2, true, true><<<grid, block, 0, s>>>(p); else gemm_small<2, true, false><<<grid, block, 0, s>>>(p); }
-            else     { if (k256) gemm_small<2, false, true><<<grid, block, 0, s>>>(p); else gemm_small<2, false, false><<<grid, block, 0, s>>>(p); }
+    case GEMM_SMALL:
+        if (pl.fn == 2) {
+            if (res) { if (pl.k256) gemm_small<2, true, true><<<grid, block, 0, s>>>(p); else gemm_small<2, true, false><<<grid, block, 0, s>>>(p); }
+            else     { if (pl.k256) gemm_small<2, false, true><<<grid, block, 0, s>>>(p); else gemm_small<2, false, false><<<grid, block, 0, s>>>(p); }
         } else {
-            if (res) { if (k256) gemm_small<4, true, true><<<grid, block, 0, s>>>(p); else gemm_small<4, true, false><<<grid, block, 0, s>>>(p); }
-            else     { if (k256) gemm_small<4, false, true><<<grid, block, 0, s>>>(p); else gemm_small<4, false, false><<<grid, block, 0, s>>>(p); }
+            if (res) { if (pl.k256) gemm_small<4, true, true><<<grid, block, 0, s>>>(p); else gemm_small<4, true, false><<<grid, block, 0, s>>>(p); }
+            else     { if (pl.k256) gemm_small<4, false, true><<<grid, block, 0, s>>>(p); else gemm_small<4, false, false><<<grid, block, 0, s>>>(p); }
         }
         return launch_check("gemm_small");
+    case GEMM_SUMS:
+        if (pl.k256) gemm_kernel<false, true, true><<<grid, block, 0, s>>>(p);
+        else         gemm_kernel<false, true, false><<<grid, block, 0, s>>>(p);
+        return launch_check("gemm_kernel");
+    case GEMM_K256:
+        if (res) gemm_k256<true><<<grid, block, 0, s>>>(p);
+        else     gemm_k256<false><<<grid, block, 0, s>>>(p);
+        return launch_check("gemm_k256");
+    case GEMM_GENERAL:
+        break;
     }
-    // K256: persistent workgroups, two per CU (the LDS ring needs 68 KiB of the 160);
-    // otherwise one workgroup per tile.
-    const int n_wg = (k256 && NXG_WG_PER_CU > 0) ? (int) std::min<long long>(G, (long long) NXG_WG_PER_CU * device_cus())
-                                                 : (int) G;
-    const dim3 grid((unsigned) n_wg), block(NTHREADS);
-    if (o.sums) {
-        if (k256) gemm_kernel<false, true, true><<<grid, block, 0, s>>>(p);
-        else      gemm_kernel<false, true, false><<<grid, block, 0, s>>>(p);
-    } else if (k256 && NXG_WG_PER_CU > 0 && p.N % 4 == 0) {
-        if (o.residual) gemm_k256<true><<<grid, block, 0, s>>>(p);
-        else            gemm_k256<false><<<grid, block, 0, s>>>(p);
-    } else if (o.residual) {
-        if (k256) gemm_kernel<true, false, true><<<grid, block, 0, s>>>(p);
-        else      gemm_kernel<true, false, false><<<grid, block, 0, s>>>(p);
+    if (res) {
+        if (pl.k256) gemm_kernel<true, false, true><<<grid, block, 0, s>>>(p);
+        else         gemm_kernel<true, false, false><<<grid, block, 0, s>>>(p);
     } else {
-        if (k256) gemm_kernel<false, false, true><<<grid, block, 0, s>>>(p);
-        else      gemm_kernel<false, false, false><<<grid, block, 0, s>>>(p);
+        if (pl.k256) gemm_kernel<false, false, true><<<grid, block, 0, s>>>(p);
+        else         gemm_kernel<false, false, false><<<grid, block, 0, s>>>(p);
     }
     return launch_check("gemm_kernel");
 }
