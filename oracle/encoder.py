@@ -7,9 +7,11 @@ TEST INFRASTRUCTURE ONLY: the checker that the GPU encoder (include/nxg_encoder.
 compared against. Only the test suite, the smoke check and the benchmark's CPU-baseline leg
 use it; nothing in the product imports it.
 
-Inputs are decoded tensors: the caller reads the GGUF file and decodes each tensor's blocks
-to float32 (that decoding is the file format's, tested on its own; its parity with ggml's
-to_float is not pinned). From there this module restates everything the reference does:
+Inputs are decoded tensors: from_gguf reads the GGUF file and decodes each tensor's blocks
+to float32 with the oracle's own reader and decoders (ggml_blocks.py, pinned by known-answer
+blocks and against the engine's separately written decoders; their parity with a compiled
+ggml is pinned only up to its block layouts). From there this module restates everything
+the reference does:
 the metadata defaults, the int8 placement rule and build_i8_weight (orc_expand_rows), the
 conv kernels re-laid out one row per tap, and each op of the graph in order.
 
@@ -25,6 +27,7 @@ from typing import Dict, List, Optional, Sequence
 
 import numpy as np
 
+from . import ggml_blocks as gb
 from . import oracle as orc
 
 MIXERS = ("lily", "swa", "attn", "hra")
@@ -109,17 +112,15 @@ class Model:
         self.n_types = self.f["token_type_embeddings.weight"].shape[0] if "token_type_embeddings.weight" in self.f else 0
 
 
-def from_gguf(nxg, path, act_max: int = 127) -> Model:
-    """A Model from a GGUF file, read and block-decoded by the engine package `nxg`
-    (its GGUF reader and to_float codecs)."""
+def from_gguf(path, act_max: int = 127) -> Model:
+    """A Model from a GGUF file, read and block-decoded by the oracle's own GGUF reader and
+    ggml decoders (ggml_blocks.py), not the engine's."""
+    meta, raw = gb.read_gguf(path)
     tensors = {}
-    with nxg.GGUF(path) as g:
-        meta = g.metadata()
-        for t in g.tensors():
-            ne = tuple(int(n) for n in t.ne[:t.n_dims])
-            n = int(np.prod(ne))
-            arr = nxg.dequantize_rows(t.type, g.tensor_bytes(t.name), ne[0], n // ne[0])
-            tensors[t.name] = (t.type, ne, arr.reshape(ne[1], ne[0]) if len(ne) == 2 else arr.reshape(-1))
+    for name, t, ne, data in raw:
+        n = int(np.prod(ne))
+        arr = gb.dequantize(t, data, n)
+        tensors[name] = (t, ne, arr.reshape(ne[1], ne[0]) if len(ne) == 2 else arr.reshape(-1))
     return Model(meta, tensors, act_max)
 
 

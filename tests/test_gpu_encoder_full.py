@@ -63,7 +63,7 @@ def small_models(nxg, synth, enc, tmp_path_factory):
                        block_types=["lily", "swa", "attn", "hra", "lily", "hra"], **cfg)
         path = tmp_path_factory.mktemp("enc") / f"{key}.gguf"
         synth.write_random_model(nxg, path, preset, seed=len(key), dims=d)
-        out[key] = (path, d, enc.from_gguf(nxg, path))
+        out[key] = (path, d, enc.from_gguf(path))
     return out
 
 
@@ -144,7 +144,7 @@ def test_encoder_full_model_1024(nxg, synth, enc, torch, tmp_path):
     with nxg.Encoder(path) as e:
         h, p = e.encode(tok, [1024], pooled=True)
     say("encoder: oracle forward")
-    m = enc.from_gguf(nxg, path)
+    m = enc.from_gguf(path)
     hr, pr = enc.encode(m, tok, [1024])
     cos = np.sum(h.astype(np.float64) * hr, 1) / (np.linalg.norm(h.astype(np.float64), axis=1) * np.linalg.norm(hr, axis=1))
     say(f"encoder: min token cosine {cos.min():.9f}")
@@ -214,7 +214,7 @@ def test_encoder_branches_match_oracle(nxg, synth, enc, torch, tmp_path, variant
     path = tmp_path / f"{variant}.gguf"
     synth.write_random_model(nxg, path, "Q8_0", seed=7, dims=d)
     act_max = 63 if variant == "act63" else 127
-    m = enc.from_gguf(nxg, path, act_max=act_max)
+    m = enc.from_gguf(path, act_max=act_max)
     rng = np.random.default_rng(3)
     cases = [[61]] if variant == "ntk" else [[61], [19, 1, 40]]
     if variant == "ntk":

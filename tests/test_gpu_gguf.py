@@ -7,6 +7,7 @@ import numpy as np
 import pytest
 
 import gguf_writer as W
+from oracle import ggml_blocks as gb
 
 pytestmark = pytest.mark.gpu
 
@@ -35,6 +36,7 @@ def test_linear_from_gguf_matches_oracle(nxg, orc, torch, tmp_path):
     path = tmp_path / "m.gguf"
     W.write_gguf(path, [("general.architecture", W.STRING, "nexterabert")], tensors)
     T = 333
+    ref_tensors = {name: (t, raw) for name, t, _, raw in gb.read_gguf(path)[1]}
     with nxg.GGUF(path) as g:
         dev = g.load_int8_weights()
         assert sorted(dev) == sorted(shapes)
@@ -45,8 +47,10 @@ def test_linear_from_gguf_matches_oracle(nxg, orc, torch, tmp_path):
             x = rng.standard_normal((T, n_in)).astype(np.float32)
             qa = nxg.quantize_rows(torch.from_numpy(x).cuda())
             y = nxg.linear_i8(d, qa).cpu().numpy()
-            E = nxg.expand_weight(ttype, g.tensor_bytes(name), n_in, n_out)
+            # the oracle's side: its own GGUF reader, ggml block decoder and build_i8_weight
+            w_ref, scale_ref, off_ref = orc.expand_rows(
+                gb.dequantize(ref_tensors[name][0], ref_tensors[name][1], n_in * n_out).reshape(n_out, n_in))
             q_ref, sx_ref = orc.quantize_rows(x)
-            y_ref = orc.linear(E.w, E.scale, E.off, q_ref, sx_ref, simd=bool(orc.vnni_flavour()),
+            y_ref = orc.linear(w_ref, scale_ref, off_ref, q_ref, sx_ref, simd=bool(orc.vnni_flavour()),
                                n_threads=orc.default_threads())
             assert (bits(y) == bits(y_ref)).all()

@@ -79,7 +79,7 @@ def model(nxg, tmp_path_factory):
             ("tokenizer.ggml.padding_token_id", W.UINT32, 3), ("tokenizer.ggml.mask_token_id", W.UINT32, 4)]
     path = tmp_path_factory.mktemp("api") / "heads.gguf"
     synth.write_random_model(nxg, path, "Q4_K_M", seed=21, dims=d, extra_metadata=meta, extra_tensors=heads)
-    return path, d, E.from_gguf(nxg, path)
+    return path, d, E.from_gguf(path)
 
 
 @pytest.fixture(scope="module")

@@ -43,7 +43,7 @@ def test_batch_invariance_and_layers(nxg, synth, enc, tmp_path):
     d = tiny_dims(synth, n_types=2)
     path = tmp_path / "tiny.gguf"
     synth.write_random_model(nxg, path, "Q4_K_M", seed=3, dims=d)
-    m = enc.from_gguf(nxg, path)
+    m = enc.from_gguf(path)
     assert m.n_types == 2 and len(m.lin) == 4 * 2 + 6 + 5 + 5 + 8
     rng = np.random.default_rng(0)
     lens = [5, 17, 1, 40]
@@ -75,7 +75,7 @@ def test_zero_residual_writers_leave_the_embedding(nxg, synth, enc, orc, tmp_pat
             t[name] = np.zeros_like(t[name])
     path = tmp_path / "zero.gguf"
     synth.write_random_model(nxg, path, "Q8_0", dims=d, tensors=t)
-    m = enc.from_gguf(nxg, path)
+    m = enc.from_gguf(path)
     tok = np.random.default_rng(1).integers(0, d.n_vocab, 50)
     h, _ = enc.encode(m, tok, [20, 30])
     emb = m.f["embedding.weight"].reshape(-1, d.n_embd)[tok]
