@@ -59,6 +59,17 @@ NXG_API int32_t nxg_encoder_n_token_types(const nxg_encoder * e);
 /* Device memory the context holds: weights, tables and the current work buffers. */
 NXG_API size_t nxg_encoder_device_bytes(const nxg_encoder * e);
 
+/* Caps the work buffers at `bytes` (0: no cap; the default). The work area holds the
+ * activations of the largest batch seen and the attention's score workspace; where the
+ * whole does not fit under the cap or in the device's free memory, the workspace is halved
+ * until it does, down to none (long documents then recompute their scores: same results,
+ * slower). A batch whose activations alone exceed the cap fails with NXG_ENOMEM. No
+ * counterpart in the reference, whose ggml allocator sizes its graph per call. */
+NXG_API int32_t nxg_encoder_set_work_limit(nxg_encoder * e, int64_t bytes);
+
+/* Bytes of attention score workspace in the current work area (0: none, or no pass yet). */
+NXG_API int64_t nxg_encoder_attention_workspace(const nxg_encoder * e);
+
 /* nextera_debug_set_layers (src/nexterabert.cpp:1815-1820): run only the first n_layers
  * blocks and return the residual stream before out_norm (-1: the full model). */
 NXG_API void nxg_encoder_set_layers(nxg_encoder * e, int32_t n_layers);

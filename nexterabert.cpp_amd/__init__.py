@@ -106,6 +106,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_encoder_n_int8": ([P], i32),
         "nxg_encoder_profile": ([P, i32], None),
         "nxg_encoder_profile_read": ([P, P, P, P, P], i32),
+        "nxg_encoder_set_work_limit": ([P, i64], i32),
+        "nxg_encoder_attention_workspace": ([P], i64),
         "nxg_rope_table": ([i32, ctypes.c_float, i32, P, P], i32),
         "nxg_qact_export": ([P, P, i32, i32, i32, P, P, P], i32),
         "nxg_weight_create": ([P, P, i32, i32, ctypes.POINTER(P)], i32),
@@ -1036,6 +1038,16 @@ class Encoder:
                                                        ctypes.byref(n)), "encoder_profile_read")
         return {"passes": int(n.value), "wall_ms": wall.value, "device_ms": dev.value,
                 "kinds": dict(zip(self.PROFILE_KINDS, list(kinds)))}
+
+    def set_work_limit(self, nbytes: int) -> None:
+        """nxg_encoder_set_work_limit: cap the work buffers (0: no cap); the attention's score
+        workspace shrinks, down to none, to fit."""
+        _check(load_library().nxg_encoder_set_work_limit(self._h, int(nbytes)), "encoder_set_work_limit")
+
+    @property
+    def attention_workspace(self) -> int:
+        """Bytes of attention score workspace in the current work area."""
+        return int(load_library().nxg_encoder_attention_workspace(self._h))
 
     def set_layers(self, n_layers: int) -> None:
         """Run only the first n_layers blocks, returning the residual stream (-1: all)."""

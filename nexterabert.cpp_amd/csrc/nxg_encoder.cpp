@@ -154,6 +154,7 @@ struct nxg_encoder {
     // in the longest one
     void * work = nullptr;
     size_t work_bytes = 0;
+    int64_t work_limit = 0;                    // nxg_encoder_set_work_limit (0: none)
     int64_t cap_T = -1, cap_TB = -1, cap_seqs = -1, cap_keys = -1;
     float * x[2] = {};
     float * F[8] = {};                         // [T][C]
@@ -275,8 +276,9 @@ int32_t nxg_encoder::ensure_work(int64_t nT, int64_t nTB, int64_t n_seqs, int64_
     const int64_t T_ = std::max(nT, cap_T), TB_ = std::max(nTB, cap_TB), S_ = std::max(n_seqs, cap_seqs);
     const int64_t K_ = std::max(n_keys, cap_keys);
     // attention over at most K_ keys on T_ rows (HRA's block rows: fewer rows and keys, less space)
-    const int64_t ws = nxg_attention_workspace_bytes((int32_t) T_, hp.n_head, hp.n_kv_head, (int32_t) K_);
-    if (ws < 0) return (int32_t) ws;
+    const int64_t ws_full = nxg_attention_workspace_bytes((int32_t) T_, hp.n_head, hp.n_kv_head, (int32_t) K_);
+    if (ws_full < 0) return (int32_t) ws_full;
+    int64_t ws = ws_full;
     const int C = hp.n_embd, KV = hp.n_kv_head * hp.head_dim, R = std::max(hp.lily_rank, 32), I = hp.n_inter;
     auto layout = [&](char * base) {
         carver c{base};
@@ -306,18 +308,35 @@ int32_t nxg_encoder::ensure_work(int64_t nT, int64_t nTB, int64_t n_seqs, int64_
         c.take(attn_ws, (size_t) ws);
         return c.off;
     };
-    const size_t bytes = layout(nullptr);
     if (work) {
         NXG_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
         release(work);
         work = nullptr;
         work_bytes = 0;
     }
+    // nxg_attention_ws runs with any workspace: fewer score slots, or none (the recomputing
+    // kernel). Where the work area does not fit (the device's memory, or work_limit), the
+    // attention's share is halved until it does, down to nothing.
     void * p = nullptr;
-    const hipError_t e = hipMalloc(&p, bytes);
+    size_t bytes = layout(nullptr);
+    hipError_t e = hipErrorOutOfMemory;
+    for (;;) {
+        if (work_limit <= 0 || (int64_t) bytes <= work_limit) {
+            e = hipMalloc(&p, bytes);
+            if (e == hipSuccess) break;
+            (void) hipGetLastError();          // the refused allocation is not a later launch's error
+        }
+        if (ws == 0) break;
+        ws = ws > (int64_t) (64 << 20) ? ws / 2 : 0;
+        bytes = layout(nullptr);
+    }
     if (e != hipSuccess) {
         cap_T = cap_TB = cap_seqs = cap_keys = -1;
         attn_ws_bytes = 0;
+        if (work_limit > 0 && (int64_t) bytes > work_limit) {
+            return fail(NXG_ENOMEM, "encoder: %zu bytes of work memory for %lld rows exceed the limit of %lld", bytes,
+                        (long long) T_, (long long) work_limit);
+        }
         return fail(NXG_ENOMEM, "encoder: %zu bytes of work memory for %lld rows: %s", bytes, (long long) T_,
                     hipGetErrorString(e));
     }
@@ -922,6 +941,24 @@ void nxg_encoder_set_layers(nxg_encoder * e, int32_t n_layers) {
 }
 double nxg_encoder_last_ms(const nxg_encoder * e) { return e ? e->last_ms : 0.0; }
 int32_t nxg_encoder_n_int8(const nxg_encoder * e) { return e ? e->n_int8 : 0; }
+
+int32_t nxg_encoder_set_work_limit(nxg_encoder * e, int64_t bytes) {
+    if (!e) return fail(NXG_EINVAL, "encoder_set_work_limit: null context");
+    if (bytes < 0) return fail(NXG_EINVAL, "encoder_set_work_limit: %lld bytes", (long long) bytes);
+    e->work_limit = bytes;
+    if (e->work) {
+        // the next pass sizes the work area again under the new limit
+        NXG_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        release(e->work);
+        e->work = nullptr;
+        e->work_bytes = 0;
+        e->attn_ws_bytes = 0;
+        e->cap_T = e->cap_TB = e->cap_seqs = e->cap_keys = -1;
+    }
+    return NXG_OK;
+}
+
+int64_t nxg_encoder_attention_workspace(const nxg_encoder * e) { return e ? e->attn_ws_bytes : 0; }
 
 void nxg_encoder_profile(nxg_encoder * e, int32_t enable) {
     if (!e) return;

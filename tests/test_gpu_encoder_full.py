@@ -102,6 +102,33 @@ def test_encoder_long_document_matches_oracle(nxg, enc, torch, small_models):
     assert (bits(p) == bits(pr)).all()
 
 
+def test_encoder_work_limit_shrinks_the_attention_workspace(nxg, enc, torch, small_models):
+    """nxg_encoder_set_work_limit: under a cap that leaves no room for the score workspace the
+    long document's attention recomputes its scores, with the same bits; a cap below the
+    activations fails with NXG_ENOMEM and leaves the context usable."""
+    path, d, m = small_models["c128_q4km"]
+    say("encoder work limit, one 2,700-token document")
+    tok = np.random.default_rng(27).integers(0, d.n_vocab, 2700).astype(np.int32)
+    with nxg.Encoder(path) as e:
+        weights = e.device_bytes
+        h0, p0 = e.encode(tok, [2700], pooled=True)
+        ws, work = e.attention_workspace, e.device_bytes - weights
+        assert ws > 0 and work > ws
+        e.set_work_limit(work - ws + 4096)           # the activations (and alignment), no room for a score slot
+        h1, p1 = e.encode(tok, [2700], pooled=True)
+        assert e.attention_workspace == 0 and e.device_bytes - weights <= work - ws + 4096
+        assert (bits(h1) == bits(h0)).all() and (bits(p1) == bits(p0)).all()
+        e.set_work_limit(work - ws - (1 << 20))      # not even the activations
+        with pytest.raises(Exception, match="exceed the limit"):
+            e.encode(tok, [2700], pooled=True)
+        e.set_work_limit(0)
+        h2, p2 = e.encode(tok, [2700], pooled=True)
+        assert e.attention_workspace == ws
+        assert (bits(h2) == bits(h0)).all() and (bits(p2) == bits(p0)).all()
+    hr, pr = enc.encode(m, tok, [2700])
+    assert (bits(h0) == bits(hr)).all() and (bits(p0) == bits(pr)).all()
+
+
 def test_encoder_batch_invariance_and_layers(nxg, enc, torch, small_models):
     path, d, m = small_models["c256_q8"]
     say("encoder batch invariance, set_layers, device entry point")
