@@ -8,6 +8,12 @@ for p in (ROOT, ROOT / "tests"):
     if str(p) not in sys.path:
         sys.path.insert(0, str(p))
 
+# The engine package (directory nexterabert.cpp_amd/) as the module nexterabert_cpp_amd, so
+# that test modules can import its submodules (gguf_writer, synth, encoder) by name.
+import __graft_entry__  # noqa: E402
+
+__graft_entry__.load_package()
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")

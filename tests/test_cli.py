@@ -7,7 +7,7 @@ from pathlib import Path
 
 import pytest
 
-import gguf_writer as W
+from nexterabert_cpp_amd import gguf_writer as W
 
 ROOT = Path(__file__).resolve().parent.parent
 

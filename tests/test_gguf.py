@@ -1,4 +1,4 @@
-"""CPU tests of the GGUF reader (include/nxg_gguf.h) on files written by tests/gguf_writer.py
+"""CPU tests of the GGUF reader (include/nxg_gguf.h) on files written by nexterabert.cpp_amd/gguf_writer.py
 from the published format: every metadata value type, tensor table and bytes, alignment,
 the int8 placement of the reference's loader, and malformed files. No GPU work."""
 from __future__ import annotations
@@ -8,7 +8,7 @@ import struct
 import numpy as np
 import pytest
 
-import gguf_writer as W
+from nexterabert_cpp_amd import gguf_writer as W
 
 
 def f16_bytes(x):

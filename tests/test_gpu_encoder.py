@@ -16,7 +16,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-import gguf_writer as W
+from nexterabert_cpp_amd import gguf_writer as W
 
 pytestmark = pytest.mark.gpu
 

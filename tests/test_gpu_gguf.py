@@ -6,7 +6,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-import gguf_writer as W
+from nexterabert_cpp_amd import gguf_writer as W
 from oracle import ggml_blocks as gb
 
 pytestmark = pytest.mark.gpu

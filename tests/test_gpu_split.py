@@ -1,8 +1,8 @@
 """GPU: one launch of a weight fused along n_out from several projections of the same input
 (nxg_linear_i8_rows_split) writes each projection's columns to its own buffer with the bits
-of a separate linear of that projection (tests/test_gpu_parity.py pins those against the
-oracle), through the few-row kernels and the 128 x 128 tiles; bad segment layouts are
-refused before any launch."""
+of a separate linear of that projection and of the oracle's linear (every row up to 1,024
+rows, else a sample around the tile boundaries and at random), through the few-row kernels
+and the 128 x 128 tiles; bad segment layouts are refused before any launch."""
 from __future__ import annotations
 
 import numpy as np
@@ -59,8 +59,15 @@ SPLITS = [
 ]
 
 
+def rows_checked(rng, T):
+    if T <= 1024:
+        return np.arange(T)
+    fixed = [0, 1, 127, 128, 255, 256, T - 129, T - 128, T - 2, T - 1]
+    return np.unique(np.concatenate([fixed, rng.choice(T, 200, replace=False)]))
+
+
 @pytest.mark.parametrize("T,n_in,cols", SPLITS)
-def test_split_equals_separate_linears(nxg, torch, dev, T, n_in, cols):
+def test_split_equals_separate_linears(nxg, orc, torch, dev, T, n_in, cols):
     say(f"linear_split T={T} n_in={n_in} cols={cols}")
     rng = np.random.default_rng(T + n_in + len(cols))
     ws = parts(nxg, rng, n_in, cols)
@@ -70,10 +77,15 @@ def test_split_equals_separate_linears(nxg, torch, dev, T, n_in, cols):
     outs = [torch.full((T, c), float("nan"), device="cuda") for c in cols]
     nxg.linear_i8_split(fused, qa, cols, outs=outs)
     torch.cuda.synchronize()
+    pick = rows_checked(rng, T)
+    q_ref, sx_ref = orc.quantize_rows(x.cpu().numpy()[pick])
     for k, w in enumerate(ws):
         ref = nxg.linear_i8(nxg.DeviceWeight(w), qa)
         torch.cuda.synchronize()
-        assert (bits(outs[k].cpu().numpy()) == bits(ref.cpu().numpy())).all(), f"segment {k}"
+        got = outs[k].cpu().numpy()
+        assert (bits(got) == bits(ref.cpu().numpy())).all(), f"segment {k}"
+        y_ref = orc.linear(w.w, w.scale, w.off, q_ref, sx_ref, simd=bool(orc.vnni_flavour()), n_threads=8)
+        assert (bits(got[pick]) == bits(y_ref)).all(), f"segment {k} against the oracle"
 
 
 def test_split_refusals(nxg, torch, dev):
