@@ -2679,14 +2679,15 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
         // waits for).
         wait_vm<0>();
         {
-            // relu(f)^2 in place: f > 0 ? f : 0 (a NaN gives 0), then r * r.
+            // relu(f)^2 in place: max(f, 0) (maxNum: a NaN gives 0; f is never a signalling
+            // NaN, being an fma result), then r * r -- the bits of (f > 0 ? f : 0)^2.
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float x = f[mi][ni][r] > 0.0f ? f[mi][ni][r] : 0.0f;
+                        const float x = fmaxf(f[mi][ni][r], 0.0f);
                         f[mi][ni][r] = x * x;
                     }
             // Row maxima (values >= 0, no NaN: the reference's MAXPS fold is the plain
@@ -2703,12 +2704,25 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                 if (lane < 16) am[(wm * 64 + mi * 16 + lane) * 4 + wn] = m;
             }
             lds_barrier();
+            // Row maxima of this lane's 4 row groups; with every one of the wave finite (the
+            // usual case) each value f * inv lies in [0, ACT_MAX + 1/2), so CVTPS2DQ and the
+            // saturating packs reduce to round-to-nearest-even, which v_cvt_pk_u8_f32 does
+            // while packing the byte. An infinite maximum takes quant1 (NaN -> 0x80000000).
+            float amx[4];
+            bool fin = true;
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi) {
                 const int t = tbase + mi * 16 + (lane & 15);
                 const v4f a4 = *reinterpret_cast<const v4f *>(am + (wm * 64 + mi * 16 + (lane & 15)) * 4);
+                amx[mi] = t < p.T ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
+                fin = fin && amx[mi] < INFINITY;
+            }
+            const bool fast = __builtin_amdgcn_ballot_w64(!fin) == 0;
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                const int t = tbase + mi * 16 + (lane & 15);
                 const bool row_ok = t < p.T;
-                const float amax = row_ok ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
+                const float amax = amx[mi];
                 const float scale = amax / (float) ACT_MAX;
                 const float inv = amax > 0.0f ? (float) ACT_MAX / amax : 0.0f;
                 // column 16ni + 4(lane/16) + r of the wave's 64: byte r of d[ni]
@@ -2716,12 +2730,18 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
 #pragma unroll
                 for (int ni = 0; ni < 4; ++ni) {
                     const int n = nt * WBN + wn * 64 + ni * 16 + 4 * (lane >> 4);
-                    int packed = 0;
-                    if (row_ok && n < p.N) {
+                    int packed;
+                    if (fast) {
+                        unsigned u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][0] * inv, 0, 0u);
+                        u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][1] * inv, 1, u);
+                        u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][2] * inv, 2, u);
+                        u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][3] * inv, 3, u);
+                        packed = (int) u;
+                    } else {
                         packed = (quant1<ACT_MAX>(f[mi][ni][0], inv) & 0xff) | ((quant1<ACT_MAX>(f[mi][ni][1], inv) & 0xff) << 8)
                                | ((quant1<ACT_MAX>(f[mi][ni][2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(f[mi][ni][3], inv) & 0xff) << 24);
                     }
-                    d[ni] = packed;
+                    d[ni] = row_ok && n < p.N ? packed : 0;
                 }
                 // lane c + 16 j now gets columns 16 j + 0..15 of row c: one fragment lane
                 rows_transpose(d);

@@ -149,6 +149,35 @@ def test_linear_relu2_q8_packed_batch(nxg, orc, torch, dev):
     assert (bits(sa_m[s0:s1]) == bits(sc_m)).all() and sa_m.shape[1] == n_blk
 
 
+def test_linear_relu2_q8_overflowing_rows(nxg, orc, torch, dev):
+    """Rows whose fp32 sums overflow: relu^2 gives +Inf, the row maximum is infinite and the
+    quantization takes the reference's NaN path (x * 0 for the infinite values). Waves that
+    hold such a row use the full CVTPS2DQ statement, the others the packed conversion; both
+    against the oracle chain, on 128 x 256 tiles (T >= 8192 keeps the many-row kernel)."""
+    say("linear_relu2_q8 with overflowing rows")
+    rng = np.random.default_rng(11)
+    T, n_in, n_out = 8200, 1024, 512
+    x = rng.standard_normal((T, n_in)).astype(np.float32)
+    x[5, :] *= np.float32(3e37)          # every block of the row: sums reach the fp32 limit
+    x[4100, ::3] = np.float32(-2e38)     # a row of mixed signs in another tile
+    x[8199, 17] = np.float32(3e38)       # the last, partial row tile
+    W = make_weight(nxg, rng, n_in, n_out, std=0.05)
+    qa, q_ref, sx_ref = quant(nxg, torch, orc, x)
+    dw = nxg.DeviceWeight(W)
+    y_ref = orc.linear(W.w, W.scale, W.off, q_ref, sx_ref, simd=bool(orc.vnni_flavour()),
+                       n_threads=orc.default_threads())
+    r = orc.relu2(y_ref)
+    assert np.isinf(r).any(), "the case needs an infinite relu^2 value"
+    for act_max in (127, 63):
+        fused = nxg.linear_i8_relu2_q8(dw, qa, act_max)
+        r_ref, rsx_ref = orc.quantize_rows(r, act_max)
+        u8, sx = nxg.export_qact(fused)
+        torch.cuda.synchronize()
+        assert (u8.cpu().numpy() == r_ref).all(), f"act_max={act_max}"
+        s = sx.cpu().numpy()
+        assert ((bits(s) == bits(rsx_ref)) | (np.isnan(s) & np.isnan(rsx_ref))).all(), f"act_max={act_max}"
+
+
 @pytest.mark.parametrize("n_in_fc", [1024, 96])
 def test_builder_mlp(nxg, orc, torch, dev, n_in_fc):
     """x + c_proj(relu(c_fc(h))^2): fused when n_in % 256 == 0, fp32 then quantize otherwise."""
