@@ -2748,7 +2748,14 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                 const int rf = mt * (BM / 16) + wm * 4 + mi, kf = nt * (WBN / 64) + wn;
                 if (rf < p.MF) {
                     if (kf < p.KSo) {
-                        *reinterpret_cast<v4i *>(p.qo + qo_byte(rf, p.KSo, kf, lane)) = v4i{d[0], d[1], d[2], d[3]};
+                        // device scope (sc1): the int8 rows go past L2, where they would evict the
+                        // activation row tile that this row's other column tiles re-read, yet
+                        // (unlike a nontemporal store) into the last-level cache, from which the next
+                        // GEMM reads them. The s_nop gives the store its wait states before the
+                        // data registers are written again (the compiler does not see into asm).
+                        asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1"
+                                     :: "v"(p.qo + qo_byte(rf, p.KSo, kf, lane)), "v"(v4i{d[0], d[1], d[2], d[3]})
+                                     : "memory");
                     }
                     if (wn == 0 && lane < 16) p.sxo[sxo_index(t, p.n_nt, nt)] = scale;
                 }
