@@ -2177,7 +2177,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
         const int tbase = mt * BM + wm * 64, ncol = nt * BN + wn * 64 + rcol;
         const bool col_ok = ncol < p.N;
         // Residual rows of pieces m0 and m0 + 1 (half before the last epilogue, half
-        // after it, to stay within the register budget). Full row tiles: a scalar row
+        // after it, to stay within the register budget), read once: nontemporal loads, which
+        // leave L2 to the operand tiles. Full row tiles: a scalar row
         // base plus one 32-bit lane offset; the last row tile clamps rows to T - 1
         // (never stored). Columns past N read the last 4 columns (never stored).
         auto load_res = [&](int m0) {
@@ -2189,14 +2190,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
                 for (int mi = m0; mi < m0 + 2; ++mi)
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
-                        rv[mi][q] = *reinterpret_cast<const v4f *>(p.res + (size_t) (row0 + mi * 16 + 4 * q) * p.N + lo);
+                        rv[mi][q] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p.res + (size_t) (row0 + mi * 16 + 4 * q) * p.N + lo));
             } else {
 #pragma unroll
                 for (int mi = m0; mi < m0 + 2; ++mi)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const int t = clamp_row(row0 + mi * 16 + 4 * q + rrow, p.T);
-                        rv[mi][q] = *reinterpret_cast<const v4f *>(p.res + (size_t) t * p.N + col);
+                        rv[mi][q] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p.res + (size_t) t * p.N + col));
                     }
             }
         };
