@@ -2071,9 +2071,9 @@ __device__ __forceinline__ void dma16s(const int8_t * base, uint32_t voff, uint3
 //  - the wait at each k-step is therefore a constant vmcnt: 8, or 9 on wave 0 for
 //    the two k-steps whose later loads include its scale load;
 //  - the output phase issues its stores at once (they write slot 3, free after the
-//    tile's last barrier); vmcnt counts loads and stores, which may complete out of
-//    order, so the next tile's first k-step waits for every outstanding operation
-//    (its three prefetched k-steps and the stores) before the constant counts resume.
+//    tile's last barrier); vmcnt counts the stores too, so the next tile's first
+//    k-step waits for every outstanding operation (its three prefetched k-steps and
+//    the stores) before the constant counts resume.
 // The residual rows are loaded after the tile's last MFMAs, under the last epilogue.
 template <bool RES>
 __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
