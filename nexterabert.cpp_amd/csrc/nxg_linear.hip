@@ -2151,136 +2151,151 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
         issue(r0, 2, 2);
         wait_vm<0>();
     }
-    for (int it = 0; it < walk.count; ++it) {
-        const int tile = walk.tile(it);
-        const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
-        const frag_rows cur = rows_of(it), nxt = rows_of(it + 1);
-        // the load that k-step j of block B issues (ring_prefetch: this tile's k-step
-        // 4B + 3 + j, or in the last block the next tile's k-step j - 1)
-        auto prefetch = [&](int B, int j, auto last_tag) {
-            const ring_load l = ring_prefetch(it, B, j, decltype(last_tag)::value);
-            issue(l.pos == it ? cur : nxt, l.ks, l.slot);
-        };
-        // wave 0's scale loads: lane l < 32 the sx of row group l of the tile, lane
-        // l >= 32 the sw of columns 4(l-32)..+3; block B adds B * sstep bytes.
-        const float * ssrc;
-        size_t sstep;
-        if (lane < 32) {
-            ssrc = p.sx + sx_group_index(mt, lane, p.MF, p.n_blk, 0);
-            sstep = 4 * sizeof(float);
-        } else {
-            ssrc = p.sw + sw_index(0, p.NP, nt * BN + 4 * (lane - 32));
-            sstep = (size_t) p.NP * sizeof(float);
-        }
-        v4f rv[4][4];                                // residual rows (RES)
-        const int rrow = lane >> 4, rcol = 4 * (lane & 15);
-        const int tbase = mt * BM + wm * 64, ncol = nt * BN + wn * 64 + rcol;
-        const bool col_ok = ncol < p.N;
-        // Residual rows of pieces m0 and m0 + 1 (half before the last epilogue, half
-        // after it, to stay within the register budget), read once: nontemporal loads, which
-        // leave L2 to the operand tiles. Full row tiles: a scalar row
-        // base plus one 32-bit lane offset; the last row tile clamps rows to T - 1
-        // (never stored). Columns past N read the last 4 columns (never stored).
-        auto load_res = [&](int m0) {
-            const int row0 = mt * BM + wm * 64;
-            const uint32_t col = (uint32_t) clamp_col4(ncol, p.N);
-            if (row0 + 64 <= p.T) {
-                const uint32_t lo = (uint32_t) rrow * (uint32_t) p.N + col;
-#pragma unroll
-                for (int mi = m0; mi < m0 + 2; ++mi)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        rv[mi][q] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p.res + (size_t) (row0 + mi * 16 + 4 * q) * p.N + lo));
+    // The tile walk, instantiated for one 256-input block per tile and for several, so that
+    // whether a block's fold starts from +0 is static in every block.
+    auto walk_tiles = [&](auto one_tag) {
+        constexpr bool one = decltype(one_tag)::value;
+        for (int it = 0; it < walk.count; ++it) {
+            const int tile = walk.tile(it);
+            const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
+            const frag_rows cur = rows_of(it), nxt = rows_of(it + 1);
+            // the load that k-step j of block B issues (ring_prefetch: this tile's k-step
+            // 4B + 3 + j, or in the last block the next tile's k-step j - 1)
+            auto prefetch = [&](int B, int j, auto last_tag) {
+                const ring_load l = ring_prefetch(it, B, j, decltype(last_tag)::value);
+                issue(l.pos == it ? cur : nxt, l.ks, l.slot);
+            };
+            // wave 0's scale loads: lane l < 32 the sx of row group l of the tile, lane
+            // l >= 32 the sw of columns 4(l-32)..+3; block B adds B * sstep bytes.
+            const float * ssrc;
+            size_t sstep;
+            if (lane < 32) {
+                ssrc = p.sx + sx_group_index(mt, lane, p.MF, p.n_blk, 0);
+                sstep = 4 * sizeof(float);
             } else {
-#pragma unroll
-                for (int mi = m0; mi < m0 + 2; ++mi)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int t = clamp_row(row0 + mi * 16 + 4 * q + rrow, p.T);
-                        rv[mi][q] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p.res + (size_t) t * p.N + col));
+                ssrc = p.sw + sw_index(0, p.NP, nt * BN + 4 * (lane - 32));
+                sstep = (size_t) p.NP * sizeof(float);
+            }
+            v4f rv[4][4];                                // residual rows (RES)
+            const int rrow = lane >> 4, rcol = 4 * (lane & 15);
+            const int tbase = mt * BM + wm * 64, ncol = nt * BN + wn * 64 + rcol;
+            const bool col_ok = ncol < p.N;
+            // Residual rows of pieces m0 and m0 + 1 (half before the last epilogue, half
+            // after it, to stay within the register budget), read once: nontemporal loads, which
+            // leave L2 to the operand tiles. Full row tiles: a scalar row
+            // base plus one 32-bit lane offset; the last row tile clamps rows to T - 1
+            // (never stored). Columns past N read the last 4 columns (never stored).
+            auto load_res = [&](int m0) {
+                const int row0 = mt * BM + wm * 64;
+                const uint32_t col = (uint32_t) clamp_col4(ncol, p.N);
+                if (row0 + 64 <= p.T) {
+                    const uint32_t lo = (uint32_t) rrow * (uint32_t) p.N + col;
+    #pragma unroll
+                    for (int mi = m0; mi < m0 + 2; ++mi)
+    #pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            rv[mi][q] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p.res + (size_t) (row0 + mi * 16 + 4 * q) * p.N + lo));
+                } else {
+    #pragma unroll
+                    for (int mi = m0; mi < m0 + 2; ++mi)
+    #pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const int t = clamp_row(row0 + mi * 16 + 4 * q + rrow, p.T);
+                            rv[mi][q] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p.res + (size_t) t * p.N + col));
+                        }
+                }
+            };
+
+            // One 256-input block: its 4 k-steps, then the epilogue. LAST: the tile's last
+            // block, whose k-steps 1..3 load the next tile's first three.
+            auto run_block = [&](int B, auto last_tag, auto first_tag) {
+                constexpr bool last = decltype(last_tag)::value, first = decltype(first_tag)::value;
+                // k-step 4B (slot 0). In block 0 k-steps 0..2 are already in LDS.
+                // block 0: the tile's first three k-steps were loaded under the previous tile; the
+                // previous tile's output stores went out after them, so wait for everything
+                if (!first) arrive(0); else { wait_vm<0>(); lds_barrier(); }
+                prefetch(B, 0, last_tag);
+                if (wave == 0) dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, ring + 3 * SLOT + SLOT_AB);
+                mma(0, true);
+                // k-step 4B + 1 (slot 1)
+                if (!first) arrive(1); else lds_barrier();
+                prefetch(B, 1, last_tag);
+                mma(1, false);
+                // k-step 4B + 2 (slot 2)
+                if (!first) arrive(2); else lds_barrier();
+                prefetch(B, 2, last_tag);
+                mma(2, false);
+                // k-step 4B + 3 (slot 3, with the block's scales)
+                arrive(3);
+                prefetch(B, 3, last_tag);
+                mma(3, false);
+                if (RES && last) load_res(0);
+
+                // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
+                const float * scl = reinterpret_cast<const float *>(ring + 3 * SLOT + SLOT_AB);
+                float sxv[4];
+    #pragma unroll
+                for (int mi = 0; mi < 4; ++mi) sxv[mi] = scl[wm * 64 + mi * 16 + (lane & 15)];
+    #pragma unroll
+                for (int ni = 0; ni < 4; ++ni) {
+                    const float4 sw4 = *reinterpret_cast<const float4 *>(scl + 128 + wn * 64 + ni * 16 + 4 * (lane >> 4));
+                    const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
+    #pragma unroll
+                    for (int mi = 0; mi < 4; ++mi)
+    #pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float prod = (float) acc[mi][ni][r] * sxv[mi];
+                            // block 0 starts from f = 0: fma(prod, sw, +0.0)
+                            f[mi][ni][r] = __builtin_fmaf(prod, swr[r], first ? 0.0f : f[mi][ni][r]);
+                        }
+                }
+                if (RES && last) load_res(2);
+            };
+            if constexpr (one) {
+                run_block(0, std::true_type{}, std::true_type{});
+            } else {
+                run_block(0, std::false_type{}, std::true_type{});
+                for (int B = 1; B < nb - 1; ++B) run_block(B, std::false_type{}, std::false_type{});
+                run_block(nb - 1, std::true_type{}, std::false_type{});
+            }
+
+            // Output through LDS, whole 128-byte lines per store. Slot 3 is free once
+            // every wave has passed this barrier (the next tile's k-step 3 is loaded only
+            // after its first barrier); each wave owns 4352 bytes of it, 16 rows of 64
+            // floats at a 272-byte pitch. Per 16-token piece mi: write it in MFMA order
+            // (lane: token lane%16, features 16ni + 4(lane/16) + 0..3), read it back as 4
+            // rows of 256 bytes per instruction and store whole lines.
+            lds_barrier();
+            const out_map om = out_of(p, ncol);
+            float * stg = reinterpret_cast<float *>(ring + 3 * SLOT + wave * STAGE_BYTES);
+            const int trow = lane & 15, tcol = 4 * (lane >> 4);
+    #pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+    #pragma unroll
+                for (int ni = 0; ni < 4; ++ni) {
+                    const v4f y = { f[mi][ni][0], f[mi][ni][1], f[mi][ni][2], f[mi][ni][3] };
+                    *reinterpret_cast<v4f *>(stg + trow * STAGE_PITCH + 16 * ni + tcol) = y;
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                // the piece's 4 reads first, then its stores: one LDS round trip per piece
+                // (the empty asm keeps the compiler from sinking each read into its store's branch)
+                v4f y[4];
+    #pragma unroll
+                for (int q = 0; q < 4; ++q) y[q] = *reinterpret_cast<const v4f *>(stg + (4 * q + rrow) * STAGE_PITCH + rcol);
+                asm volatile("s_waitcnt lgkmcnt(0)" :: "v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]) : "memory");
+    #pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int t = tbase + mi * 16 + 4 * q + rrow;
+                    if (t < p.T && col_ok) {
+                        const v4f o = RES ? rv[mi][q] + y[q] : y[q];
+                        __builtin_nontemporal_store(o, reinterpret_cast<v4f *>(om.base + (size_t) t * om.ld + om.col));
                     }
-            }
-        };
-
-        // One 256-input block: its 4 k-steps, then the epilogue. LAST: the tile's last
-        // block, whose k-steps 1..3 load the next tile's first three.
-        auto run_block = [&](int B, auto last_tag) {
-            constexpr bool last = decltype(last_tag)::value;
-            // k-step 4B (slot 0). In block 0 k-steps 0..2 are already in LDS.
-            // block 0: the tile's first three k-steps were loaded under the previous tile; the
-            // previous tile's output stores went out after them, so wait for everything
-            if (B > 0) arrive(0); else { wait_vm<0>(); lds_barrier(); }
-            prefetch(B, 0, last_tag);
-            if (wave == 0) dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, ring + 3 * SLOT + SLOT_AB);
-            mma(0, true);
-            // k-step 4B + 1 (slot 1)
-            if (B > 0) arrive(1); else lds_barrier();
-            prefetch(B, 1, last_tag);
-            mma(1, false);
-            // k-step 4B + 2 (slot 2)
-            if (B > 0) arrive(2); else lds_barrier();
-            prefetch(B, 2, last_tag);
-            mma(2, false);
-            // k-step 4B + 3 (slot 3, with the block's scales)
-            arrive(3);
-            prefetch(B, 3, last_tag);
-            mma(3, false);
-            if (RES && last) load_res(0);
-
-            // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
-            const float * scl = reinterpret_cast<const float *>(ring + 3 * SLOT + SLOT_AB);
-            float sxv[4];
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) sxv[mi] = scl[wm * 64 + mi * 16 + (lane & 15)];
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) {
-                const float4 sw4 = *reinterpret_cast<const float4 *>(scl + 128 + wn * 64 + ni * 16 + 4 * (lane >> 4));
-                const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
-#pragma unroll
-                for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float prod = (float) acc[mi][ni][r] * sxv[mi];
-                        // block 0 starts from f = 0: fma(prod, sw, +0.0)
-                        f[mi][ni][r] = __builtin_fmaf(prod, swr[r], B == 0 ? 0.0f : f[mi][ni][r]);
-                    }
-            }
-            if (RES && last) load_res(2);
-        };
-        for (int B = 0; B < nb - 1; ++B) run_block(B, std::false_type{});
-        run_block(nb - 1, std::true_type{});
-
-        // Output through LDS, whole 128-byte lines per store. Slot 3 is free once
-        // every wave has passed this barrier (the next tile's k-step 3 is loaded only
-        // after its first barrier); each wave owns 4352 bytes of it, 16 rows of 64
-        // floats at a 272-byte pitch. Per 16-token piece mi: write it in MFMA order
-        // (lane: token lane%16, features 16ni + 4(lane/16) + 0..3), read it back as 4
-        // rows of 256 bytes per instruction and store whole lines.
-        lds_barrier();
-        const out_map om = out_of(p, ncol);
-        float * stg = reinterpret_cast<float *>(ring + 3 * SLOT + wave * STAGE_BYTES);
-        const int trow = lane & 15, tcol = 4 * (lane >> 4);
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) {
-                const v4f y = { f[mi][ni][0], f[mi][ni][1], f[mi][ni][2], f[mi][ni][3] };
-                *reinterpret_cast<v4f *>(stg + trow * STAGE_PITCH + 16 * ni + tcol) = y;
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int row = 4 * q + rrow;
-                v4f y = *reinterpret_cast<const v4f *>(stg + row * STAGE_PITCH + rcol);
-                const int t = tbase + mi * 16 + row;
-                if (t < p.T && col_ok) {
-                    if (RES) y = rv[mi][q] + y;
-                    __builtin_nontemporal_store(y, reinterpret_cast<v4f *>(om.base + (size_t) t * om.ld + om.col));
                 }
             }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         }
-    }
+    };
+    if (nb == 1) walk_tiles(std::true_type{});
+    else         walk_tiles(std::false_type{});
     wait_vm<0>();
 }
 
@@ -2606,163 +2621,175 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
         issue(r0, 2, 2);
         wait_vm<0>();
     }
-    for (int it = 0; it < walk.count; ++it) {
-        const int tile = walk.tile(it);
-        const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
-        const frag_rows cur = rows_of(it), nxt = rows_of(it + 1);
-        // the load that k-step j of block B issues (ring_prefetch: this tile's k-step
-        // 4B + 3 + j, or in the last block the next tile's k-step j - 1)
-        auto prefetch = [&](int B, int j, auto last_tag) {
-            const ring_load l = ring_prefetch(it, B, j, decltype(last_tag)::value);
-            issue(l.pos == it ? cur : nxt, l.ks, l.slot);
-        };
-        // Scale loads of block B (B * sstep bytes on): wave 0 lane l < 32 the sx of row
-        // group l, wave 0 lane l >= 32 the sw of columns 4(l-32)..+3, wave 1 lane l < 32
-        // the sw of columns 128 + 4l..+3; lane l lands at scl + 16 l (+ 1024 on wave 1).
-        const float * ssrc;
-        size_t sstep;
-        if (wave == 0 && lane < 32) {
-            ssrc = p.sx + sx_group_index(mt, lane, p.MF, p.n_blk, 0);
-            sstep = 4 * sizeof(float);
-        } else {
-            ssrc = p.sw + sw_index(0, p.NP, nt * WBN + (wave == 0 ? 4 * (lane - 32) : 128 + 4 * lane));
-            sstep = (size_t) p.NP * sizeof(float);
-        }
-        const int tbase = mt * BM + wm * 64;
+    // The tile walk, instantiated for one 256-input block per tile and for several, so that
+    // whether a block's fold starts from +0 is static in every block.
+    auto walk_tiles = [&](auto one_tag) {
+        constexpr bool one = decltype(one_tag)::value;
+        for (int it = 0; it < walk.count; ++it) {
+            const int tile = walk.tile(it);
+            const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
+            const frag_rows cur = rows_of(it), nxt = rows_of(it + 1);
+            // the load that k-step j of block B issues (ring_prefetch: this tile's k-step
+            // 4B + 3 + j, or in the last block the next tile's k-step j - 1)
+            auto prefetch = [&](int B, int j, auto last_tag) {
+                const ring_load l = ring_prefetch(it, B, j, decltype(last_tag)::value);
+                issue(l.pos == it ? cur : nxt, l.ks, l.slot);
+            };
+            // Scale loads of block B (B * sstep bytes on): wave 0 lane l < 32 the sx of row
+            // group l, wave 0 lane l >= 32 the sw of columns 4(l-32)..+3, wave 1 lane l < 32
+            // the sw of columns 128 + 4l..+3; lane l lands at scl + 16 l (+ 1024 on wave 1).
+            const float * ssrc;
+            size_t sstep;
+            if (wave == 0 && lane < 32) {
+                ssrc = p.sx + sx_group_index(mt, lane, p.MF, p.n_blk, 0);
+                sstep = 4 * sizeof(float);
+            } else {
+                ssrc = p.sw + sw_index(0, p.NP, nt * WBN + (wave == 0 ? 4 * (lane - 32) : 128 + 4 * lane));
+                sstep = (size_t) p.NP * sizeof(float);
+            }
+            const int tbase = mt * BM + wm * 64;
 
-        auto run_block = [&](int B, auto last_tag) {
-            constexpr bool last = decltype(last_tag)::value;
-            // k-step 4B (slot 0). In block 0 k-steps 0..2 are already in LDS.
-            if (B > 0) arrive(0); else lds_barrier();
-            prefetch(B, 0, last_tag);
-            if (wave == 0) {
-                dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl);
-            } else if (wave == 1 && lane < 32) {
-                dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, reinterpret_cast<const char *>(scl) + 1024);
-            }
-            mma(0, true);
-            // k-step 4B + 1 (slot 1)
-            if (B > 0) arrive(1); else lds_barrier();
-            prefetch(B, 1, last_tag);
-            mma(1, false);
-            // k-step 4B + 2 (slot 2)
-            if (B > 0) arrive(2); else lds_barrier();
-            prefetch(B, 2, last_tag);
-            mma(2, false);
-            // k-step 4B + 3 (slot 3); the block's scales arrive with it
-            arrive(3);
-            prefetch(B, 3, last_tag);
-            mma(3, false);
+            auto run_block = [&](int B, auto last_tag, auto first_tag) {
+                constexpr bool last = decltype(last_tag)::value, first = decltype(first_tag)::value;
+                // k-step 4B (slot 0). In block 0 k-steps 0..2 are already in LDS.
+                if (!first) arrive(0); else lds_barrier();
+                prefetch(B, 0, last_tag);
+                if (wave == 0) {
+                    dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl);
+                } else if (wave == 1 && lane < 32) {
+                    dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, reinterpret_cast<const char *>(scl) + 1024);
+                }
+                mma(0, true);
+                // k-step 4B + 1 (slot 1)
+                if (!first) arrive(1); else lds_barrier();
+                prefetch(B, 1, last_tag);
+                mma(1, false);
+                // k-step 4B + 2 (slot 2)
+                if (!first) arrive(2); else lds_barrier();
+                prefetch(B, 2, last_tag);
+                mma(2, false);
+                // k-step 4B + 3 (slot 3); the block's scales arrive with it
+                arrive(3);
+                prefetch(B, 3, last_tag);
+                mma(3, false);
 
-            // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
-            float sxv[4];
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) sxv[mi] = scl[wm * 64 + mi * 16 + (lane & 15)];
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) {
-                const float4 sw4 = *reinterpret_cast<const float4 *>(scl + BM + wn * 64 + ni * 16 + 4 * (lane >> 4));
-                const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
-#pragma unroll
-                for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float prod = (float) acc[mi][ni][r] * sxv[mi];
-                        // block 0 starts from f = 0: fma(prod, sw, +0.0)
-                        f[mi][ni][r] = __builtin_fmaf(prod, swr[r], B == 0 ? 0.0f : f[mi][ni][r]);
-                    }
-            }
-        };
-        for (int B = 0; B < nb - 1; ++B) run_block(B, std::false_type{});
-        run_block(nb - 1, std::true_type{});
-
-        // Every load of this wave first: the next tile's first three k-steps (its block
-        // 0 then waits only at k-step 3, and the stores below stand behind no load it
-        // waits for).
-        wait_vm<0>();
-        {
-            // relu(f)^2 in place: max(f, 0) (maxNum: a NaN gives 0; f is never a signalling
-            // NaN, being an fma result), then r * r -- the bits of (f > 0 ? f : 0)^2.
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float x = fmaxf(f[mi][ni][r], 0.0f);
-                        f[mi][ni][r] = x * x;
-                    }
-            // Row maxima (values >= 0, no NaN: the reference's MAXPS fold is the plain
-            // maximum here): over this lane's 16 values, the wave's 4 lanes of the row,
-            // then the 4 waves of the row through LDS, am[wm][row][wn].
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
-                float m = 0.0f;
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) m = fmaxf(m, f[mi][ni][r]);
-                m = rows_max(m);
-                if (lane < 16) am[(wm * 64 + mi * 16 + lane) * 4 + wn] = m;
-            }
-            lds_barrier();
-            // Row maxima of this lane's 4 row groups; with every one of the wave finite (the
-            // usual case) each value f * inv lies in [0, ACT_MAX + 1/2), so CVTPS2DQ and the
-            // saturating packs reduce to round-to-nearest-even, which v_cvt_pk_u8_f32 does
-            // while packing the byte. An infinite maximum takes quant1 (NaN -> 0x80000000).
-            float amx[4];
-            bool fin = true;
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
-                const int t = tbase + mi * 16 + (lane & 15);
-                const v4f a4 = *reinterpret_cast<const v4f *>(am + (wm * 64 + mi * 16 + (lane & 15)) * 4);
-                amx[mi] = t < p.T ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
-                fin = fin && amx[mi] < INFINITY;
-            }
-            const bool fast = __builtin_amdgcn_ballot_w64(!fin) == 0;
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
-                const int t = tbase + mi * 16 + (lane & 15);
-                const bool row_ok = t < p.T;
-                const float amax = amx[mi];
-                const float scale = amax / (float) ACT_MAX;
-                const float inv = amax > 0.0f ? (float) ACT_MAX / amax : 0.0f;
-                // column 16ni + 4(lane/16) + r of the wave's 64: byte r of d[ni]
-                int d[4];
-#pragma unroll
+                // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
+                float sxv[4];
+    #pragma unroll
+                for (int mi = 0; mi < 4; ++mi) sxv[mi] = scl[wm * 64 + mi * 16 + (lane & 15)];
+    #pragma unroll
                 for (int ni = 0; ni < 4; ++ni) {
-                    const int n = nt * WBN + wn * 64 + ni * 16 + 4 * (lane >> 4);
-                    int packed;
-                    if (fast) {
-                        unsigned u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][0] * inv, 0, 0u);
-                        u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][1] * inv, 1, u);
-                        u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][2] * inv, 2, u);
-                        u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][3] * inv, 3, u);
-                        packed = (int) u;
-                    } else {
-                        packed = (quant1<ACT_MAX>(f[mi][ni][0], inv) & 0xff) | ((quant1<ACT_MAX>(f[mi][ni][1], inv) & 0xff) << 8)
-                               | ((quant1<ACT_MAX>(f[mi][ni][2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(f[mi][ni][3], inv) & 0xff) << 24);
-                    }
-                    d[ni] = row_ok && n < p.N ? packed : 0;
+                    const float4 sw4 = *reinterpret_cast<const float4 *>(scl + BM + wn * 64 + ni * 16 + 4 * (lane >> 4));
+                    const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
+    #pragma unroll
+                    for (int mi = 0; mi < 4; ++mi)
+    #pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float prod = (float) acc[mi][ni][r] * sxv[mi];
+                            // block 0 starts from f = 0: fma(prod, sw, +0.0)
+                            f[mi][ni][r] = __builtin_fmaf(prod, swr[r], first ? 0.0f : f[mi][ni][r]);
+                        }
                 }
-                // lane c + 16 j now gets columns 16 j + 0..15 of row c: one fragment lane
-                rows_transpose(d);
-                const int rf = mt * (BM / 16) + wm * 4 + mi, kf = nt * (WBN / 64) + wn;
-                if (rf < p.MF) {
-                    if (kf < p.KSo) {
-                        // device scope (sc1): the int8 rows go past L2, where they would evict the
-                        // activation row tile that this row's other column tiles re-read, yet
-                        // (unlike a nontemporal store) into the last-level cache, from which the next
-                        // GEMM reads them. The s_nop gives the store its wait states before the
-                        // data registers are written again (the compiler does not see into asm).
-                        asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1"
-                                     :: "v"(p.qo + qo_byte(rf, p.KSo, kf, lane)), "v"(v4i{d[0], d[1], d[2], d[3]})
-                                     : "memory");
+            };
+            if constexpr (one) {
+                run_block(0, std::true_type{}, std::true_type{});
+            } else {
+                run_block(0, std::false_type{}, std::true_type{});
+                for (int B = 1; B < nb - 1; ++B) run_block(B, std::false_type{}, std::false_type{});
+                run_block(nb - 1, std::true_type{}, std::false_type{});
+            }
+
+            // Every load of this wave first: the next tile's first three k-steps (its block
+            // 0 then waits only at k-step 3, and the stores below stand behind no load it
+            // waits for).
+            wait_vm<0>();
+            {
+                // relu(f)^2 in place: max(f, 0) (maxNum: a NaN gives 0; f is never a signalling
+                // NaN, being an fma result), then r * r -- the bits of (f > 0 ? f : 0)^2.
+    #pragma unroll
+                for (int mi = 0; mi < 4; ++mi)
+    #pragma unroll
+                    for (int ni = 0; ni < 4; ++ni)
+    #pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float x = fmaxf(f[mi][ni][r], 0.0f);
+                            f[mi][ni][r] = x * x;
+                        }
+                // Row maxima (values >= 0, no NaN: the reference's MAXPS fold is the plain
+                // maximum here): over this lane's 16 values, the wave's 4 lanes of the row,
+                // then the 4 waves of the row through LDS, am[wm][row][wn].
+    #pragma unroll
+                for (int mi = 0; mi < 4; ++mi) {
+                    float m = 0.0f;
+    #pragma unroll
+                    for (int ni = 0; ni < 4; ++ni)
+    #pragma unroll
+                        for (int r = 0; r < 4; ++r) m = fmaxf(m, f[mi][ni][r]);
+                    m = rows_max(m);
+                    if (lane < 16) am[(wm * 64 + mi * 16 + lane) * 4 + wn] = m;
+                }
+                lds_barrier();
+                // Row maxima of this lane's 4 row groups; with every one of the wave finite (the
+                // usual case) each value f * inv lies in [0, ACT_MAX + 1/2), so CVTPS2DQ and the
+                // saturating packs reduce to round-to-nearest-even, which v_cvt_pk_u8_f32 does
+                // while packing the byte. An infinite maximum takes quant1 (NaN -> 0x80000000).
+                float amx[4];
+                bool fin = true;
+    #pragma unroll
+                for (int mi = 0; mi < 4; ++mi) {
+                    const int t = tbase + mi * 16 + (lane & 15);
+                    const v4f a4 = *reinterpret_cast<const v4f *>(am + (wm * 64 + mi * 16 + (lane & 15)) * 4);
+                    amx[mi] = t < p.T ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
+                    fin = fin && amx[mi] < INFINITY;
+                }
+                const bool fast = __builtin_amdgcn_ballot_w64(!fin) == 0;
+    #pragma unroll
+                for (int mi = 0; mi < 4; ++mi) {
+                    const int t = tbase + mi * 16 + (lane & 15);
+                    const bool row_ok = t < p.T;
+                    const float amax = amx[mi];
+                    const float scale = amax / (float) ACT_MAX;
+                    const float inv = amax > 0.0f ? (float) ACT_MAX / amax : 0.0f;
+                    // column 16ni + 4(lane/16) + r of the wave's 64: byte r of d[ni]
+                    int d[4];
+    #pragma unroll
+                    for (int ni = 0; ni < 4; ++ni) {
+                        const int n = nt * WBN + wn * 64 + ni * 16 + 4 * (lane >> 4);
+                        int packed;
+                        if (fast) {
+                            unsigned u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][0] * inv, 0, 0u);
+                            u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][1] * inv, 1, u);
+                            u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][2] * inv, 2, u);
+                            u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][3] * inv, 3, u);
+                            packed = (int) u;
+                        } else {
+                            packed = (quant1<ACT_MAX>(f[mi][ni][0], inv) & 0xff) | ((quant1<ACT_MAX>(f[mi][ni][1], inv) & 0xff) << 8)
+                                   | ((quant1<ACT_MAX>(f[mi][ni][2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(f[mi][ni][3], inv) & 0xff) << 24);
+                        }
+                        d[ni] = row_ok && n < p.N ? packed : 0;
                     }
-                    if (wn == 0 && lane < 16) p.sxo[sxo_index(t, p.n_nt, nt)] = scale;
+                    // lane c + 16 j now gets columns 16 j + 0..15 of row c: one fragment lane
+                    rows_transpose(d);
+                    const int rf = mt * (BM / 16) + wm * 4 + mi, kf = nt * (WBN / 64) + wn;
+                    if (rf < p.MF) {
+                        if (kf < p.KSo) {
+                            // device scope (sc1): the int8 rows go past L2, where they would evict the
+                            // activation row tile that this row's other column tiles re-read, yet
+                            // (unlike a nontemporal store) into the last-level cache, from which the next
+                            // GEMM reads them. The s_nop gives the store its wait states before the
+                            // data registers are written again (the compiler does not see into asm).
+                            asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1"
+                                         :: "v"(p.qo + qo_byte(rf, p.KSo, kf, lane)), "v"(v4i{d[0], d[1], d[2], d[3]})
+                                         : "memory");
+                        }
+                        if (wn == 0 && lane < 16) p.sxo[sxo_index(t, p.n_nt, nt)] = scale;
+                    }
                 }
             }
         }
-    }
+    };
+    if (nb == 1) walk_tiles(std::true_type{});
+    else         walk_tiles(std::false_type{});
     wait_vm<0>();
 }
 
