@@ -2190,15 +2190,15 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
                 const uint32_t col = (uint32_t) clamp_col4(ncol, p.N);
                 if (row0 + 64 <= p.T) {
                     const uint32_t lo = (uint32_t) rrow * (uint32_t) p.N + col;
-    #pragma unroll
+#pragma unroll
                     for (int mi = m0; mi < m0 + 2; ++mi)
-    #pragma unroll
+#pragma unroll
                         for (int q = 0; q < 4; ++q)
                             rv[mi][q] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p.res + (size_t) (row0 + mi * 16 + 4 * q) * p.N + lo));
                 } else {
-    #pragma unroll
+#pragma unroll
                     for (int mi = m0; mi < m0 + 2; ++mi)
-    #pragma unroll
+#pragma unroll
                         for (int q = 0; q < 4; ++q) {
                             const int t = clamp_row(row0 + mi * 16 + 4 * q + rrow, p.T);
                             rv[mi][q] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p.res + (size_t) t * p.N + col));
@@ -2234,15 +2234,15 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
                 // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
                 const float * scl = reinterpret_cast<const float *>(ring + 3 * SLOT + SLOT_AB);
                 float sxv[4];
-    #pragma unroll
+#pragma unroll
                 for (int mi = 0; mi < 4; ++mi) sxv[mi] = scl[wm * 64 + mi * 16 + (lane & 15)];
-    #pragma unroll
+#pragma unroll
                 for (int ni = 0; ni < 4; ++ni) {
                     const float4 sw4 = *reinterpret_cast<const float4 *>(scl + 128 + wn * 64 + ni * 16 + 4 * (lane >> 4));
                     const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
-    #pragma unroll
+#pragma unroll
                     for (int mi = 0; mi < 4; ++mi)
-    #pragma unroll
+#pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const float prod = (float) acc[mi][ni][r] * sxv[mi];
                             // block 0 starts from f = 0: fma(prod, sw, +0.0)
@@ -2269,9 +2269,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
             const out_map om = out_of(p, ncol);
             float * stg = reinterpret_cast<float *>(ring + 3 * SLOT + wave * STAGE_BYTES);
             const int trow = lane & 15, tcol = 4 * (lane >> 4);
-    #pragma unroll
+#pragma unroll
             for (int mi = 0; mi < 4; ++mi) {
-    #pragma unroll
+#pragma unroll
                 for (int ni = 0; ni < 4; ++ni) {
                     const v4f y = { f[mi][ni][0], f[mi][ni][1], f[mi][ni][2], f[mi][ni][3] };
                     *reinterpret_cast<v4f *>(stg + trow * STAGE_PITCH + 16 * ni + tcol) = y;
@@ -2280,10 +2280,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
                 // the piece's 4 reads first, then its stores: one LDS round trip per piece
                 // (the empty asm keeps the compiler from sinking each read into its store's branch)
                 v4f y[4];
-    #pragma unroll
+#pragma unroll
                 for (int q = 0; q < 4; ++q) y[q] = *reinterpret_cast<const v4f *>(stg + (4 * q + rrow) * STAGE_PITCH + rcol);
                 asm volatile("s_waitcnt lgkmcnt(0)" :: "v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]) : "memory");
-    #pragma unroll
+#pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int t = tbase + mi * 16 + 4 * q + rrow;
                     if (t < p.T && col_ok) {
@@ -2675,15 +2675,15 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
 
                 // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
                 float sxv[4];
-    #pragma unroll
+#pragma unroll
                 for (int mi = 0; mi < 4; ++mi) sxv[mi] = scl[wm * 64 + mi * 16 + (lane & 15)];
-    #pragma unroll
+#pragma unroll
                 for (int ni = 0; ni < 4; ++ni) {
                     const float4 sw4 = *reinterpret_cast<const float4 *>(scl + BM + wn * 64 + ni * 16 + 4 * (lane >> 4));
                     const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
-    #pragma unroll
+#pragma unroll
                     for (int mi = 0; mi < 4; ++mi)
-    #pragma unroll
+#pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const float prod = (float) acc[mi][ni][r] * sxv[mi];
                             // block 0 starts from f = 0: fma(prod, sw, +0.0)
@@ -2706,11 +2706,11 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
             {
                 // relu(f)^2 in place: max(f, 0) (maxNum: a NaN gives 0; f is never a signalling
                 // NaN, being an fma result), then r * r -- the bits of (f > 0 ? f : 0)^2.
-    #pragma unroll
+#pragma unroll
                 for (int mi = 0; mi < 4; ++mi)
-    #pragma unroll
+#pragma unroll
                     for (int ni = 0; ni < 4; ++ni)
-    #pragma unroll
+#pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const float x = fmaxf(f[mi][ni][r], 0.0f);
                             f[mi][ni][r] = x * x;
@@ -2718,43 +2718,43 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                 // Row maxima (values >= 0, no NaN: the reference's MAXPS fold is the plain
                 // maximum here): over this lane's 16 values, the wave's 4 lanes of the row,
                 // then the 4 waves of the row through LDS, am[wm][row][wn].
-    #pragma unroll
+#pragma unroll
                 for (int mi = 0; mi < 4; ++mi) {
                     float m = 0.0f;
-    #pragma unroll
+#pragma unroll
                     for (int ni = 0; ni < 4; ++ni)
-    #pragma unroll
+#pragma unroll
                         for (int r = 0; r < 4; ++r) m = fmaxf(m, f[mi][ni][r]);
                     m = rows_max(m);
                     if (lane < 16) am[(wm * 64 + mi * 16 + lane) * 4 + wn] = m;
                 }
                 lds_barrier();
-                // Row maxima of this lane's 4 row groups; with every one of the wave finite (the
-                // usual case) each value f * inv lies in [0, ACT_MAX + 1/2), so CVTPS2DQ and the
-                // saturating packs reduce to round-to-nearest-even, which v_cvt_pk_u8_f32 does
-                // while packing the byte. An infinite maximum takes quant1 (NaN -> 0x80000000).
-                float amx[4];
-                bool fin = true;
-    #pragma unroll
-                for (int mi = 0; mi < 4; ++mi) {
-                    const int t = tbase + mi * 16 + (lane & 15);
-                    const v4f a4 = *reinterpret_cast<const v4f *>(am + (wm * 64 + mi * 16 + (lane & 15)) * 4);
-                    amx[mi] = t < p.T ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
-                    fin = fin && amx[mi] < INFINITY;
-                }
-                const bool fast = __builtin_amdgcn_ballot_w64(!fin) == 0;
-    #pragma unroll
-                for (int mi = 0; mi < 4; ++mi) {
-                    const int t = tbase + mi * 16 + (lane & 15);
-                    const bool row_ok = t < p.T;
-                    const float amax = amx[mi];
-                    const float scale = amax / (float) ACT_MAX;
-                    const float inv = amax > 0.0f ? (float) ACT_MAX / amax : 0.0f;
+                // Lane l takes row l of the wave's 64 (row group l / 16, row l % 16): the row's
+                // maximum over the 4 waves, its scale amax / ACT_MAX and inv = ACT_MAX / amax, each
+                // computed once per row; a transpose then gives every lane the inv of its 4 row
+                // groups. With every maximum of the wave finite (the usual case) each value f * inv
+                // lies in [0, ACT_MAX + 1/2), so CVTPS2DQ and the saturating packs reduce to
+                // round-to-nearest-even, which v_cvt_pk_u8_f32 does while packing the byte. An
+                // infinite maximum takes quant1 (NaN -> 0x80000000).
+                const int tl = tbase + lane;
+                const v4f a4 = *reinterpret_cast<const v4f *>(am + (wm * 64 + lane) * 4);
+                const float amax_l = tl < p.T ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
+                const float inv_l = amax_l > 0.0f ? (float) ACT_MAX / amax_l : 0.0f;
+                const bool fast = __builtin_amdgcn_ballot_w64(!(amax_l < INFINITY)) == 0;
+                int invs[4] = { __float_as_int(inv_l), __float_as_int(inv_l), __float_as_int(inv_l), __float_as_int(inv_l) };
+                rows_transpose(invs);                        // invs[mi]: row group mi, row lane % 16
+                if (wn == 0 && mt * (BM / 16) + wm * 4 + (lane >> 4) < p.MF)
+                    p.sxo[sxo_index(tl, p.n_nt, nt)] = amax_l / (float) ACT_MAX;
+                // Row group mi: its int8 values, zero past row T - 1 and column N - 1 (GUARD; a
+                // tile inside both bounds skips the tests).
+                auto quantize_store = [&](int mi, auto guard_tag) {
+                    constexpr bool guard = decltype(guard_tag)::value;
+                    const float inv = __int_as_float(invs[mi]);
+                    const bool row_ok = tbase + mi * 16 + (lane & 15) < p.T;
                     // column 16ni + 4(lane/16) + r of the wave's 64: byte r of d[ni]
                     int d[4];
-    #pragma unroll
+#pragma unroll
                     for (int ni = 0; ni < 4; ++ni) {
-                        const int n = nt * WBN + wn * 64 + ni * 16 + 4 * (lane >> 4);
                         int packed;
                         if (fast) {
                             unsigned u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][0] * inv, 0, 0u);
@@ -2766,24 +2766,32 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                             packed = (quant1<ACT_MAX>(f[mi][ni][0], inv) & 0xff) | ((quant1<ACT_MAX>(f[mi][ni][1], inv) & 0xff) << 8)
                                    | ((quant1<ACT_MAX>(f[mi][ni][2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(f[mi][ni][3], inv) & 0xff) << 24);
                         }
-                        d[ni] = row_ok && n < p.N ? packed : 0;
+                        if (guard) {
+                            const int n = nt * WBN + wn * 64 + ni * 16 + 4 * (lane >> 4);
+                            packed = row_ok && n < p.N ? packed : 0;
+                        }
+                        d[ni] = packed;
                     }
                     // lane c + 16 j now gets columns 16 j + 0..15 of row c: one fragment lane
                     rows_transpose(d);
                     const int rf = mt * (BM / 16) + wm * 4 + mi, kf = nt * (WBN / 64) + wn;
-                    if (rf < p.MF) {
-                        if (kf < p.KSo) {
-                            // device scope (sc1): the int8 rows go past L2, where they would evict the
-                            // activation row tile that this row's other column tiles re-read, yet
-                            // (unlike a nontemporal store) into the last-level cache, from which the next
-                            // GEMM reads them. The s_nop gives the store its wait states before the
-                            // data registers are written again (the compiler does not see into asm).
-                            asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1"
-                                         :: "v"(p.qo + qo_byte(rf, p.KSo, kf, lane)), "v"(v4i{d[0], d[1], d[2], d[3]})
-                                         : "memory");
-                        }
-                        if (wn == 0 && lane < 16) p.sxo[sxo_index(t, p.n_nt, nt)] = scale;
+                    if (rf < p.MF && kf < p.KSo) {
+                        // device scope (sc1): the int8 rows go past L2, where they would evict the
+                        // activation row tile that this row's other column tiles re-read, yet
+                        // (unlike a nontemporal store) into the last-level cache, from which the next
+                        // GEMM reads them. The s_nop gives the store its wait states before the
+                        // data registers are written again (the compiler does not see into asm).
+                        asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1"
+                                     :: "v"(p.qo + qo_byte(rf, p.KSo, kf, lane)), "v"(v4i{d[0], d[1], d[2], d[3]})
+                                     : "memory");
                     }
+                };
+                if (mt * BM + BM <= p.T && nt * WBN + WBN <= p.N) {
+#pragma unroll
+                    for (int mi = 0; mi < 4; ++mi) quantize_store(mi, std::false_type{});
+                } else {
+#pragma unroll
+                    for (int mi = 0; mi < 4; ++mi) quantize_store(mi, std::true_type{});
                 }
             }
         }
