@@ -2704,20 +2704,11 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
             // waits for).
             wait_vm<0>();
             {
-                // relu(f)^2 in place: max(f, 0) (maxNum: a NaN gives 0; f is never a signalling
-                // NaN, being an fma result), then r * r -- the bits of (f > 0 ? f : 0)^2.
-#pragma unroll
-                for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                    for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const float x = fmaxf(f[mi][ni][r], 0.0f);
-                            f[mi][ni][r] = x * x;
-                        }
-                // Row maxima (values >= 0, no NaN: the reference's MAXPS fold is the plain
-                // maximum here): over this lane's 16 values, the wave's 4 lanes of the row,
-                // then the 4 waves of the row through LDS, am[wm][row][wn].
+                // Row maxima of relu(f) = max(f, 0) (maxNum: a NaN counts as 0; f is never a
+                // signalling NaN, being an fma result): over this lane's 16 values, the wave's 4
+                // lanes of the row, then the 4 waves of the row through LDS, am[wm][row][wn]. The
+                // block amax of relu(f)^2 (values >= 0, no NaN: the reference's MAXPS fold is the
+                // plain maximum) is the square of that maximum, r * r being monotonic in r >= 0.
 #pragma unroll
                 for (int mi = 0; mi < 4; ++mi) {
                     float m = 0.0f;
@@ -2738,7 +2729,8 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                 // infinite maximum takes quant1 (NaN -> 0x80000000).
                 const int tl = tbase + lane;
                 const v4f a4 = *reinterpret_cast<const v4f *>(am + (wm * 64 + lane) * 4);
-                const float amax_l = tl < p.T ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
+                const float rmax = tl < p.T ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
+                const float amax_l = rmax * rmax;
                 const float inv_l = amax_l > 0.0f ? (float) ACT_MAX / amax_l : 0.0f;
                 const bool fast = __builtin_amdgcn_ballot_w64(!(amax_l < INFINITY)) == 0;
                 int invs[4] = { __float_as_int(inv_l), __float_as_int(inv_l), __float_as_int(inv_l), __float_as_int(inv_l) };
@@ -2757,14 +2749,22 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                     for (int ni = 0; ni < 4; ++ni) {
                         int packed;
                         if (fast) {
-                            unsigned u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][0] * inv, 0, 0u);
-                            u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][1] * inv, 1, u);
-                            u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][2] * inv, 2, u);
-                            u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][3] * inv, 3, u);
+                            // f * |f| is relu(f)^2 for f >= +0 and <= 0 (or NaN) otherwise, which
+                            // v_cvt_pk_u8_f32 turns into 0 like the reference's relu
+                            unsigned u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][0] * fabsf(f[mi][ni][0]) * inv, 0, 0u);
+                            u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][1] * fabsf(f[mi][ni][1]) * inv, 1, u);
+                            u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][2] * fabsf(f[mi][ni][2]) * inv, 2, u);
+                            u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][3] * fabsf(f[mi][ni][3]) * inv, 3, u);
                             packed = (int) u;
                         } else {
-                            packed = (quant1<ACT_MAX>(f[mi][ni][0], inv) & 0xff) | ((quant1<ACT_MAX>(f[mi][ni][1], inv) & 0xff) << 8)
-                                   | ((quant1<ACT_MAX>(f[mi][ni][2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(f[mi][ni][3], inv) & 0xff) << 24);
+                            float r2[4];
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float x = fmaxf(f[mi][ni][r], 0.0f);
+                                r2[r] = x * x;
+                            }
+                            packed = (quant1<ACT_MAX>(r2[0], inv) & 0xff) | ((quant1<ACT_MAX>(r2[1], inv) & 0xff) << 8)
+                                   | ((quant1<ACT_MAX>(r2[2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(r2[3], inv) & 0xff) << 24);
                         }
                         if (guard) {
                             const int n = nt * WBN + wn * 64 + ni * 16 + 4 * (lane >> 4);
