@@ -2291,6 +2291,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
                         __builtin_nontemporal_store(o, reinterpret_cast<v4f *>(om.base + (size_t) t * om.ld + om.col));
                     }
                 }
+                // The residual rows count as used on every path: where no lane of a store is
+                // active, the compiler would otherwise wait for their loads (vmcnt(0), draining
+                // the prefetched k-steps) only where the next tile first writes those registers.
+                if (RES) asm volatile("" :: "v"(rv[mi][0]), "v"(rv[mi][1]), "v"(rv[mi][2]), "v"(rv[mi][3]));
             }
         }
     };
