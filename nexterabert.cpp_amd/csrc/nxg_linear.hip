@@ -1794,10 +1794,12 @@ typedef __attribute__((address_space(3))) void lds_void;
 // Issued from inline asm so that the compiler's wait-count pass does not track it
 // (it would drain every prefetch at the loop back-edge); each use is synchronized
 // explicitly with wait_vm before the barrier that precedes its readers.
-__device__ __forceinline__ void dma16(const void * gptr, const void * lds) {
-    const uint32_t la = (uint32_t) (uintptr_t) (lds_void *) lds;
+__device__ __forceinline__ void dma16l(const void * gptr, uint32_t la) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :: "v"(gptr), "s"(la) : "memory", "m0");
+}
+__device__ __forceinline__ void dma16(const void * gptr, const void * lds) {
+    dma16l(gptr, (uint32_t) (uintptr_t) (lds_void *) lds);
 }
 
 // Waits until at most n of this wave's vector-memory loads are outstanding.
@@ -2570,6 +2572,9 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
     const size_t frow = (size_t) p.KS * FRAG;        // bytes of one fragment row
     const uint32_t ring_lds = (uint32_t) (uintptr_t) (lds_void *) ring;
     const uint32_t lane16 = (uint32_t) lane * 16;
+    // LDS address of the scale area as an integer, so that no generic pointer to it is
+    // merged across the waves' branches below
+    const uint32_t scl_lds = (uint32_t) (uintptr_t) (lds_void *) scl;
 
     struct frag_rows {                               // this wave's 3 fragment rows of a tile
         const int8_t * a;
@@ -2659,9 +2664,9 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                 if (!first) arrive(0); else lds_barrier();
                 prefetch(B, 0, last_tag);
                 if (wave == 0) {
-                    dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl);
+                    dma16l(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl_lds);
                 } else if (wave == 1 && lane < 32) {
-                    dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, reinterpret_cast<const char *>(scl) + 1024);
+                    dma16l(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl_lds + 1024);
                 }
                 mma(0, true);
                 // k-step 4B + 1 (slot 1)
