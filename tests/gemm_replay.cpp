@@ -447,8 +447,14 @@ void replay_relu2_q8(replay & r) {
                 }
                 for (int mi = 0; mi < 4; ++mi) {
                     const int rf = mt * (BM / 16) + wm * 4 + mi, kf = nt * (WBN / 64) + wn;
-                    relu2_store(r, wg, wave, rf, kf, nt, wn == 0, "gemm_relu2_q8 output");
+                    relu2_store(r, wg, wave, rf, kf, nt, false, "gemm_relu2_q8 output");
                 }
+                // the row scales: lane l of a wn == 0 wave stores row l of the wave's 64 (row
+                // group l / 16) when that fragment row exists
+                for (int lane = 0; lane < 64 && wn == 0; ++lane)
+                    if (mt * (BM / 16) + wm * 4 + (lane >> 4) < p.MF)
+                        r.store(SXO, sxo_index(mt * BM + wm * 64 + lane, p.n_nt, nt) * 4, 4, wg, wave, lane,
+                                "gemm_relu2_q8 row scales");
             }
         }
     }

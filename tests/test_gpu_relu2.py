@@ -93,6 +93,7 @@ def test_quantize_relu2_matches_oracle(nxg, orc, torch, dev, act_max):
 # (T, n_in, n_out) for c_fc -> relu^2 -> int8; n_out % 32 == 0, n_in % 256 == 0
 RELU2_SHAPES = [(4096, 1024, 2304),   # the MLP's c_fc, 4 blocks, 9 column tiles
                 (9000, 512, 1216),    # 2 blocks, ragged rows, a 192-column last tile, several tiles per workgroup
+                (9000, 256, 1216),    # the same with one block per tile (its own tile walk)
                 (777, 512, 320),      # ragged rows, a 64-column last tile, KSo = 5
                 (33, 256, 96),        # one row tile, n_out % 64 = 32
                 (1, 1024, 256)]
