@@ -2551,12 +2551,14 @@ __device__ __forceinline__ void rows_transpose(int (&d)[4]) {
 // computing the same 64 x 64 piece as in gemm_k256, over a 128 x 256 tile -- exactly one
 // 256-input block of the next linear, so a row's block amax is reduced here (over the
 // lanes of a wave, then over the 4 waves through LDS) and each wave stores whole 1 KiB
-// activation fragments; the fp32 rows are never written. The k-step schedule is
-// gemm_k256's: ring slot g % 4; after k-step g's barrier each wave loads its A fragment
-// and its 2 B fragments of k-step g + 3, the last three k-steps of a tile loading the
-// first three of the next; constant waits (6 later loads; 7 on waves 0 and 1 at the two
-// k-steps whose later loads include their scale loads). The block scales have an LDS
-// area of their own.
+// activation fragments; the fp32 rows are never written. The k-step schedule: k-step g
+// lives in ring slot g % 4 and is read into registers one step ahead (two operand sets).
+// Step g's barrier publishes k-step g + 1 and certifies that every wave has read k-step g,
+// so each wave then loads its A fragment and its 2 B fragments of k-step g + 4 into slot
+// g % 4 (the last four k-steps of a tile load the first four of the next), reads k-step
+// g + 1 from LDS among k-step g's MFMAs, and runs them; constant waits (6 later loads; 7
+// on waves 0 and 1 at the two k-steps whose later loads include their scale loads). The
+// block scales have an LDS area of their own.
 template <int ACT_MAX>
 __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
     __shared__ __attribute__((aligned(1024))) int8_t ring[4 * WSLOT];
@@ -2598,29 +2600,26 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
         dma16s(r.w0, vo, m + 8 * FRAG);
         dma16s(r.w1, vo, m + 16 * FRAG);
     };
-    auto arrive = [&](int j) {
-        if ((j == 1 || j == 2) && wave < 2) wait_vm<7>();
-        else wait_vm<6>();
-        lds_barrier();
-    };
 
     v4i acc[4][4];
     float f[4][4][4];
-    auto mma = [&](int j, bool first) {
+    v4i oa[2][4], ob[2][4];                          // operand sets: k-step g in set g % 2
+    auto rd = [&](int j, int set) {
         const int8_t * slot = ring + j * WSLOT;
-        v4i a[4], b[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            a[i] = *reinterpret_cast<const v4i *>(slot + (wm * 4 + i) * FRAG + lane * 16);
-            b[i] = *reinterpret_cast<const v4i *>(slot + (8 + wn * 4 + i) * FRAG + lane * 16);
+            oa[set][i] = *reinterpret_cast<const v4i *>(slot + (wm * 4 + i) * FRAG + lane * 16);
+            ob[set][i] = *reinterpret_cast<const v4i *>(slot + (8 + wn * 4 + i) * FRAG + lane * 16);
         }
+    };
+    auto mm = [&](int set, bool first, int m0, int m1) {
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
+        for (int mi = m0; mi < m1; ++mi)
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni)
                 acc[mi][ni] = first
-                    ? __builtin_amdgcn_mfma_i32_16x16x64_i8(b[ni], a[mi], v4i{0, 0, 0, 0}, 0, 0, 0)
-                    : __builtin_amdgcn_mfma_i32_16x16x64_i8(b[ni], a[mi], acc[mi][ni], 0, 0, 0);
+                    ? __builtin_amdgcn_mfma_i32_16x16x64_i8(ob[set][ni], oa[set][mi], v4i{0, 0, 0, 0}, 0, 0, 0)
+                    : __builtin_amdgcn_mfma_i32_16x16x64_i8(ob[set][ni], oa[set][mi], acc[mi][ni], 0, 0, 0);
     };
 
     {
@@ -2628,7 +2627,9 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
         issue(r0, 0, 0);
         issue(r0, 1, 1);
         issue(r0, 2, 2);
+        issue(r0, 3, 3);
         wait_vm<0>();
+        lds_barrier();
     }
     // The tile walk, instantiated for one 256-input block per tile and for several, so that
     // whether a block's fold starts from +0 is static in every block.
@@ -2638,12 +2639,6 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
             const int tile = walk.tile(it);
             const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
             const frag_rows cur = rows_of(it), nxt = rows_of(it + 1);
-            // the load that k-step j of block B issues (ring_prefetch: this tile's k-step
-            // 4B + 3 + j, or in the last block the next tile's k-step j - 1)
-            auto prefetch = [&](int B, int j, auto last_tag) {
-                const ring_load l = ring_prefetch(it, B, j, decltype(last_tag)::value);
-                issue(l.pos == it ? cur : nxt, l.ks, l.slot);
-            };
             // Scale loads of block B (B * sstep bytes on): wave 0 lane l < 32 the sx of row
             // group l, wave 0 lane l >= 32 the sw of columns 4(l-32)..+3, wave 1 lane l < 32
             // the sw of columns 128 + 4l..+3; lane l lands at scl + 16 l (+ 1024 on wave 1).
@@ -2657,30 +2652,37 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                 sstep = (size_t) p.NP * sizeof(float);
             }
             const int tbase = mt * BM + wm * 64;
+            rd(0, 0);                                // the tile's k-step 0 (slots 0..3 published)
 
             auto run_block = [&](int B, auto last_tag, auto first_tag) {
                 constexpr bool last = decltype(last_tag)::value, first = decltype(first_tag)::value;
-                // k-step 4B (slot 0). In block 0 k-steps 0..2 are already in LDS.
-                if (!first) arrive(0); else lds_barrier();
-                prefetch(B, 0, last_tag);
-                if (wave == 0) {
-                    dma16l(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl_lds);
-                } else if (wave == 1 && lane < 32) {
-                    dma16l(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl_lds + 1024);
-                }
-                mma(0, true);
-                // k-step 4B + 1 (slot 1)
-                if (!first) arrive(1); else lds_barrier();
-                prefetch(B, 1, last_tag);
-                mma(1, false);
-                // k-step 4B + 2 (slot 2)
-                if (!first) arrive(2); else lds_barrier();
-                prefetch(B, 2, last_tag);
-                mma(2, false);
-                // k-step 4B + 3 (slot 3); the block's scales arrive with it
-                arrive(3);
-                prefetch(B, 3, last_tag);
-                mma(3, false);
+                // Step s (k-step g = 4B + s, in registers since step s - 1): publish k-step g + 1
+                // (its DMA, issued 3 steps ago, waited; every wave done reading k-step g), load
+                // k-step g + 4 into slot s, read k-step g + 1 into the other operand set, then
+                // k-step g's MFMAs. The tile's last step reads nothing ahead.
+                auto step = [&](auto s_tag) {
+                    constexpr int s = decltype(s_tag)::value;
+                    if ((s == 1 || s == 2) && wave < 2) wait_vm<7>();
+                    else wait_vm<6>();
+                    lds_barrier();
+                    if (last) issue(nxt, s, s);
+                    else      issue(cur, 4 * B + 4 + s, s);
+                    if (s == 0) {
+                        if (wave == 0) {
+                            dma16l(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl_lds);
+                        } else if (wave == 1 && lane < 32) {
+                            dma16l(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl_lds + 1024);
+                        }
+                    }
+                    // half of the MFMAs first: their A operands are then free for the next set
+                    mm(s & 1, s == 0, 0, 3);
+                    if (!(last && s == 3)) rd((s + 1) & 3, (s + 1) & 1);
+                    mm(s & 1, s == 0, 3, 4);
+                };
+                step(std::integral_constant<int, 0>{});
+                step(std::integral_constant<int, 1>{});
+                step(std::integral_constant<int, 2>{});
+                step(std::integral_constant<int, 3>{});
 
                 // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
                 float sxv[4];

@@ -422,6 +422,7 @@ void replay_relu2_q8(replay & r) {
                 issue(r0, 0, 0);
                 issue(r0, 1, 1);
                 issue(r0, 2, 2);
+                issue(r0, 3, 3);
             }
             for (int it = 0; it < walk.count && !r.status; ++it) {
                 const int tile = walk.tile(it);
@@ -430,8 +431,10 @@ void replay_relu2_q8(replay & r) {
                 for (int B = 0; B < nb; ++B) {
                     const bool last = B == nb - 1;
                     for (int j = 0; j < 4; ++j) {
-                        const ring_load l = ring_prefetch(it, B, j, last);
-                        issue(rows_of(l.pos), l.ks, l.slot);
+                        // step j: k-step 4B + 4 + j into slot j, or in the last block the next
+                        // tile's k-step j
+                        if (last) issue(rows_of(it + 1), j, j);
+                        else      issue(rows_of(it), 4 * B + 4 + j, j);
                         if (j == 0 && (wave == 0 || wave == 1)) {
                             for (int lane = 0; lane < (wave == 0 ? 64 : 32); ++lane) {
                                 if (wave == 0 && lane < 32) {
