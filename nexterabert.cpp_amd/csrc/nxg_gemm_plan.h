@@ -165,17 +165,19 @@ NXG_HD size_t sxo_index(int t, int n_nt, int nt) { return sx_index(t, n_nt, nt);
 
 // --- the k-step schedule of gemm_k256 and gemm_relu2_q8 -----------------------------
 
-// k-step g of a workgroup's walk lives in ring slot g % 4. At k-step j (0..3) of block B
-// of walk position it, after that k-step's barrier, each wave loads the k-step three
-// ahead: k-step 4B + 3 + j of the same tile, or, in the tile's last block (last), k-step
-// j - 1 of the next walk position (clamped to the last tile by the caller).
+// k-step g of a workgroup's walk lives in ring slot g % 4 and is read into registers one
+// step ahead. At step s (0..3) of block B of walk position it, after that step's barrier,
+// each wave loads the k-step four ahead into slot s: k-step 4B + 4 + s of the same tile,
+// or, in the tile's last block (last), k-step s of the next walk position (clamped to the
+// last tile by the caller). With stage3 (gemm_k256, whose output is staged in slot 3)
+// the last step loads nothing (pos < 0): the next tile's start loads its k-step 3.
 struct ring_load {
     int pos, ks, slot;
 };
-NXG_HD ring_load ring_prefetch(int it, int B, int j, bool last) {
-    if (j == 0) return ring_load{ it, 4 * B + 3, 3 };
-    if (last) return ring_load{ it + 1, j - 1, j - 1 };
-    return ring_load{ it, 4 * B + 3 + j, j - 1 };
+NXG_HD ring_load ring_prefetch(int it, int B, int s, bool last, bool stage3) {
+    if (!last) return ring_load{ it, 4 * B + 4 + s, s };
+    if (stage3 && s == 3) return ring_load{ -1, 0, 3 };
+    return ring_load{ it + 1, s, s };
 }
 
 // --- the launch plan ----------------------------------------------------------------

@@ -2066,16 +2066,18 @@ __device__ __forceinline__ void dma16s(const int8_t * base, uint32_t voff, uint3
 // schedule that has no data-dependent branches inside a tile:
 //  - k-step g of the walk lives in ring slot g % 4; because a tile has a multiple
 //    of 4 k-steps, the slot of each k-step of a block is a compile-time constant;
-//  - at k-step g (after its barrier) each wave loads its 4 fragments of k-step
-//    g + 3, the last three k-steps of a tile loading the first three of the next
-//    tile (past the last tile, the last tile again: harmless re-reads that keep the
-//    counts constant); wave 0 adds block B's scales at k-step 4B;
+//  - a k-step is read from LDS one step ahead, into the second of two operand sets:
+//    the barrier of step g publishes k-step g + 1 and certifies that every wave has
+//    read k-step g, so each wave then loads its 4 fragments of k-step g + 4 into slot
+//    g % 4 and reads k-step g + 1 among k-step g's MFMAs; the last block loads the
+//    next tile's k-steps 0..2 (past the last tile, the last tile again: harmless
+//    re-reads that keep the counts constant); wave 0 adds block B's scales at k-step 4B;
 //  - the wait at each k-step is therefore a constant vmcnt: 8, or 9 on wave 0 for
 //    the two k-steps whose later loads include its scale load;
-//  - the output phase issues its stores at once (they write slot 3, free after the
-//    tile's last barrier); vmcnt counts the stores too, so the next tile's first
-//    k-step waits for every outstanding operation (its three prefetched k-steps and
-//    the stores) before the constant counts resume.
+//  - the output phase issues its stores at once (they write slot 3, which the last
+//    block leaves unloaded); vmcnt counts the stores too, so the next tile starts by
+//    waiting for every outstanding operation (its k-steps 0..2 and the stores), then
+//    loads its k-step 3 into slot 3, and the constant counts resume.
 // The residual rows are loaded after the tile's last MFMAs, under the last epilogue.
 template <bool RES>
 __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
@@ -2119,31 +2121,26 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
         dma16s(r.w0, vo, m + 8 * FRAG);
         dma16s(r.w1, vo, m + 12 * FRAG);
     };
-    // Waits for k-step j of a block (j = 1, 2: wave 0 has its scale load among the
-    // later ones), then the barrier that publishes the slot to all waves.
-    auto arrive = [&](int j) {
-        if ((j == 1 || j == 2) && wave == 0) wait_vm<9>();
-        else wait_vm<8>();
-        lds_barrier();
-    };
 
     v4i acc[4][4];
     float f[4][4][4];
-    auto mma = [&](int j, bool first) {
+    v4i oa[2][4], ob[2][4];                          // operand sets: k-step g in set g % 2
+    auto rd = [&](int j, int set) {
         const int8_t * slot = ring + j * SLOT;
-        v4i a[4], b[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            a[i] = *reinterpret_cast<const v4i *>(slot + (wm * 4 + i) * FRAG + lane * 16);
-            b[i] = *reinterpret_cast<const v4i *>(slot + (8 + wn * 4 + i) * FRAG + lane * 16);
+            oa[set][i] = *reinterpret_cast<const v4i *>(slot + (wm * 4 + i) * FRAG + lane * 16);
+            ob[set][i] = *reinterpret_cast<const v4i *>(slot + (8 + wn * 4 + i) * FRAG + lane * 16);
         }
+    };
+    auto mm = [&](int set, bool first, int m0, int m1) {
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
+        for (int mi = m0; mi < m1; ++mi)
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni)
                 acc[mi][ni] = first
-                    ? __builtin_amdgcn_mfma_i32_16x16x64_i8(b[ni], a[mi], v4i{0, 0, 0, 0}, 0, 0, 0)
-                    : __builtin_amdgcn_mfma_i32_16x16x64_i8(b[ni], a[mi], acc[mi][ni], 0, 0, 0);
+                    ? __builtin_amdgcn_mfma_i32_16x16x64_i8(ob[set][ni], oa[set][mi], v4i{0, 0, 0, 0}, 0, 0, 0)
+                    : __builtin_amdgcn_mfma_i32_16x16x64_i8(ob[set][ni], oa[set][mi], acc[mi][ni], 0, 0, 0);
     };
 
     {
@@ -2161,12 +2158,6 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
             const int tile = walk.tile(it);
             const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
             const frag_rows cur = rows_of(it), nxt = rows_of(it + 1);
-            // the load that k-step j of block B issues (ring_prefetch: this tile's k-step
-            // 4B + 3 + j, or in the last block the next tile's k-step j - 1)
-            auto prefetch = [&](int B, int j, auto last_tag) {
-                const ring_load l = ring_prefetch(it, B, j, decltype(last_tag)::value);
-                issue(l.pos == it ? cur : nxt, l.ks, l.slot);
-            };
             // wave 0's scale loads: lane l < 32 the sx of row group l of the tile, lane
             // l >= 32 the sw of columns 4(l-32)..+3; block B adds B * sstep bytes.
             const float * ssrc;
@@ -2182,6 +2173,13 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
             const int rrow = lane >> 4, rcol = 4 * (lane & 15);
             const int tbase = mt * BM + wm * 64, ncol = nt * BN + wn * 64 + rcol;
             const bool col_ok = ncol < p.N;
+            // Tile start: every outstanding operation (the tile's k-steps 0..2, loaded under the
+            // previous tile, and that tile's output stores) done, slot 3 free of the staged
+            // output, then k-step 3 into slot 3 and k-step 0 into operand set 0.
+            wait_vm<0>();
+            lds_barrier();
+            issue(cur, 3, 3);
+            rd(0, 0);
             // Residual rows of pieces m0 and m0 + 1 (half before the last epilogue, half
             // after it, to stay within the register budget), read once: nontemporal loads, which
             // leave L2 to the operand tiles. Full row tiles: a scalar row
@@ -2212,25 +2210,26 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
             // block, whose k-steps 1..3 load the next tile's first three.
             auto run_block = [&](int B, auto last_tag, auto first_tag) {
                 constexpr bool last = decltype(last_tag)::value, first = decltype(first_tag)::value;
-                // k-step 4B (slot 0). In block 0 k-steps 0..2 are already in LDS.
-                // block 0: the tile's first three k-steps were loaded under the previous tile; the
-                // previous tile's output stores went out after them, so wait for everything
-                if (!first) arrive(0); else { wait_vm<0>(); lds_barrier(); }
-                prefetch(B, 0, last_tag);
-                if (wave == 0) dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, ring + 3 * SLOT + SLOT_AB);
-                mma(0, true);
-                // k-step 4B + 1 (slot 1)
-                if (!first) arrive(1); else lds_barrier();
-                prefetch(B, 1, last_tag);
-                mma(1, false);
-                // k-step 4B + 2 (slot 2)
-                if (!first) arrive(2); else lds_barrier();
-                prefetch(B, 2, last_tag);
-                mma(2, false);
-                // k-step 4B + 3 (slot 3, with the block's scales)
-                arrive(3);
-                prefetch(B, 3, last_tag);
-                mma(3, false);
+                // Step s (k-step g = 4B + s, in registers since step s - 1): publish k-step g + 1
+                // and certify that every wave has read k-step g, load k-step g + 4 into slot s
+                // (in the last block the next tile's k-step s; its k-step 3 waits for the tile
+                // start, slot 3 staging the output), read k-step g + 1 among k-step g's MFMAs.
+                auto step = [&](auto s_tag) {
+                    constexpr int s = decltype(s_tag)::value;
+                    if ((s == 1 || s == 2) && wave == 0) wait_vm<9>();
+                    else wait_vm<8>();
+                    lds_barrier();
+                    const ring_load l = ring_prefetch(it, B, s, last, true);
+                    if (l.pos >= 0) issue(l.pos == it ? cur : nxt, l.ks, l.slot);
+                    if (s == 0 && wave == 0) dma16(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, ring + 3 * SLOT + SLOT_AB);
+                    mm(s & 1, s == 0, 0, 3);
+                    if (!(last && s == 3)) rd((s + 1) & 3, (s + 1) & 1);
+                    mm(s & 1, s == 0, 3, 4);
+                };
+                step(std::integral_constant<int, 0>{});
+                step(std::integral_constant<int, 1>{});
+                step(std::integral_constant<int, 2>{});
+                step(std::integral_constant<int, 3>{});
                 if (RES && last) load_res(0);
 
                 // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
@@ -2665,8 +2664,8 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                     if ((s == 1 || s == 2) && wave < 2) wait_vm<7>();
                     else wait_vm<6>();
                     lds_barrier();
-                    if (last) issue(nxt, s, s);
-                    else      issue(cur, 4 * B + 4 + s, s);
+                    const ring_load l = ring_prefetch(it, B, s, last, false);
+                    issue(l.pos == it ? cur : nxt, l.ks, l.slot);
                     if (s == 0) {
                         if (wave == 0) {
                             dma16l(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl_lds);

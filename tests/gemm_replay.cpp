@@ -131,11 +131,12 @@ void replay_k256(replay & r, bool res) {
                 const int tile = walk.tile(it);
                 const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
                 if (tile >= p.G) r.failf(1, "gemm_k256: workgroup %d walks tile %d of %d", wg, tile, p.G);
+                issue(rows_of(it), 3, 3);        // the tile start: its k-step 3 into slot 3
                 for (int B = 0; B < nb; ++B) {
                     const bool last = B == nb - 1;
                     for (int j = 0; j < 4; ++j) {
-                        const ring_load l = ring_prefetch(it, B, j, last);
-                        issue(rows_of(l.pos), l.ks, l.slot);
+                        const ring_load l = ring_prefetch(it, B, j, last, true);
+                        if (l.pos >= 0) issue(rows_of(l.pos), l.ks, l.slot);
                         if (j == 0 && wave == 0) {
                             // the block's scales, lane l at ring + 3 SLOT + SLOT_AB + 16 l
                             for (int lane = 0; lane < 64; ++lane) {
@@ -431,10 +432,8 @@ void replay_relu2_q8(replay & r) {
                 for (int B = 0; B < nb; ++B) {
                     const bool last = B == nb - 1;
                     for (int j = 0; j < 4; ++j) {
-                        // step j: k-step 4B + 4 + j into slot j, or in the last block the next
-                        // tile's k-step j
-                        if (last) issue(rows_of(it + 1), j, j);
-                        else      issue(rows_of(it), 4 * B + 4 + j, j);
+                        const ring_load l = ring_prefetch(it, B, j, last, false);
+                        issue(rows_of(l.pos), l.ks, l.slot);
                         if (j == 0 && (wave == 0 || wave == 1)) {
                             for (int lane = 0; lane < (wave == 0 ? 64 : 32); ++lane) {
                                 if (wave == 0 && lane < 32) {
