@@ -2673,7 +2673,8 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                             dma16l(reinterpret_cast<const char *>(ssrc) + (size_t) B * sstep, scl_lds + 1024);
                         }
                     }
-                    // half of the MFMAs first: their A operands are then free for the next set
+                    // three quarters of the MFMAs first: their A operands are then free for the next
+                    // set (earlier, the two sets do not fit in the register budget)
                     mm(s & 1, s == 0, 0, 3);
                     if (!(last && s == 3)) rd((s + 1) & 3, (s + 1) & 1);
                     mm(s & 1, s == 0, 3, 4);
