@@ -2737,13 +2737,15 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
                 // groups. With every maximum of the wave finite (the usual case) each value f * inv
                 // lies in [0, ACT_MAX + 1/2), so CVTPS2DQ and the saturating packs reduce to
                 // round-to-nearest-even, which v_cvt_pk_u8_f32 does while packing the byte. An
-                // infinite maximum takes quant1 (NaN -> 0x80000000).
+                // infinite maximum, or one so small (below ACT_MAX / FLT_MAX, denormals
+                // included) that inv overflows to +Inf, takes quant1: there x * inv is Inf or
+                // NaN, which CVTPS2DQ turns into 0x80000000 (u8 0) for every value of the row.
                 const int tl = tbase + lane;
                 const v4f a4 = *reinterpret_cast<const v4f *>(am + (wm * 64 + lane) * 4);
                 const float rmax = tl < p.T ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
                 const float amax_l = rmax * rmax;
                 const float inv_l = amax_l > 0.0f ? (float) ACT_MAX / amax_l : 0.0f;
-                const bool fast = __builtin_amdgcn_ballot_w64(!(amax_l < INFINITY)) == 0;
+                const bool fast = __builtin_amdgcn_ballot_w64(!(amax_l < INFINITY) || !(inv_l < INFINITY)) == 0;
                 int invs[4] = { __float_as_int(inv_l), __float_as_int(inv_l), __float_as_int(inv_l), __float_as_int(inv_l) };
                 rows_transpose(invs);                        // invs[mi]: row group mi, row lane % 16
                 if (wn == 0 && mt * (BM / 16) + wm * 4 + (lane >> 4) < p.MF)
@@ -3686,6 +3688,36 @@ int32_t nxg_linear_i8_relu2_q8(const nxg_weight * W, const int8_t * q, const flo
     int32_t T = 0;
     const int32_t rc = packed_rows(cu_offsets, n_seqs, T);
     return rc ? rc : nxg_linear_i8_relu2_q8_rows(W, q, sx, T, act_max, q_out, sx_out, stream);
+}
+
+const char * nxg_gemm_kernel_name(int32_t T, int32_t n_in, int32_t n_out, int32_t flags, int32_t cus) {
+    const bool res = flags & NXG_GEMM_RESIDUAL, relu2 = flags & NXG_GEMM_RELU2, sums = flags & NXG_GEMM_SUMS;
+    if (T <= 0 || n_in <= 0 || n_in % 32 != 0 || n_out <= 0 || (relu2 && (res || sums)) || (res && sums)) return nullptr;
+    if (relu2 && (n_in % 256 != 0 || n_out % 32 != 0)) return nullptr;
+    if (cus <= 0) {
+        if (check_device() != NXG_OK) return nullptr;
+        cus = device_cus();
+    }
+    gemm_plan pl;
+    if (!plan_gemm(T, n_in, n_out, sums, relu2, cus, pl)) return nullptr;
+    const bool a63 = flags & NXG_GEMM_ACT63;
+    switch (pl.kind) {
+    case GEMM_RELU2_SMALL: return a63 ? "gemm_relu2_small<63>" : "gemm_relu2_small<127>";
+    case GEMM_RELU2_Q8:    return a63 ? "gemm_relu2_q8<63>" : "gemm_relu2_q8<127>";
+    case GEMM_SMALL: {
+        static const char * const names[2][2][2] = {
+            { { "gemm_small<2, false, false>", "gemm_small<2, false, true>" },
+              { "gemm_small<2, true, false>", "gemm_small<2, true, true>" } },
+            { { "gemm_small<4, false, false>", "gemm_small<4, false, true>" },
+              { "gemm_small<4, true, false>", "gemm_small<4, true, true>" } } };
+        return names[pl.fn == 4][res][pl.k256];
+    }
+    case GEMM_SUMS:  return pl.k256 ? "gemm_kernel<false, true, true>" : "gemm_kernel<false, true, false>";
+    case GEMM_K256:  return res ? "gemm_k256<true>" : "gemm_k256<false>";
+    case GEMM_GENERAL: break;
+    }
+    if (res) return pl.k256 ? "gemm_kernel<true, false, true>" : "gemm_kernel<true, false, false>";
+    return pl.k256 ? "gemm_kernel<false, false, true>" : "gemm_kernel<false, false, false>";
 }
 
 int32_t nxg_linear_i8_block_sums(const nxg_weight * W, const int8_t * q, int32_t T, int32_t * sums, void * stream) {

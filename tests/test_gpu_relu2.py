@@ -180,6 +180,43 @@ def test_linear_relu2_q8_overflowing_rows(nxg, orc, torch, dev):
         assert ((bits(s) == bits(rsx_ref)) | (np.isnan(s) & np.isnan(rsx_ref))).all(), f"act_max={act_max}"
 
 
+def test_linear_relu2_q8_tiny_row_maxima(nxg, orc, torch, dev):
+    """Rows whose relu^2 maximum is positive but below ACT_MAX / FLT_MAX (normal and
+    denormal), so that inv = ACT_MAX / amax overflows to +Inf: the reference's CVTPS2DQ then
+    gives 0x80000000 for every value of the row (u8 0). Rows are scaled by powers of two, which
+    scale the quantized activations' sx and every fold step exactly, so the maxima land where
+    chosen (2^-62: just above the bound, inv finite; 2^-64, 2^-65: normal maxima below it;
+    2^-70: a denormal maximum; 2^-80: relu^2 underflows to 0). T >= 8192 keeps the
+    128 x 256 kernel; checked against the oracle chain and against the two-step path."""
+    say("linear_relu2_q8 with tiny row maxima")
+    rng = np.random.default_rng(12)
+    T, n_in, n_out = 8200, 1024, 512
+    x = rng.standard_normal((T, n_in)).astype(np.float32)
+    scaled = {5: -62, 6: -65, 70: -64, 3000: -70, 3001: -62, 6000: -80, 8195: -65}
+    for t, e in scaled.items():
+        x[t] *= np.float32(2.0 ** e)
+    W = make_weight(nxg, rng, n_in, n_out, std=0.05)
+    qa, q_ref, sx_ref = quant(nxg, torch, orc, x)
+    dw = nxg.DeviceWeight(W)
+    y_ref = orc.linear(W.w, W.scale, W.off, q_ref, sx_ref, simd=bool(orc.vnni_flavour()),
+                       n_threads=orc.default_threads())
+    r = orc.relu2(y_ref)
+    rmax = r[list(scaled)].max(axis=1)
+    assert (rmax[[1, 2, 3, 6]] > 0).all() and (rmax[[1, 2, 3, 6]] < 63 / np.finfo(np.float32).max).all()
+    assert rmax[3] < np.finfo(np.float32).tiny, "the case needs a denormal row maximum"
+    assert rmax[0] > 127 / np.finfo(np.float32).max and rmax[5] == 0
+    for act_max in (127, 63):
+        fused = nxg.linear_i8_relu2_q8(dw, qa, act_max)
+        two = nxg.quantize_rows_relu2(nxg.linear_i8(dw, qa), act_max)
+        r_ref, rsx_ref = orc.quantize_rows(r, act_max)
+        u8, sx = nxg.export_qact(fused)
+        torch.cuda.synchronize()
+        assert (r_ref[[6, 70, 3000, 8195]] == 0).all(), "the oracle maps these rows to u8 0"
+        assert (u8.cpu().numpy() == r_ref).all(), f"act_max={act_max}"
+        assert (bits(sx.cpu().numpy()) == bits(rsx_ref)).all(), f"act_max={act_max}"
+        assert torch.equal(fused.q, two.q) and torch.equal(fused.sx.view(torch.int32), two.sx.view(torch.int32))
+
+
 @pytest.mark.parametrize("n_in_fc", [1024, 96])
 def test_builder_mlp(nxg, orc, torch, dev, n_in_fc):
     """x + c_proj(relu(c_fc(h))^2): fused when n_in % 256 == 0, fp32 then quantize otherwise."""
