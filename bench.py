@@ -14,8 +14,15 @@ N(0, 0.02), Q8_0-encoded, expanded to int8 on the host; activations N(0, 1); all
 inputs are resident in HBM before timing starts.
 
 Output: one JSON line. `value` is int8 TOPS of the whole step (quantization
-included, 2 ops per MAC of the GEMMs); `roofline` describes the GEMM kernel from
-HIP events around every GEMM launch of the timed steps; `cpu_baseline` times the
+included, 2 ops per MAC of the GEMMs). HIP events around every launch of the timed
+steps give `rooflines_by_kernel` (one roofline object per kernel the step launches:
+algorithmic ops and bytes per launch, average launch time, the bound its intensity
+selects and the fraction of it reached), `roofline` (the GEMM kernel with the largest
+share of the step) and `shapes` (per GEMM shape, the fraction of its own roofline bound
+min(MFMA peak, intensity x HBM peak)). `linear_path_8192` is the same path at 8,192
+rows (one GPU's share of 65,536 rows over 8 GPUs) and `ragged_layer_32docs` one
+attention layer's linears over 32 packed documents (M = 32,935, Q4_K_M weights,
+cumulative offsets on every launch) beside the same rows as one sequence. `cpu_baseline` times the
 CPU oracle (the same path on VPDPBUSD, the reference's instruction) on a row
 sample on this host; `mfma_counters` gives each GEMM kind's MFMA-busy %, counted int8
 ops and shader clock from a rocprofv3 --pmc pass over the same workload, run as a
@@ -61,6 +68,9 @@ def LinearPath(nxg, M: int, **kw):
 
 
 def time_steps(path, steps: int, warmup: int):
+    """W untimed steps, then K steps with HIP events around every launch (on the launching
+    stream). Returns ms per step (events around the K steps), wall ms per step, GEMM ms per
+    step by output kind, quantize ms per step, and the event lists."""
     torch = path.torch
     for _ in range(warmup):
         path.step()
@@ -77,11 +87,131 @@ def time_steps(path, steps: int, warmup: int):
     wall = time.perf_counter() - t0
     total_ms = s0.elapsed_time(s1)
     gemm_ms = {}
-    for a, b, g, kind in gemm_ev:
+    for a, b, g, kind, rows, res in gemm_ev:
         k = "relu2" if kind == "relu2" else "fp32"
         gemm_ms[k] = gemm_ms.get(k, 0.0) + a.elapsed_time(b) / steps
-    quant_ms = sum(a.elapsed_time(b) for a, b in quant_ev)
-    return total_ms / steps, wall / steps * 1e3, gemm_ms, quant_ms / steps, gemm_ev
+    quant_ms = sum(e[0].elapsed_time(e[1]) for e in quant_ev)
+    return total_ms / steps, wall / steps * 1e3, gemm_ms, quant_ms / steps, gemm_ev, quant_ev
+
+
+RIDGE = PEAK_INT8_TOPS * 1e12 / (PEAK_HBM_GBS * 1e9)     # int8 ops per HBM byte
+
+
+def roofline_of(kernel: str, n_launch: int, ms_total: float, ops: int, nbytes: int, steps: int) -> dict:
+    """Roofline object of one kernel over n_launch launches taking ms_total together: the
+    MFMA peak when its algorithmic intensity (ops / bytes per launch) is above the ridge,
+    else HBM bandwidth. achieved = algorithmic ops (or bytes) per launch / average launch
+    time."""
+    avg_s = ms_total * 1e-3 / n_launch
+    ops_pl, bytes_pl = ops / n_launch, nbytes / n_launch
+    ai = ops / nbytes if nbytes else 0.0
+    if ops and ai >= RIDGE:
+        r = {"bound": "mfma", "achieved": round(ops_pl / avg_s / 1e12, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s"}
+    else:
+        r = {"bound": "hbm", "achieved": round(bytes_pl / avg_s / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    r["frac"] = round(r["achieved"] / r["peak"], 4)
+    r["traffic"] = None
+    r["kernel"] = kernel
+    r["launches_per_step"] = round(n_launch / steps, 2)
+    r["ms_per_step"] = round(ms_total / steps, 4)
+    r["per_launch"] = {"algorithmic_ops": int(ops_pl), "algorithmic_bytes": int(bytes_pl),
+                       "avg_us": round(avg_s * 1e6, 2), "arith_intensity": round(ai, 1),
+                       "int8_tops": round(ops_pl / avg_s / 1e12, 2), "gb_per_s": round(bytes_pl / avg_s / 1e9, 1)}
+    return r
+
+
+def kernel_rooflines(nxg, gemm_ev, quant_ev, steps: int) -> list:
+    """One roofline object per kernel the step launches (the GEMM kernel of each launch as
+    the launch plan picks it, nxg_gemm_kernel_name; the quantize kernel), most time first."""
+    from nexterabert_cpp_amd.encoder import gemm_bytes, quantize_bytes
+    acc = {}
+    for a, b, g, kind, rows, res in gemm_ev:
+        relu2 = kind == "relu2"
+        name = nxg.gemm_kernel_name(rows, g.n_in, g.n_out, residual=res, relu2=relu2)
+        d = acc.setdefault(name, [0, 0.0, 0, 0])
+        d[0] += 1
+        d[1] += a.elapsed_time(b)
+        d[2] += 2 * rows * g.n_in * g.n_out
+        d[3] += gemm_bytes(rows, g.n_in, g.n_out, relu2, res)
+    for a, b, rows, n_in, relu2 in quant_ev:
+        d = acc.setdefault(f"quantize_kernel<127, {int(relu2)}>", [0, 0.0, 0, 0])
+        d[0] += 1
+        d[1] += a.elapsed_time(b)
+        d[3] += quantize_bytes(rows, n_in)
+    out = [roofline_of(k, n, ms, ops, nb, steps) for k, (n, ms, ops, nb) in acc.items()]
+    return sorted(out, key=lambda r: -r["ms_per_step"])
+
+
+def shape_table(gemm_ev, steps: int) -> list:
+    """Per GEMM shape of the step: average launch time, int8 TOPS, and the shape's roofline
+    bound min(MFMA peak, AI x HBM peak) with the fraction of it reached."""
+    from nexterabert_cpp_amd.encoder import gemm_bytes
+    acc = {}
+    for a, b, g, kind, rows, res in gemm_ev:
+        relu2 = kind == "relu2"
+        k = (rows, g.n_in, g.n_out, bool(res), relu2)
+        d = acc.setdefault(k, [0, 0.0, g.name])
+        d[0] += 1
+        d[1] += a.elapsed_time(b)
+    out = []
+    for (rows, n_in, n_out, res, relu2), (n, ms, name) in acc.items():
+        ops = 2 * rows * n_in * n_out
+        nb = gemm_bytes(rows, n_in, n_out, relu2, res)
+        avg_us = ms * 1e3 / n
+        tops = ops / (avg_us * 1e-6) / 1e12
+        bound = min(PEAK_INT8_TOPS, ops / nb * PEAK_HBM_GBS / 1e3)
+        out.append({"shape": f"{rows}x{n_in}->{n_out}" + (" +res" if res else "") + (" relu2->int8" if relu2 else ""),
+                    "example": name.split(".")[-2] if "." in name else name,
+                    "launches_per_step": round(n / steps, 2), "avg_us": round(avg_us, 2),
+                    "int8_tops": round(tops, 1), "pct_of_mfma_peak": round(100 * tops / PEAK_INT8_TOPS, 2),
+                    "bound_tops": round(bound, 1), "frac_of_bound": round(tops / bound, 4)})
+    return sorted(out, key=lambda r: -r["avg_us"] * r["launches_per_step"])
+
+
+def path_line(nxg, path, steps: int, warmup: int, workload: str) -> dict:
+    """A linear-path workload other than the headline one: ms per step, int8 TOPS, tokens/s,
+    the per-shape table and the per-kernel rooflines."""
+    ms, wall_ms, gemm_ms, quant_ms, gemm_ev, quant_ev = time_steps(path, steps, warmup)
+    tops = path.ops / (ms * 1e-3) / 1e12
+    return {"workload": workload, "rows": path.M, "n_seqs": len(path.lengths), "gemm_launches": path.n_gemm,
+            "quantize_launches": path.n_quant, "ms_per_step": round(ms, 4), "int8_tops": round(tops, 2),
+            "pct_of_mfma_peak": round(100 * tops / PEAK_INT8_TOPS, 2),
+            "tokens_per_s": round(path.M / (ms * 1e-3), 1),
+            "gemm_ms_per_step": {k: round(v, 4) for k, v in gemm_ms.items()},
+            "quantize_ms_per_step": round(quant_ms, 4),
+            "shapes": shape_table(gemm_ev, steps), "kernels": kernel_rooflines(nxg, gemm_ev, quant_ev, steps)}
+
+
+# The ragged batch of 32 documents (lengths numpy.random.default_rng(1).integers(16, 2048, 32,
+# endpoint=True)), M = 32,935, through one attention layer's projections with Q4_K_M weights.
+RAGGED_LENGTHS = [977, 1056, 1551, 1948, 86, 309, 1689, 1944, 522, 649, 1782, 876, 571, 1698, 538, 847,
+                  1324, 1133, 190, 72, 1775, 1547, 1719, 1110, 1678, 686, 936, 1618, 267, 632, 268, 937]
+
+
+def ragged_layer_line(nxg, steps: int, warmup: int) -> dict:
+    """One attention layer's linears (fused QKV, c_gate, c_proj + residual, c_fc -> relu^2 ->
+    int8, mlp.c_proj + residual) over the packed 32-document batch, cu_offsets on every
+    launch, beside the same rows as one sequence with the same weights."""
+    from nexterabert_cpp_amd.encoder import EncoderLinearPath
+    lengths = [int(n) for n in np.random.default_rng(1).integers(16, 2048, 32, endpoint=True)]
+    assert lengths == RAGGED_LENGTHS
+    ragged = EncoderLinearPath(nxg, lengths, kinds=["attn"], preset="Q4_K_M")
+    r = path_line(nxg, ragged, steps, warmup,
+                  "one attention layer's 5 int8 linears (QKV fused) over 32 packed documents, Q4_K_M weights")
+    one = EncoderLinearPath(nxg, [ragged.M], kinds=["attn"], preset="Q4_K_M", weights=ragged.dev_weights)
+    # the packed batch against the same rows as one sequence: alternating, best of 3 each
+    t_ragged, t_one = [r["ms_per_step"]], []
+    for i in range(3):
+        t_one.append(time_steps(one, steps, warmup)[0])
+        if i < 2:
+            t_ragged.append(time_steps(ragged, steps, warmup)[0])
+    r["lengths"] = lengths
+    r["weights"] = "random N(0, 0.02); c_q, c_k, c_fc Q4_K; c_v, c_gate, c_proj, mlp.c_proj Q6_K; expanded to int8"
+    r["ragged_ms_best_of_3"] = round(min(t_ragged), 4)
+    r["one_sequence_same_rows_ms_best_of_3"] = round(min(t_one), 4)
+    r["ragged_over_one_sequence"] = round(min(t_ragged) / min(t_one), 4)
+    del ragged, one
+    return r
 
 
 def time_graph(path, steps: int, warmup: int):
@@ -343,22 +473,51 @@ def counter_pass(args) -> int:
     return 0
 
 
+def short_name(name: str) -> str:
+    """A profiler kernel name without return type, namespace and arguments:
+    "gemm_k256<true>", "quantize_kernel<127, 0>"."""
+    n = name.replace("(anonymous namespace)::", "").replace("void ", "", 1)
+    depth, out = 0, []
+    for ch in n:
+        if ch == "(" and depth == 0:
+            break
+        depth += ch == "<"
+        depth -= ch == ">"
+        out.append(ch)
+    return "".join(out).strip()
+
+
 def summarize_counters(csv_path: Path, cus: int, skip_first: int) -> dict:
-    """Per GEMM kind, from a counter_collection.csv of MFMA_COUNTERS: MFMA-busy % (the
-    MfmaUtil metric: busy cycles summed over all SIMDs / (GUI-active cycles of an XCD x
-    SIMDs)), the int8 ops the MFMAs counted (MOPS_I8 x 512), the shader clock (GUI-active
-    cycles of an XCD / dispatch time) and the ops rate against the peak at that clock.
-    The first skip_first dispatches of each kind (the warm-up step) are left out."""
+    """Per GEMM kind, and per GEMM kernel under "by_kernel", from a counter_collection.csv of
+    MFMA_COUNTERS: MFMA-busy % (the MfmaUtil metric: busy cycles summed over all SIMDs /
+    (GUI-active cycles of an XCD x SIMDs)), the int8 ops the MFMAs counted (MOPS_I8 x 512),
+    the shader clock (GUI-active cycles of an XCD / dispatch time) and the ops rate against
+    the peak at that clock. Rates are sums over the dispatches (total ops / total time, total
+    busy cycles / total cycles), not means of per-dispatch rates. The first skip_first
+    dispatches of each kind (the warm-up step) are left out."""
     import csv
     disp = {}
     for row in csv.DictReader(open(csv_path)):
         kind = gemm_class(row["Kernel_Name"])
         if kind is None:
             continue
-        d = disp.setdefault(int(row["Dispatch_Id"]), {"kind": kind, "name": row["Kernel_Name"]})
+        d = disp.setdefault(int(row["Dispatch_Id"]), {"kind": kind, "name": short_name(row["Kernel_Name"])})
         d[row["Counter_Name"]] = float(row["Counter_Value"])
         d["ns"] = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
     simds = 4 * cus
+
+    def summary(ds):
+        cyc = sum(d["GRBM_GUI_ACTIVE"] / N_XCC for d in ds)          # shader cycles of one XCD
+        ns = sum(d["ns"] for d in ds)
+        ops = sum(d["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512 for d in ds)
+        return {"dispatches": len(ds),
+                "mfma_busy_pct": round(100.0 * sum(d["SQ_VALU_MFMA_BUSY_CYCLES"] for d in ds) / (cyc * simds), 2),
+                "int8_ops_counted_per_launch": int(ops / len(ds)),
+                "clock_ghz": round(cyc / ns, 3),
+                "us_per_launch_profiled": round(ns / len(ds) / 1e3, 2),
+                "int8_tops_profiled": round(ops / ns / 1e3, 1),
+                "pct_of_peak_at_clock": round(100.0 * ops / (simds * INT8_OPS_PER_SIMD_CYCLE * cyc), 2)}
+
     res = {}
     for kind in ("fp32", "relu2"):
         ds = [disp[k] for k in sorted(disp) if disp[k]["kind"] == kind]
@@ -366,20 +525,10 @@ def summarize_counters(csv_path: Path, cus: int, skip_first: int) -> dict:
         ds = [d for d in ds if all(c in d for c in MFMA_COUNTERS) and d["ns"] > 0]
         if not ds:
             continue
-        busy = [100.0 * d["SQ_VALU_MFMA_BUSY_CYCLES"] / (d["GRBM_GUI_ACTIVE"] / N_XCC * simds) for d in ds]
-        ghz = [d["GRBM_GUI_ACTIVE"] / N_XCC / d["ns"] for d in ds]
-        ops = [d["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512 for d in ds]
-        tops = [o / d["ns"] / 1e3 for o, d in zip(ops, ds)]
-        at_clk = [100.0 * t * 1e12 / (simds * INT8_OPS_PER_SIMD_CYCLE * g * 1e9) for t, g in zip(tops, ghz)]
-        names = sorted({d["name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
-                        for d in ds})
-        res[kind] = {"kernels": names, "dispatches": len(ds),
-                     "mfma_busy_pct": round(statistics.mean(busy), 2),
-                     "int8_ops_counted_per_launch": int(statistics.mean(ops)),
-                     "clock_ghz": round(statistics.mean(ghz), 3),
-                     "us_per_launch_profiled": round(statistics.mean(d["ns"] for d in ds) / 1e3, 2),
-                     "int8_tops_profiled": round(statistics.mean(tops), 1),
-                     "pct_of_peak_at_clock": round(statistics.mean(at_clk), 2)}
+        r = summary(ds)
+        r["kernels"] = sorted({d["name"] for d in ds})
+        r["by_kernel"] = {n: summary([d for d in ds if d["name"] == n]) for n in r["kernels"]}
+        res[kind] = r
     return res
 
 
@@ -431,41 +580,50 @@ def mfma_counters(args, timeout_s: int = 240) -> dict:
 
 
 def pmc_summary(fetch_csv: str, write_csv: str, calib_mib: int, out_path: Path) -> dict:
-    """HBM traffic per launch of the GEMM and quantize kernels from two rocprofv3 --pmc
-    runs of this script (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by
-    what the same counter reads for the calibration copy of calib_mib MiB (a device to
-    device copy, dispatched by the HIP runtime as its copy-buffer kernel)."""
+    """HBM traffic per launch of each GEMM and quantize kernel from two rocprofv3 --pmc runs
+    of this script (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the
+    same counter reads for the calibration copy of calib_mib MiB (a device to device copy,
+    dispatched by the HIP runtime as its copy-buffer kernel). Per kernel name, and per class
+    (gemm_fp32, gemm_relu2, quant) as the mean over the class's launches."""
     import csv
 
     def per_kernel(path, counter):
-        vals = {"gemm_fp32": [], "gemm_relu2": [], "quant": [], "copy": []}
+        vals, copies = {}, []
         for row in csv.DictReader(open(path)):
             if row["Counter_Name"] != counter:
                 continue
             name, v = row["Kernel_Name"], float(row["Counter_Value"])
-            if "gemm_relu2_q8" in name or "gemm_relu2_small" in name:
-                vals["gemm_relu2"].append(v)
-            elif "gemm_k256" in name or "gemm_kernel" in name or "gemm_small" in name:
-                vals["gemm_fp32"].append(v)
-            elif "quantize_kernel" in name:
-                vals["quant"].append(v)
+            if gemm_class(name) or "quantize_kernel" in name:
+                vals.setdefault(short_name(name), []).append(v)
             elif "copy" in name.lower():
-                vals["copy"].append(v)
-        # the calibration copy is the largest copy dispatch (weight uploads are smaller)
-        return {k: ((max(v) if k == "copy" else sum(v) / len(v)) if v else None) for k, v in vals.items()}
+                copies.append(v)
+        return vals, (max(copies) if copies else None)   # the calibration copy is the largest copy
 
-    f = per_kernel(fetch_csv, "FETCH_SIZE")
-    w = per_kernel(write_csv, "WRITE_SIZE")
+    def cls(n):
+        c = gemm_class(n)
+        return {"fp32": "gemm_fp32", "relu2": "gemm_relu2"}.get(c, "quant")
+
+    f, fc = per_kernel(fetch_csv, "FETCH_SIZE")
+    w, wc = per_kernel(write_csv, "WRITE_SIZE")
     kib = calib_mib * 1024.0
-    fs, ws = kib / f["copy"], kib / w["copy"]
+    fs, ws = kib / fc, kib / wc
     res = {"fetch_scale": round(fs, 4), "write_scale": round(ws, 4),
-           "calibration": f"plain device copy of {calib_mib} MiB (reads and writes {calib_mib} MiB)"}
-    for k in ("gemm_fp32", "gemm_relu2", "quant"):
-        if f[k] is None or w[k] is None:
-            continue
-        res[k] = {"fetch_bytes_per_launch": int(f[k] * fs * 1024), "write_bytes_per_launch": int(w[k] * ws * 1024),
-                  "hbm_bytes_per_launch": int((f[k] * fs + w[k] * ws) * 1024),
-                  "raw_fetch_kib": round(f[k], 1), "raw_write_kib": round(w[k], 1)}
+           "calibration": f"plain device copy of {calib_mib} MiB (reads and writes {calib_mib} MiB)",
+           "by_kernel": {}}
+
+    def entry(fv, wv):
+        fm, wm = sum(fv) / len(fv), sum(wv) / len(wv)
+        return {"launches": len(fv), "fetch_bytes_per_launch": int(fm * fs * 1024),
+                "write_bytes_per_launch": int(wm * ws * 1024), "hbm_bytes_per_launch": int((fm * fs + wm * ws) * 1024),
+                "raw_fetch_kib": round(fm, 1), "raw_write_kib": round(wm, 1)}
+
+    for n in sorted(set(f) & set(w)):
+        res["by_kernel"][n] = entry(f[n], w[n])
+    for c in ("gemm_fp32", "gemm_relu2", "quant"):
+        fv = [v for n in f if cls(n) == c for v in f[n]]
+        wv = [v for n in w if cls(n) == c for v in w[n]]
+        if fv and wv:
+            res[c] = entry(fv, wv)
     out_path.write_text(json.dumps(res, indent=2) + "\n")
     return res
 
@@ -484,6 +642,8 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-encoder1024", action="store_true")
     ap.add_argument("--no-encoder", action="store_true", help="skip the whole-encoder timing")
+    ap.add_argument("--no-extra-lines", action="store_true",
+                    help="skip the M=8192 linear-path line and the ragged 32-document layer line")
     ap.add_argument("--encoder-long", default="8192,65536", metavar="T1,T2",
                     help="also time the whole encoder on one document of each of these lengths ('': none)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -531,53 +691,48 @@ def main() -> int:
     log(f"setup {time.perf_counter() - t0:.1f} s: M={args.rows}, {path.n_gemm} GEMMs ({path.n_relu2} with the "
         f"relu^2 -> int8 output) + {path.n_quant} quantizations per step, {path.ops / 1e12:.3f} T int8 ops")
 
-    ms, wall_ms, gemm_ms, quant_ms, gemm_ev = time_steps(path, args.steps, args.warmup)
+    ms, wall_ms, gemm_ms, quant_ms, gemm_ev, quant_ev = time_steps(path, args.steps, args.warmup)
     gemm_total = sum(gemm_ms.values())
     log(f"timed {args.steps} steps: {ms:.3f} ms/step (wall {wall_ms:.3f}), GEMMs {gemm_total:.3f} ms "
         f"({gemm_ms}), quantize {quant_ms:.3f} ms")
 
     value = path.ops / (ms * 1e-3) / 1e12
     gemm_tops = path.ops / (gemm_total * 1e-3) / 1e12
-    ridge = PEAK_INT8_TOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
 
-    def roofline(n_launch, ops, nbytes, ms_step, kernel):
-        avg_launch_s = ms_step * 1e-3 / n_launch
-        ops_pl, bytes_pl, ai = ops / n_launch, nbytes / n_launch, ops / nbytes
-        if ai >= ridge:
-            r = {"bound": "mfma", "achieved": round(ops_pl / avg_launch_s / 1e12, 2),
-                 "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s"}
-        else:
-            r = {"bound": "hbm", "achieved": round(bytes_pl / avg_launch_s / 1e9, 1),
-                 "peak": PEAK_HBM_GBS, "unit": "GB/s"}
-        r["frac"] = round(r["achieved"] / r["peak"], 4)
-        r["traffic"] = None
-        r["kernel"] = kernel
-        r["per_launch"] = {"algorithmic_ops": int(ops_pl), "algorithmic_bytes": int(bytes_pl),
-                           "avg_us": round(avg_launch_s * 1e6, 2), "arith_intensity": round(ai, 1),
-                           "int8_tops": round(ops_pl / avg_launch_s / 1e12, 2)}
-        return r
+    # One roofline per kernel; `roofline` is the GEMM kernel with the largest share of the step.
+    kernels = kernel_rooflines(nxg, gemm_ev, quant_ev, args.steps)
+    tr = json.loads(TRAFFIC_FILE.read_text()) if TRAFFIC_FILE.exists() else {}
+    use_traffic = args.rows == 65536 and not args.no_fuse and not args.no_fuse_mlp
+    for r in kernels:
+        by = (tr.get("by_kernel") or {}).get(r["kernel"])
+        if use_traffic and by:
+            r["traffic"] = by["hbm_bytes_per_launch"]
+            r["traffic_over_algorithmic"] = round(by["hbm_bytes_per_launch"] / r["per_launch"]["algorithmic_bytes"], 3)
+        for kind in ("fp32", "relu2"):
+            bk = ((counters or {}).get(kind) or {}).get("by_kernel", {}).get(r["kernel"])
+            if bk:
+                r["mfma_busy_pct"] = bk["mfma_busy_pct"]
+    roof = dict(next(r for r in kernels if not r["kernel"].startswith("quantize")))
+    if roof.get("traffic") is not None:
+        roof["traffic_source"] = (f"{TRAFFIC_FILE.relative_to(ROOT)}: rocprofv3 FETCH_SIZE x {tr['fetch_scale']} + "
+                                  f"WRITE_SIZE x {tr['write_scale']} per launch of this kernel in this workload")
+    roof_relu2 = next((r for r in kernels if r["kernel"].startswith("gemm_relu2")), None)
+    shapes = shape_table(gemm_ev, args.steps)
+    log(f"dominant kernel {roof['kernel']}: {roof['per_launch']['avg_us']} us/launch, frac {roof['frac']}")
 
-    # The dominant kernel: the fp32-output GEMM (most launches and most of the time).
-    n_fp32 = path.n_gemm - path.n_relu2
-    roof = roofline(n_fp32, path.ops_fp32, path.gemm_bytes, gemm_ms["fp32"], "gemm_k256 (nxg_linear_i8)")
-    if counters and "fp32" in counters:
-        roof["mfma_busy_pct"] = counters["fp32"]["mfma_busy_pct"]
-    if TRAFFIC_FILE.exists() and args.rows == 65536 and not args.no_fuse:
-        tr = json.loads(TRAFFIC_FILE.read_text())
-        if "gemm_fp32" in tr:
-            roof["traffic"] = tr["gemm_fp32"]["hbm_bytes_per_launch"]
-            roof["traffic_source"] = (f"{TRAFFIC_FILE.relative_to(ROOT)}: rocprofv3 FETCH_SIZE x {tr['fetch_scale']}"
-                                      f" + WRITE_SIZE x {tr['write_scale']} per fp32-output GEMM launch of this workload")
-    roof_relu2 = None
-    if path.n_relu2:
-        roof_relu2 = roofline(path.n_relu2, path.ops_relu2, path.relu2_bytes, gemm_ms["relu2"],
-                              "gemm_relu2_q8 (nxg_linear_i8_relu2_q8)")
-        if counters and "relu2" in counters:
-            roof_relu2["mfma_busy_pct"] = counters["relu2"]["mfma_busy_pct"]
-        if TRAFFIC_FILE.exists() and args.rows == 65536 and not args.no_fuse:
-            tr = json.loads(TRAFFIC_FILE.read_text())
-            if "gemm_relu2" in tr:
-                roof_relu2["traffic"] = tr["gemm_relu2"]["hbm_bytes_per_launch"]
+    m8k = None
+    if not args.no_extra_lines and args.rows != 8192:
+        p8 = LinearPath(nxg, 8192, fuse=not args.no_fuse, weights=path.dev_weights, fuse_mlp=not args.no_fuse_mlp)
+        m8k = path_line(nxg, p8, max(args.steps, 20), args.warmup,
+                        "all 140 encoder int8 projections, one 8192-token sequence (one GPU's share of 65,536 "
+                        "rows over 8 GPUs)")
+        log(f"M=8192: {m8k['ms_per_step']} ms/step, {m8k['int8_tops']} TOPS")
+        del p8
+    ragged = None
+    if not args.no_extra_lines:
+        ragged = ragged_layer_line(nxg, max(args.steps, 20), args.warmup)
+        log(f"ragged 32-document layer: {ragged['ms_per_step']} ms/step, {ragged['int8_tops']} TOPS, "
+            f"x{ragged['ragged_over_one_sequence']} of one sequence")
 
     enc = None
     if not args.no_encoder1024:
@@ -631,6 +786,10 @@ def main() -> int:
         "encoder": full,
         "roofline": roof,
         "roofline_relu2_q8": roof_relu2,
+        "rooflines_by_kernel": kernels,
+        "shapes": shapes,
+        "linear_path_8192": m8k,
+        "ragged_layer_32docs": ragged,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

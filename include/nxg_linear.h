@@ -378,6 +378,19 @@ NXG_API int32_t nxg_linear_i8_relu2_q8_rows(const nxg_weight * w, const int8_t *
 NXG_API int32_t nxg_linear_i8_block_sums(const nxg_weight * w, const int8_t * q, int32_t T,
                                          int32_t * sums, void * stream);
 
+/* Diagnostic, no counterpart in the reference (whose op_linear_i8 has one kernel): the
+ * kernel a GEMM of T rows, n_in inputs and n_out outputs launches, as the profiler names
+ * its template instance (e.g. "gemm_k256<true>"), for a device of `cus` compute units
+ * (cus <= 0: the current device, which must be a gfx950 GPU). flags: NXG_GEMM_RESIDUAL
+ * (nxg_linear_i8 with a residual), NXG_GEMM_RELU2 (nxg_linear_i8_relu2_q8; with
+ * NXG_GEMM_ACT63 for act_max 63), NXG_GEMM_SUMS (nxg_linear_i8_block_sums). A static
+ * string, or NULL for a shape or flag combination the entry points refuse. */
+#define NXG_GEMM_RESIDUAL 1
+#define NXG_GEMM_RELU2    2
+#define NXG_GEMM_SUMS     4
+#define NXG_GEMM_ACT63    8
+NXG_API const char * nxg_gemm_kernel_name(int32_t T, int32_t n_in, int32_t n_out, int32_t flags, int32_t cus);
+
 #ifdef __cplusplus
 }
 #endif

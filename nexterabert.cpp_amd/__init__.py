@@ -121,6 +121,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_linear_i8_block_sums": ([P, P, i32, P, P], i32),
         "nxg_linear_i8_relu2_q8": ([P, P, P, P, i32, i32, P, P, P], i32),
         "nxg_linear_i8_relu2_q8_rows": ([P, P, P, i32, i32, P, P, P], i32),
+        "nxg_gemm_kernel_name": ([i32, i32, i32, i32, i32], ctypes.c_char_p),
         # include/nxg_gguf.h
         "nxg_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(P)], i32),
         "nxg_gguf_close": ([P], None),
@@ -769,6 +770,21 @@ def linear_i8(weight: DeviceWeight, qa: QAct, residual=None, cu_offsets: Optiona
                                   out.data_ptr(), _stream_ptr(stream))
     _check(rc, "linear_i8")
     return out
+
+
+GEMM_RESIDUAL, GEMM_RELU2, GEMM_SUMS, GEMM_ACT63 = 1, 2, 4, 8
+
+
+def gemm_kernel_name(T: int, n_in: int, n_out: int, residual: bool = False, relu2: bool = False,
+                     act_max: int = 127, sums: bool = False, cus: int = 0) -> str:
+    """The kernel a GEMM of this shape launches, as the profiler names its template instance
+    (nxg_gemm_kernel_name); cus = 0 asks the current device."""
+    flags = ((GEMM_RESIDUAL if residual else 0) | (GEMM_RELU2 if relu2 else 0) | (GEMM_SUMS if sums else 0)
+             | (GEMM_ACT63 if relu2 and act_max == 63 else 0))
+    name = load_library().nxg_gemm_kernel_name(T, n_in, n_out, flags, cus)
+    if name is None:
+        raise ValueError(f"gemm_kernel_name: no kernel for T={T} n_in={n_in} n_out={n_out} flags={flags}")
+    return name.decode()
 
 
 def linear_i8_split(weight: DeviceWeight, qa: QAct, cols: Sequence[int], outs=None, stream=None):

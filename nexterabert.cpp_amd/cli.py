@@ -123,11 +123,11 @@ def bench(nxg, args, gguf) -> str:
         path.step(gemm_ev, quant_ev)
         torch.cuda.synchronize()
         per = {}
-        for a, b, grp, kind in gemm_ev:
+        for a, b, grp, kind, *_ in gemm_ev:
             k = f"GEMM {'relu^2 -> int8' if kind == 'relu2' else 'fp32 out'}"
             n, t = per.get(k, (0, 0.0))
             per[k] = (n + 1, t + a.elapsed_time(b))
-        per["quantize"] = (len(quant_ev), sum(a.elapsed_time(b) for a, b in quant_ev))
+        per["quantize"] = (len(quant_ev), sum(e[0].elapsed_time(e[1]) for e in quant_ev))
         total = sum(t for _, t in per.values())
         for k, (n, t) in per.items():
             lines.append(f"  {k:22s} {n:4d} launches  {t:8.3f} ms  {100 * t / total:5.1f}%")

@@ -24,6 +24,22 @@ import numpy as np
 from . import model
 
 
+def gemm_bytes(rows: int, n_in: int, n_out: int, relu2: bool, residual: bool) -> int:
+    """Algorithmic HBM bytes of one GEMM launch: int8 activations and their scales, int8
+    weights and their scales, then the output -- fp32 rows (+ the fp32 residual read), or
+    for the relu^2 -> int8 epilogue the next linear's int8 activations and scales."""
+    nb, nb_out = (n_in + 255) // 256, (n_out + 255) // 256
+    b = rows * n_in + 4 * rows * nb + n_out * n_in + 4 * n_out * nb
+    if relu2:
+        return b + rows * n_out + 4 * rows * nb_out
+    return b + 4 * rows * n_out * (2 if residual else 1)
+
+
+def quantize_bytes(rows: int, n_in: int) -> int:
+    """Algorithmic HBM bytes of one quantize_row pass: fp32 in, int8 and the scales out."""
+    return 5 * rows * n_in + 4 * rows * ((n_in + 255) // 256)
+
+
 class EncoderLinearPath:
     """Device buffers and the launch sequence of one forward of the linear path.
 
@@ -33,10 +49,15 @@ class EncoderLinearPath:
               quantize_rows_relu2)
     weights   device weights from an earlier path (same fuse setting), reused
     gguf      an open nxg.GGUF holding the encoder's int8 tensors (else random weights)
+    kinds     the block kind of each layer to run (default: the 18 blocks of the model);
+              e.g. ["attn"] for the linears of one attention layer
+    preset    block types of the random weights: "Q8_0" everywhere, or the "Q4_K_M" mix
+              (Q4_K, Q6_K where the _M rule wants more bits; tools/quantize.cpp:79-98)
     """
 
     def __init__(self, nxg, lengths: Sequence[int], fuse: bool = True, weights=None, seed: int = 0,
-                 fuse_mlp: bool = True, gguf=None):
+                 fuse_mlp: bool = True, gguf=None, kinds: Optional[Sequence[str]] = None,
+                 preset: str = "Q8_0"):
         import torch
         lengths = [int(n) for n in lengths]
         if not lengths or min(lengths) <= 0:
@@ -63,7 +84,8 @@ class EncoderLinearPath:
         self.relu2_bytes = 0      # ... of the c_fc -> relu^2 -> int8 GEMMs
         self.quant_bytes = 0      # ... of the standalone quantizations
         M = self.M
-        for l, kind in enumerate(model.BLOCK_TYPES):
+        self.preset = preset
+        for l, kind in enumerate(model.BLOCK_TYPES if kinds is None else kinds):
             steps = []
             seen = set()
             made = set()          # qact keys produced by a GEMM of this layer (relu^2 -> int8)
@@ -88,7 +110,7 @@ class EncoderLinearPath:
                     self.outs[okey] = torch.empty(rows, g.n_out, device="cuda")
                 wname = g.name if len(g.specs) == 1 else f"blocks.{l}.{g.name}"
                 if wname not in self.dev_weights:
-                    parts = [self._expand(nxg, s, rng, gguf, types) for s in g.specs]
+                    parts = [self._expand(nxg, s, rng, gguf, types, preset) for s in g.specs]
                     W = parts[0] if len(parts) == 1 else nxg.I8Weight(
                         np.concatenate([p.w for p in parts]),
                         np.ascontiguousarray(np.concatenate([p.scale for p in parts], 1)),
@@ -101,29 +123,27 @@ class EncoderLinearPath:
                 steps.append((key, first, wname, okey, res, g, gkind))
                 ops = 2 * rows * g.n_in * g.n_out
                 self.ops += ops
-                nb = (g.n_in + 255) // 256
-                nb_out = (g.n_out + 255) // 256
-                w_in = rows * g.n_in + 4 * rows * nb + g.n_out * g.n_in + 4 * g.n_out * nb
                 if gkind == "relu2":
                     self.ops_relu2 += ops
-                    self.relu2_bytes += w_in + rows * g.n_out + 4 * rows * nb_out
+                    self.relu2_bytes += gemm_bytes(rows, g.n_in, g.n_out, relu2=True, residual=False)
                 else:
                     self.ops_fp32 += ops
-                    self.gemm_bytes += w_in + 4 * rows * g.n_out * (2 if res else 1)
+                    self.gemm_bytes += gemm_bytes(rows, g.n_in, g.n_out, relu2=False, residual=res)
                 if gkind == "relu2_unfused":      # fp32 rows, then relu^2 + quantize_row
-                    self.quant_bytes += 5 * rows * g.n_out + 4 * rows * nb_out
+                    self.quant_bytes += quantize_bytes(rows, g.n_out)
                 if first:
-                    self.quant_bytes += 5 * rows * g.n_in + 4 * rows * nb
+                    self.quant_bytes += quantize_bytes(rows, g.n_in)
             self.layers.append(steps)
         self.n_gemm = sum(len(s) for s in self.layers)
         self.n_relu2 = sum(1 for s in self.layers for st in s if st[6] == "relu2")
         self.n_quant = sum(1 for s in self.layers for st in s if st[1] or st[6] == "relu2_unfused")
 
     @staticmethod
-    def _expand(nxg, spec, rng, gguf, types):
+    def _expand(nxg, spec, rng, gguf, types, preset):
         if gguf is None:
             rows_f = (0.02 * rng.standard_normal((spec.n_out, spec.n_in))).astype(np.float32)
-            return nxg.expand_weight(nxg.TYPE_Q8_0, nxg.quantize_weight(nxg.TYPE_Q8_0, rows_f), spec.n_in, spec.n_out)
+            t = model.file_type_of(spec.name, spec.n_in, preset)
+            return nxg.expand_weight(t, nxg.quantize_weight(t, rows_f), spec.n_in, spec.n_out)
         info = types.get(spec.name)
         if info is None:
             raise KeyError(f"{spec.name}: not in the GGUF file")
@@ -142,10 +162,11 @@ class EncoderLinearPath:
         self._mark = e                         # this launch's end is the next one's start
 
     def step(self, gemm_events: Optional[List] = None, quant_events: Optional[List] = None) -> None:
-        """One forward of the path on the current stream. With event lists, every GEMM
-        (tagged with its group and kind) and every quantization is bracketed by HIP events:
-        one event before the first launch and one after each launch, so consecutive launches
-        share the event between them."""
+        """One forward of the path on the current stream. With event lists, every GEMM and
+        every quantization is bracketed by HIP events: one event before the first launch and
+        one after each launch, so consecutive launches share the event between them. GEMM
+        entries are (start, end, group, kind, rows, residual), quantization entries (start,
+        end, rows, n_in, relu2)."""
         nxg = self.nxg
         if gemm_events is not None or quant_events is not None:
             if gemm_events is None or quant_events is None:
@@ -158,13 +179,14 @@ class EncoderLinearPath:
                 w = self.dev_weights[wname]
                 cu = self.cu_block if g.block_rows else self.cu
                 if first:
-                    self._timed(quant_events, lambda: nxg.quantize_rows(self.inputs[key], out=qa))
+                    self._timed(quant_events, lambda: nxg.quantize_rows(self.inputs[key], out=qa), qa.T, g.n_in, False)
                 if gkind == "relu2":
                     self._timed(gemm_events, lambda: nxg.linear_i8_relu2_q8(w, qa, cu_offsets=cu, out=self.qacts[okey]),
-                                g, gkind)
+                                g, gkind, qa.T, False)
                     continue
                 self._timed(gemm_events, lambda: nxg.linear_i8(w, qa, residual=self.residual if res else None,
-                                                               cu_offsets=cu, out=self.outs[okey]), g, gkind)
+                                                               cu_offsets=cu, out=self.outs[okey]), g, gkind, qa.T, res)
                 if gkind == "relu2_unfused":
                     rkey = (g.relu2_into, g.n_out, qa.T)
-                    self._timed(quant_events, lambda: nxg.quantize_rows_relu2(self.outs[okey], out=self.qacts[rkey]))
+                    self._timed(quant_events, lambda: nxg.quantize_rows_relu2(self.outs[okey], out=self.qacts[rkey]),
+                                qa.T, g.n_out, True)

@@ -90,6 +90,25 @@ def test_arguments_checked_before_device_work(nxg):
     assert L.nxg_attention_workspace_bytes(0, 2, 1, 8) == 0
 
 
+def test_gemm_kernel_name(nxg):
+    """The launch plan's kernel choice on a 256-CU device, as the profiler names it: the
+    encoder's shapes at 65,536 rows, few-row shapes, refusals."""
+    k = lambda *a, **kw: nxg.gemm_kernel_name(*a, cus=256, **kw)
+    assert k(65536, 1024, 2048) == "gemm_k256<false>"
+    assert k(65536, 2304, 1024, residual=True) == "gemm_k256<true>"
+    assert k(65536, 64, 1024, residual=True) == "gemm_kernel<true, false, false>"
+    assert k(65536, 1024, 2304, relu2=True) == "gemm_relu2_q8<127>"
+    assert k(65536, 1024, 2304, relu2=True, act_max=63) == "gemm_relu2_q8<63>"
+    assert k(1024, 1024, 2304, relu2=True) == "gemm_relu2_small<127>"
+    assert k(1024, 1024, 1024) == "gemm_small<2, false, true>"
+    assert k(1024, 320, 64, sums=True) == "gemm_kernel<false, true, false>"
+    L = nxg.load_library()
+    assert L.nxg_gemm_kernel_name(64, 1024, 2304, nxg.GEMM_RELU2 | nxg.GEMM_RESIDUAL, 256) is None
+    assert L.nxg_gemm_kernel_name(64, 96, 2304, nxg.GEMM_RELU2, 256) is None      # n_in % 256
+    assert L.nxg_gemm_kernel_name(64, 48, 64, 0, 256) is None
+    assert L.nxg_gemm_kernel_name(0, 64, 64, 0, 256) is None
+
+
 def test_device_calls_fail_loudly_without_gpu(nxg):
     import torch
     if torch.cuda.is_available():

@@ -52,6 +52,44 @@ def test_counter_summary(bench, tmp_path):
         assert r["int8_ops_counted_per_launch"] == pytest.approx(ops, rel=1e-9)
         assert r["pct_of_peak_at_clock"] == pytest.approx(25.0)
         assert r["us_per_launch_profiled"] == pytest.approx(100.0)
+        assert r["by_kernel"][name]["dispatches"] == 2
+        assert r["by_kernel"][name]["int8_tops_profiled"] == r["int8_tops_profiled"]
+
+
+def test_counter_rates_are_sums(bench, tmp_path):
+    """int8_tops_profiled is total ops / total time, not a mean of per-dispatch rates: a
+    dispatch twice as long at the same ops weighs in with its time."""
+    cus, simds, ghz = 256, 1024, 2.0
+    k256 = "void (anonymous namespace)::gemm_k256<false>((anonymous namespace)::gemm_params)"
+    rows = []
+    for ns in (100_000, 100_000, 100_000, 200_000):      # first is the warm-up quarter
+        gui = ghz * ns * bench.N_XCC
+        rows.append((k256, ns, {"SQ_VALU_MFMA_BUSY_CYCLES": 0.2 * gui / bench.N_XCC * simds,
+                                "SQ_INSTS_VALU_MFMA_MOPS_I8": 1e12 / 512, "GRBM_GUI_ACTIVE": gui}))
+    _write(tmp_path / "c.csv", rows)
+    r = bench.summarize_counters(tmp_path / "c.csv", cus, skip_first=1)["fp32"]
+    assert r["dispatches"] == 3
+    assert r["int8_tops_profiled"] == pytest.approx(3e12 / 400_000 / 1e3, rel=1e-3)   # 7500, not 8333
+    assert r["mfma_busy_pct"] == pytest.approx(20.0)
+
+
+def test_short_name(bench):
+    assert bench.short_name("void (anonymous namespace)::gemm_k256<true>((anonymous namespace)::gemm_params)") \
+        == "gemm_k256<true>"
+    assert bench.short_name("void (anonymous namespace)::quantize_kernel<127, 0>(float const*, int, int)") \
+        == "quantize_kernel<127, 0>"
+    assert bench.short_name("void (anonymous namespace)::gemm_small<2, false, true>((anonymous namespace)::"
+                            "gemm_params)") == "gemm_small<2, false, true>"
+
+
+def test_roofline_of(bench):
+    # 10 launches of 1 ms each, 2e12 ops and 1e9 bytes per launch: AI 2000 > ridge -> MFMA bound
+    r = bench.roofline_of("k", 10, 10.0, 2e13, 1e10, 5)
+    assert r["bound"] == "mfma" and r["achieved"] == pytest.approx(2000.0) and r["frac"] == pytest.approx(0.4)
+    assert r["launches_per_step"] == 2 and r["per_launch"]["avg_us"] == pytest.approx(1000.0)
+    # no ops (a quantize pass): HBM bound, 1e9 bytes per 1 ms launch = 1000 GB/s
+    r = bench.roofline_of("q", 10, 10.0, 0, 1e10, 5)
+    assert r["bound"] == "hbm" and r["achieved"] == pytest.approx(1000.0) and r["frac"] == pytest.approx(0.125)
 
 
 def test_gemm_class(bench):
