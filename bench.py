@@ -449,7 +449,7 @@ INT8_OPS_PER_SIMD_CYCLE = 2048  # v_mfma_i32_32x32x32_i8: 65,536 ops in 32 cycle
 
 
 def gemm_class(name: str):
-    if "gemm_relu2_q8" in name or "gemm_relu2_small" in name:
+    if "gemm_relu2_q8" in name or "gemm_relu2_small" in name or "gemm_relu2_rt" in name:
         return "relu2"
     if "gemm_k256" in name or "gemm_kernel" in name or "gemm_small" in name:
         return "fp32"

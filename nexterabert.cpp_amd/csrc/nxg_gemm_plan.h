@@ -35,6 +35,9 @@
 #ifndef NXG_RELU2_SMALL_MAX_WAVES_PER_CU
 #define NXG_RELU2_SMALL_MAX_WAVES_PER_CU 6 // gemm_relu2_small likewise
 #endif
+#ifndef NXG_RELU2_RT
+#define NXG_RELU2_RT 1                     // relu^2 -> int8 with n_in 256 or 1024 on gemm_relu2_rt (0: gemm_relu2_q8)
+#endif
 #ifndef NXG_SMALL_FN
 #define NXG_SMALL_FN 0                     // weight fragments per wave of gemm_small (0: chosen per launch)
 #endif
@@ -65,6 +68,18 @@ constexpr int STAGE_PITCH = 68;                        // floats per staging row
 // gemm_relu2_q8's ring: 8 A + 16 B fragments per slot; its scales have an area of their own.
 constexpr int WSLOT = (BM / 16 + WBN / 16) * FRAG;    // 24 KiB
 constexpr int WSCALE = 4 * (BM + WBN);                 // bytes: sx of 128 rows, then sw of 256 columns
+
+// gemm_relu2_rt: 64 x 256 tiles, 4 waves of 64 x 64, two workgroups per CU. The activation
+// row tile (64 rows x n_in, n_in <= 1024) stays in LDS while the workgroup walks its column
+// tiles; weights go straight to registers. LDS per workgroup: the row tile, two tiles'
+// scales (sx of 64 rows as 16 groups x n_blk x 4, then sw of 256 columns per block) and
+// two tiles' row maxima.
+constexpr int RM = 64;                                  // rows per tile
+constexpr int RNB_MAX = 4;                              // 256-input blocks the row tile holds
+constexpr int RTHREADS = 256;
+constexpr int RDEPTH = 4;                               // k-steps of weights in flight per wave
+constexpr int RSX_BYTES = 16 * RNB_MAX * 16;            // sx area: 1 KiB
+constexpr int RSCALE = RSX_BYTES + RNB_MAX * WBN * 4;   // bytes per tile's scales: 5 KiB
 
 // Few-row GEMMs: k-steps in flight per wave: two 256-input blocks for 32 x 32 pieces (fn
 // 2), one for 32 x 64 pieces (whose 6 fragments per k-step would otherwise need more
@@ -97,6 +112,24 @@ struct tile_walk {
     NXG_HD int tile_clamped(int i) const { return tile(imin(i, count - 1)); }
 };
 
+// gemm_relu2_rt: each XCD owns a contiguous range of tile numbers (as tile_walk), split
+// into near-equal contiguous pieces, one per workgroup of the XCD. Tiles are numbered with
+// the column tile fastest, so a workgroup walks the column tiles of a row tile in turn and
+// loads each activation row tile into LDS once; an XCD's workgroups share the weight in L2.
+struct tile_span {
+    int first, count;
+    NXG_HD tile_span(int wg, int n_wg, int G) {
+        const int xcd = wg % N_XCD, idx = wg / N_XCD;
+        const int per = n_wg / N_XCD + (xcd < n_wg % N_XCD ? 1 : 0);     // workgroups on this XCD
+        const int q = G / N_XCD, r = G % N_XCD;
+        const int lo = xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q;
+        const int n = q + (xcd < r ? 1 : 0);                              // tiles of this XCD
+        const long long a = (long long) n * idx / per, b = (long long) n * (idx + 1) / per;
+        first = lo + (int) a;
+        count = (int) (b - a);
+    }
+};
+
 // --- operand addresses ------------------------------------------------------------
 
 // Activation fragment row i (0 .. BM/16 - 1) of row tile mt. Rows past the last fragment
@@ -106,6 +139,8 @@ NXG_HD int a_frag(int mt, int i, int MF) { return imin(mt * (BM / 16) + i, MF - 
 // Weight fragment row i of column tile nt of `width` columns. NP is a multiple of WBN, so
 // every fragment row of a tile exists.
 NXG_HD int w_frag(int nt, int width, int i) { return nt * (width / 16) + i; }
+// gemm_relu2_rt: activation fragment row i (0 .. 3) of 64-row tile mt, clamped likewise.
+NXG_HD int a_frag_rt(int mt, int i, int MF) { return imin(mt * (RM / 16) + i, MF - 1); }
 // Few-row GEMMs: activation fragment row j (0 .. SDT - 1) of piece row mt, clamped likewise.
 NXG_HD int small_a_frag(int mt, int j, int MF) { return imin(mt * SDT + j, MF - 1); }
 // Byte offset of lane `lane`'s 16 bytes of k-step ks of fragment row r.
@@ -123,6 +158,11 @@ NXG_HD size_t sx_index(int t, int n_blk, int B) {
 // past the last one re-read it.
 NXG_HD size_t sx_group_index(int mt, int g, int MF, int n_blk, int B) {
     return ((size_t) imin(mt * (BM / 4) + g, MF * 4 - 1) * n_blk + B) * 4;
+}
+// gemm_relu2_rt: float index of the 4 sx of row group g (0 .. 15) of 64-row tile mt, block
+// B; groups past the last one re-read it.
+NXG_HD size_t sx_group_index_rt(int mt, int g, int MF, int n_blk, int B) {
+    return ((size_t) imin(mt * (RM / 4) + g, MF * 4 - 1) * n_blk + B) * 4;
 }
 // Float index of sw[B][n].
 NXG_HD size_t sw_index(int B, int NP, int n) { return (size_t) B * NP + n; }
@@ -188,7 +228,8 @@ enum gemm_kind : int {
     GEMM_K256 = 2,       // gemm_k256: fp32 out, n_in % 256 == 0, N % 4 == 0, persistent
     GEMM_SMALL = 3,      // gemm_small: few rows, one wave per 32 x 16fn piece
     GEMM_RELU2_Q8 = 4,   // gemm_relu2_q8: relu^2 -> int8, 128 x 256 tiles, one workgroup per CU
-    GEMM_RELU2_SMALL = 5 // gemm_relu2_small: relu^2 -> int8 for few rows
+    GEMM_RELU2_SMALL = 5,// gemm_relu2_small: relu^2 -> int8 for few rows
+    GEMM_RELU2_RT = 6    // gemm_relu2_rt: relu^2 -> int8, 64 x 256 tiles, row tile in LDS, n_in 256 or 1024
 };
 
 struct gemm_plan {
@@ -234,6 +275,15 @@ inline bool plan_gemm(int T, int n_in, int n_out, bool sums, bool relu2, int cus
             pl.G = (int) G_small;
             pl.grid = pl.G;
             pl.block = 256;
+            return true;
+        }
+        if ((pl.n_blk == 1 || pl.n_blk == RNB_MAX) && NXG_RELU2_RT) {
+            const long long G_rt = (long long) ceil_div(T, RM) * pl.n_nt;
+            pl.kind = GEMM_RELU2_RT;
+            pl.n_mt = ceil_div(T, RM);
+            pl.G = (int) G_rt;
+            pl.grid = persistent_grid(G_rt, 2LL * cus);
+            pl.block = RTHREADS;
             return true;
         }
         pl.kind = GEMM_RELU2_Q8;

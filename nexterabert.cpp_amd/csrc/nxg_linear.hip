@@ -2055,6 +2055,25 @@ __device__ __forceinline__ const int8_t * uniform_ptr(const int8_t * ptr) {
     return reinterpret_cast<const int8_t *>((uintptr_t) (((uint64_t) hi << 32) | lo));
 }
 
+// This lane's number, computed where it is used: an asm the compiler cannot hoist, so
+// that values derived from it are not kept live across a loop (register pressure).
+__device__ __forceinline__ int lane_here() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
+// A raw buffer resource over `bytes` bytes at `base` (gfx9 descriptor word 3): buffer
+// loads take a scalar base, a scalar offset and one vector offset, so that a wave's
+// address arithmetic stays on the scalar unit, and they count in vmcnt only.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void * base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short) 0, (int) bytes, 0x00020000);
+}
+// 16 bytes per lane at byte soff (wave-uniform) + voff (per lane) of the buffer.
+__device__ __forceinline__ v4i bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int) voff, (int) soff, 0);
+}
+
 // dma16 from a scalar base: lane l copies the 16 bytes at base + voff_l to LDS
 // address lds + 16 l. The address arithmetic stays on the scalar unit.
 __device__ __forceinline__ void dma16s(const int8_t * base, uint32_t voff, uint32_t lds) {
@@ -2811,6 +2830,284 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
     };
     if (nb == 1) walk_tiles(std::true_type{});
     else         walk_tiles(std::false_type{});
+    wait_vm<0>();
+}
+
+// relu(linear(x))^2 quantized for the next linear (the same output as gemm_relu2_q8), for
+// n_in <= 1024. Tiles of 64 rows x 256 columns (one 256-input block of the next linear),
+// two workgroups of 4 waves per CU, each wave the 64 x 64 piece of gemm_k256 at columns
+// 64 w. A workgroup walks a contiguous range of tiles (tile_span), so it loads each
+// activation row tile (64 rows x n_in, at most 64 KiB) into LDS once and walks its column
+// tiles; every wave loads its 4 weight fragments per k-step straight into registers,
+// RDEPTH k-steps ahead. So the k-loop has no barrier: each wave runs its k-steps and
+// per-block folds in its own phase, and a fold overlaps the MFMAs of the waves of the other
+// workgroup and of its own. The tile's one barrier publishes the row maxima (each row's
+// 256 columns span the 4 waves) and the next tile's scales, which were loaded under this
+// tile; the next tile's first weight k-steps are loaded before this tile's stores, so that
+// their waits do not wait for the stores. A new row tile is loaded after that barrier,
+// under the tile's quantization and stores, and published by a second barrier.
+template <int ACT_MAX, int NB>
+__global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
+    constexpr int KS = 4 * NB;                       // k-steps of a tile (p.KS)
+    constexpr int D = RDEPTH;
+    static_assert(NB >= 1 && NB <= RNB_MAX, "row tile of 1..4 blocks");
+    __shared__ __attribute__((aligned(1024))) int8_t arow[KS * (RM / 16) * FRAG];   // [ks][row group] fragments
+    __shared__ __attribute__((aligned(16))) float scl[2][RSCALE / 4];             // two tiles' scales
+    __shared__ __attribute__((aligned(16))) float am[2][RM * 4];                  // row maxima [row][wave]
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const tile_span span(blockIdx.x, gridDim.x, p.G);
+    if (span.count == 0) return;
+    const size_t frow = (size_t) KS * FRAG;          // bytes of one fragment row
+    const uint32_t lane16 = (uint32_t) lane * 16;
+    const uint32_t arow_lds = (uint32_t) (uintptr_t) (lds_void *) arow;
+    const uint32_t scl_lds = (uint32_t) (uintptr_t) (lds_void *) &scl[0][0];
+
+    // Row tile mt into LDS: wave w loads row group w of every k-step.
+    auto load_rows = [&](int mt) {
+        const int8_t * src = p.a + (size_t) a_frag_rt(mt, wave, p.MF) * frow;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            dma16s(uniform_ptr(src + (size_t) ks * FRAG), lane16, arow_lds + (uint32_t) ((ks * 4 + wave) * FRAG));
+    };
+    // A tile's scales into buffer b: wave w < NB the sw of block w (1 KiB: lane l columns
+    // 4l..4l+3); wave 0 lanes l < 16 NB the sx of row group l / NB, block l % NB.
+    // Scalar bases and 32-bit lane offsets (computed here, not kept across the tile loop).
+    auto load_scales = [&](int tile, int b) {
+        const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
+        const uint32_t base = scl_lds + (uint32_t) (b * RSCALE);
+        const int ln = lane_here();
+        if (wave < NB) {
+            const int8_t * sw_row = uniform_ptr(reinterpret_cast<const int8_t *>(p.sw + sw_index(wave, p.NP, nt * WBN)));
+            dma16s(sw_row, (uint32_t) ln * 16, base + RSX_BYTES + wave * (WBN * 4));
+        }
+        if (wave == 0 && ln < 16 * NB) {
+            dma16s(uniform_ptr(reinterpret_cast<const int8_t *>(p.sx)),
+                   (uint32_t) (sx_group_index_rt(mt, ln / NB, p.MF, NB, ln % NB) * sizeof(float)), base);
+        }
+    };
+
+    v4i acc[4][4];
+    float f[4][4][4];
+    v4i oa[4];                                       // activation operands (row groups) of one k-step
+    v4i ob[D][4];                                    // weight operands: k-step ks in ob[ks % D]
+    auto rd = [&](int ks, int i) {
+        oa[i] = *reinterpret_cast<const v4i *>(arow + (ks * 4 + i) * FRAG + lane * 16);
+    };
+    // The weight fragments 4w .. 4w + 3 of column tile nt, k-step ks, into ob[j]. The
+    // scheduling barrier keeps the loads where they are issued.
+    const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(p.w, (uint32_t) ((size_t) p.NP * KS * 64));
+    auto ldw = [&](int nt, int ks, int j) {
+        const uint32_t so = (uint32_t) __builtin_amdgcn_readfirstlane(w_frag(nt, WBN, 4 * wave) * (int) frow + ks * FRAG);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ob[j][i] = bload16(wrsrc, lane16, so + (uint32_t) (i * frow));
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // One k-step's 16 MFMAs (weights in ob[j]); as soon as the 4 that use row group mi are
+    // issued, oa[mi] is refilled with row group mi of k-step nk (none if nk < 0), so that
+    // every LDS read has 12 MFMAs to land before its use. The group barriers keep that order.
+    auto kstep = [&](int j, bool first, int nk) {
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni)
+                acc[mi][ni] = first
+                    ? __builtin_amdgcn_mfma_i32_16x16x64_i8(ob[j][ni], oa[mi], v4i{0, 0, 0, 0}, 0, 0, 0)
+                    : __builtin_amdgcn_mfma_i32_16x16x64_i8(ob[j][ni], oa[mi], acc[mi][ni], 0, 0, 0);
+            if (nk >= 0) rd(nk, mi);
+        }
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);       // 4 MFMAs
+            if (nk >= 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // 1 LDS read
+        }
+    };
+
+    int tile = span.first;
+    int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
+    load_rows(mt);
+    load_scales(tile, 0);
+    wait_vm<0>();
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < D; ++j) ldw(nt, j, j);
+
+    for (int it = 0; it < span.count; ++it) {
+        const int cur = it & 1;
+        const bool more = it + 1 < span.count;
+        // the next tile's scales into the other buffer (its last readers, the previous
+        // tile's folds, are all behind the previous tile's barrier)
+        if (more) load_scales(tile + 1, cur ^ 1);
+        const float * sc = &scl[cur][0];
+        const int nt_next = more ? (tile + 1) % p.n_nt : 0;
+
+        // Block B: k-steps 4B .. 4B + 3 (k-step ks's weights in ob[ks % 4], RDEPTH == 4), each
+        // slot refilled with the k-step 4 later (REFILL: every block but the tile's last),
+        // then the block's fold. Blocks past the first run in a loop that is not unrolled,
+        // so that the compiler keeps one block's load addresses at a time.
+        static_assert(D == 4, "one block of weight k-steps in flight");
+        auto block = [&](int B, auto first_tag, auto refill_tag) {
+            constexpr bool first = decltype(first_tag)::value, refill = decltype(refill_tag)::value;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                kstep(s, s == 0, s < 3 || refill ? 4 * B + s + 1 : -1);
+                __builtin_amdgcn_sched_barrier(0);
+                if (refill) ldw(nt, 4 * B + 4 + s, s);
+                else if (s == 0 && more) ldw(nt_next, 0, 0);  // the tile's last block: the next tile's k-step 0
+            }
+            // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
+            const int ln = lane_here();
+            float sxv[4];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                const int r = mi * 16 + (ln & 15);
+                sxv[mi] = sc[((r >> 2) * NB + B) * 4 + (r & 3)];
+            }
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const float4 sw4 = *reinterpret_cast<const float4 *>(sc + RSX_BYTES / 4 + B * WBN + wave * 64 + ni * 16 + 4 * (ln >> 4));
+                const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float prod = (float) acc[mi][ni][r] * sxv[mi];
+                        // block 0 starts from f = 0: fma(prod, sw, +0.0)
+                        f[mi][ni][r] = __builtin_fmaf(prod, swr[r], first ? 0.0f : f[mi][ni][r]);
+                    }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rd(0, i);
+        if (NB == 1) {
+            block(0, std::true_type{}, std::false_type{});
+        } else {
+            block(0, std::true_type{}, std::true_type{});
+#pragma unroll 1
+            for (int B = 1; B < NB - 1; ++B) block(B, std::false_type{}, std::true_type{});
+            block(NB - 1, std::false_type{}, std::false_type{});
+        }
+
+        // Row maxima of relu(f) = max(f, 0) (maxNum: a NaN counts as 0): over this lane's 16
+        // values, the wave's 4 lanes of the row, then the 4 waves through LDS, am[cur][row][w].
+        // The block amax of relu(f)^2 (values >= 0, no NaN: the reference's MAXPS fold is the
+        // plain maximum) is the square of that maximum, r * r being monotonic in r >= 0.
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+            float m = 0.0f;
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) m = fmaxf(m, f[mi][ni][r]);
+            m = rows_max(m);
+            const int ln = lane_here();
+            if (ln < 16) am[cur][(mi * 16 + ln) * 4 + wave] = m;
+        }
+        // This wave's loads done but the next tile's first weight k-step (4 loads, issued
+        // after the scale loads), then the barrier: the row maxima and the next tile's scales
+        // published, and every wave past its last read of this row tile.
+        if (more) wait_vm<4>();
+        else      wait_vm<0>();
+        lds_barrier();
+        const int tbase = mt * RM;
+        const int mt_t = mt, nt_t = nt;
+        const bool reload = more && (tile + 1) / p.n_nt != mt;
+        if (more) {
+            ++tile;
+            mt = tile / p.n_nt;
+            nt = tile - mt * p.n_nt;
+            if (reload) load_rows(mt);
+        }
+
+        // Lane l takes row l of the tile: the row's maximum over the 4 waves, its scale
+        // amax / ACT_MAX and inv = ACT_MAX / amax, each computed once per row; a transpose
+        // then gives every lane the inv of its 4 row groups. With every maximum of the wave
+        // finite and inv finite (the usual case) each value f * inv lies in [0, ACT_MAX + 1/2),
+        // so CVTPS2DQ and the saturating packs reduce to round-to-nearest-even, which
+        // v_cvt_pk_u8_f32 does while packing the byte. An infinite maximum, or one so small
+        // that inv overflows to +Inf, takes quant1 (NaN and Inf -> 0x80000000, u8 0).
+        {
+            const int lane = lane_here();               // (shadows the outer one: see lane_here)
+            const int tl = tbase + lane;
+            const v4f a4 = *reinterpret_cast<const v4f *>(&am[cur][lane * 4]);
+            const float rmax = tl < p.T ? fmaxf(fmaxf(a4.x, a4.y), fmaxf(a4.z, a4.w)) : 0.0f;
+            const float amax_l = rmax * rmax;
+            const float inv_l = amax_l > 0.0f ? (float) ACT_MAX / amax_l : 0.0f;
+            const bool fast = __builtin_amdgcn_ballot_w64(!(amax_l < INFINITY) || !(inv_l < INFINITY)) == 0;
+            int invs[4] = { __float_as_int(inv_l), __float_as_int(inv_l), __float_as_int(inv_l), __float_as_int(inv_l) };
+            rows_transpose(invs);                        // invs[mi]: row group mi, row lane % 16
+            if (wave == 0 && mt_t * (RM / 16) + (lane >> 4) < p.MF)
+                p.sxo[sxo_index(tl, p.n_nt, nt_t)] = amax_l / (float) ACT_MAX;
+            // Row group mi: its int8 values, zero past row T - 1 and column N - 1 (GUARD; a
+            // tile inside both bounds skips the tests).
+            auto quantize_store = [&](int mi, auto guard_tag) {
+                constexpr bool guard = decltype(guard_tag)::value;
+                const float inv = __int_as_float(invs[mi]);
+                const bool row_ok = tbase + mi * 16 + (lane & 15) < p.T;
+                // column 16ni + 4(lane/16) + r of the wave's 64: byte r of d[ni]
+                int d[4];
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) {
+                    int packed;
+                    if (fast) {
+                        // f * |f| is relu(f)^2 for f >= +0 and <= 0 (or NaN) otherwise, which
+                        // v_cvt_pk_u8_f32 turns into 0 like the reference's relu
+                        unsigned u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][0] * fabsf(f[mi][ni][0]) * inv, 0, 0u);
+                        u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][1] * fabsf(f[mi][ni][1]) * inv, 1, u);
+                        u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][2] * fabsf(f[mi][ni][2]) * inv, 2, u);
+                        u = __builtin_amdgcn_cvt_pk_u8_f32(f[mi][ni][3] * fabsf(f[mi][ni][3]) * inv, 3, u);
+                        packed = (int) u;
+                    } else {
+                        float r2[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float x = fmaxf(f[mi][ni][r], 0.0f);
+                            r2[r] = x * x;
+                        }
+                        packed = (quant1<ACT_MAX>(r2[0], inv) & 0xff) | ((quant1<ACT_MAX>(r2[1], inv) & 0xff) << 8)
+                               | ((quant1<ACT_MAX>(r2[2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(r2[3], inv) & 0xff) << 24);
+                    }
+                    if (guard) {
+                        const int n = nt_t * WBN + wave * 64 + ni * 16 + 4 * (lane >> 4);
+                        packed = row_ok && n < p.N ? packed : 0;
+                    }
+                    d[ni] = packed;
+                }
+                // lane c + 16 j now gets columns 16 j + 0..15 of row c: one fragment lane
+                rows_transpose(d);
+                const int rf = mt_t * (RM / 16) + mi, kf = nt_t * (WBN / 64) + wave;
+                if (rf < p.MF && kf < p.KSo) {
+                    // device scope (sc1): past L2, into the last-level cache, from which the next
+                    // GEMM reads them. The s_nop gives the store its wait states before the data
+                    // registers are written again (the compiler does not see into asm).
+                    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1"
+                                 :: "v"(p.qo + qo_byte(rf, p.KSo, kf, lane)), "v"(v4i{d[0], d[1], d[2], d[3]})
+                                 : "memory");
+                }
+            };
+            if (tbase + RM <= p.T && nt_t * WBN + WBN <= p.N) {
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi) quantize_store(mi, std::false_type{});
+            } else {
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi) quantize_store(mi, std::true_type{});
+            }
+        }
+        if (more) {
+            // the next tile's weight k-steps 1..3 (0 is in flight since this tile's last block)
+            ldw(nt, 1, 1);
+            ldw(nt, 2, 2);
+            ldw(nt, 3, 3);
+        }
+        if (reload) {
+            // the new row tile (and the weight loads and stores before it) landed, then
+            // published to every wave
+            wait_vm<0>();
+            lds_barrier();
+        }
+    }
     wait_vm<0>();
 }
 
@@ -3602,6 +3899,16 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
         if (o.act_max == 127) gemm_relu2_q8<127><<<grid, block, 0, s>>>(p);
         else                  gemm_relu2_q8<63><<<grid, block, 0, s>>>(p);
         return launch_check("gemm_relu2_q8");
+    case GEMM_RELU2_RT:
+        if ((p.n_blk != 1 && p.n_blk != RNB_MAX) || p.KS != 4 * p.n_blk) return fail(NXG_EINVAL, "linear_relu2_q8: plan/shape mismatch");
+        if (o.act_max == 127) {
+            if (p.n_blk == 1) gemm_relu2_rt<127, 1><<<grid, block, 0, s>>>(p);
+            else              gemm_relu2_rt<127, 4><<<grid, block, 0, s>>>(p);
+        } else {
+            if (p.n_blk == 1) gemm_relu2_rt<63, 1><<<grid, block, 0, s>>>(p);
+            else              gemm_relu2_rt<63, 4><<<grid, block, 0, s>>>(p);
+        }
+        return launch_check("gemm_relu2_rt");
     case GEMM_SMALL:
         if (pl.fn == 2) {
             if (res) { if (pl.k256) gemm_small<2, true, true><<<grid, block, 0, s>>>(p); else gemm_small<2, true, false><<<grid, block, 0, s>>>(p); }
@@ -3704,6 +4011,9 @@ const char * nxg_gemm_kernel_name(int32_t T, int32_t n_in, int32_t n_out, int32_
     switch (pl.kind) {
     case GEMM_RELU2_SMALL: return a63 ? "gemm_relu2_small<63>" : "gemm_relu2_small<127>";
     case GEMM_RELU2_Q8:    return a63 ? "gemm_relu2_q8<63>" : "gemm_relu2_q8<127>";
+    case GEMM_RELU2_RT:
+        if (pl.n_blk == 1) return a63 ? "gemm_relu2_rt<63, 1>" : "gemm_relu2_rt<127, 1>";
+        return a63 ? "gemm_relu2_rt<63, 4>" : "gemm_relu2_rt<127, 4>";
     case GEMM_SMALL: {
         static const char * const names[2][2][2] = {
             { { "gemm_small<2, false, false>", "gemm_small<2, false, true>" },

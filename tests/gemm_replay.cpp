@@ -462,6 +462,112 @@ void replay_relu2_q8(replay & r) {
     }
 }
 
+// gemm_relu2_rt: a contiguous span of 64 x 256 tiles per workgroup, the row tile in LDS
+// (loaded at the span's start and whenever the row tile changes), each wave's 4 weight
+// fragments per k-step into registers 4 k-steps ahead, a tile's scales loaded under the
+// previous tile into the other of two buffers.
+void replay_relu2_rt(replay & r) {
+    const gemm_plan & p = r.pl;
+    const int NB = p.n_blk, KS = p.KS;
+    if (KS != 4 * NB || (NB != 1 && NB != RNB_MAX)) {
+        r.failf(1, "gemm_relu2_rt: n_blk %d, KS %d", NB, KS);
+        return;
+    }
+    const size_t frow = (size_t) KS * FRAG;
+    const size_t arow = (size_t) KS * (RM / 16) * FRAG, scl = 2 * (size_t) RSCALE, am = 2 * RM * 4 * sizeof(float);
+    for (int wg = 0; wg < p.grid && !r.status; ++wg) {
+        const tile_span span(wg, p.grid, p.G);
+        if (span.count < 0 || (span.count > 0 && (span.first < 0 || span.first + span.count > p.G))) {
+            r.failf(1, "gemm_relu2_rt: workgroup %d spans tiles [%d, %d) of %d", wg, span.first, span.first + span.count, p.G);
+            return;
+        }
+        if (span.count == 0) continue;
+        for (int wave = 0; wave < RTHREADS / 64; ++wave) {
+            auto load_rows = [&](int mt) {
+                for (int ks = 0; ks < KS; ++ks)
+                    for (int lane = 0; lane < 64; ++lane) {
+                        r.load(A, (size_t) a_frag_rt(mt, wave, p.MF) * frow + (size_t) ks * FRAG + (size_t) lane * 16, 16,
+                               wg, wave, lane, "gemm_relu2_rt row tile");
+                        r.lds((size_t) (ks * 4 + wave) * FRAG + (size_t) lane * 16, 16, arow, wg, wave, lane,
+                              "gemm_relu2_rt row tile");
+                    }
+            };
+            auto load_scales = [&](int tile, int b) {
+                const int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
+                for (int lane = 0; lane < 64; ++lane) {
+                    if (wave < NB) {
+                        r.load(SW, sw_index(wave, p.NP, nt * WBN + 4 * lane) * 4, 16, wg, wave, lane, "gemm_relu2_rt sw");
+                        r.lds((size_t) b * RSCALE + RSX_BYTES + (size_t) wave * WBN * 4 + (size_t) lane * 16, 16, scl, wg,
+                              wave, lane, "gemm_relu2_rt sw");
+                    }
+                    if (wave == 0 && lane < 16 * NB) {
+                        r.load(SX, sx_group_index_rt(mt, lane / NB, p.MF, NB, lane % NB) * 4, 16, wg, wave, lane,
+                               "gemm_relu2_rt sx");
+                        r.lds((size_t) b * RSCALE + (size_t) lane * 16, 16, scl, wg, wave, lane, "gemm_relu2_rt sx");
+                    }
+                }
+            };
+            auto ldw = [&](int nt, int ks) {
+                for (int i = 0; i < 4; ++i)
+                    for (int lane = 0; lane < 64; ++lane)
+                        r.load(W, (size_t) w_frag(nt, WBN, 4 * wave) * frow + (size_t) ks * FRAG + (size_t) i * frow +
+                                      (size_t) lane * 16, 16, wg, wave, lane, "gemm_relu2_rt weights");
+            };
+            int tile = span.first;
+            int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
+            load_rows(mt);
+            load_scales(tile, 0);
+            for (int j = 0; j < RDEPTH; ++j) ldw(nt, j);
+            for (int it = 0; it < span.count && !r.status; ++it) {
+                const int cur = it & 1;
+                const bool more = it + 1 < span.count;
+                if (more) load_scales(tile + 1, cur ^ 1);
+                for (int B = 0; B < NB; ++B) {
+                    for (int s4 = 0; s4 < 4; ++s4) {
+                        for (int lane = 0; lane < 64; ++lane)
+                            for (int i = 0; i < 4; ++i)
+                                r.lds((size_t) ((4 * B + s4) * 4 + i) * FRAG + (size_t) lane * 16, 16, arow, wg, wave, lane,
+                                      "gemm_relu2_rt operand read");
+                        if (B < NB - 1) ldw(nt, 4 * B + 4 + s4);
+                        else if (s4 == 0 && more) ldw((tile + 1) % p.n_nt, 0);   // the next tile's k-step 0
+                    }
+                    for (int lane = 0; lane < 64; ++lane) {
+                        for (int mi = 0; mi < 4; ++mi) {
+                            const int rr = mi * 16 + (lane & 15);
+                            r.lds((size_t) cur * RSCALE + (((size_t) (rr >> 2) * NB + B) * 4 + (rr & 3)) * 4, 4, scl, wg, wave,
+                                  lane, "gemm_relu2_rt sx read");
+                        }
+                        for (int ni = 0; ni < 4; ++ni)
+                            r.lds((size_t) cur * RSCALE + RSX_BYTES + ((size_t) B * WBN + wave * 64 + ni * 16 + 4 * (lane >> 4)) * 4,
+                                  16, scl, wg, wave, lane, "gemm_relu2_rt sw read");
+                    }
+                }
+                for (int lane = 0; lane < 64; ++lane) {
+                    for (int mi = 0; mi < 4 && lane < 16; ++mi)
+                        r.lds(((size_t) cur * RM * 4 + (size_t) (mi * 16 + lane) * 4 + wave) * 4, 4, am, wg, wave, lane,
+                              "gemm_relu2_rt row maxima");
+                    r.lds(((size_t) cur * RM * 4 + (size_t) lane * 4) * 4, 16, am, wg, wave, lane, "gemm_relu2_rt row maxima");
+                }
+                const int mt_t = mt, nt_t = nt;
+                if (more) {
+                    const bool reload = (tile + 1) / p.n_nt != mt;
+                    ++tile;
+                    mt = tile / p.n_nt;
+                    nt = tile - mt * p.n_nt;
+                    if (reload) load_rows(mt);
+                }
+                for (int mi = 0; mi < 4; ++mi)
+                    relu2_store(r, wg, wave, mt_t * (RM / 16) + mi, nt_t * (WBN / 64) + wave, nt_t, false, "gemm_relu2_rt output");
+                for (int lane = 0; lane < 64 && wave == 0; ++lane)
+                    if (mt_t * (RM / 16) + (lane >> 4) < p.MF)
+                        r.store(SXO, sxo_index(mt_t * RM + lane, p.n_nt, nt_t) * 4, 4, wg, wave, lane, "gemm_relu2_rt row scales");
+                if (more)
+                    for (int j = 1; j < RDEPTH; ++j) ldw(nt, j);   // the next tile's k-steps 1..3
+            }
+        }
+    }
+}
+
 void replay_relu2_small(replay & r) {
     const gemm_plan & p = r.pl;
     for (int wg = 0; wg < p.grid && !r.status; ++wg) {
@@ -525,6 +631,7 @@ extern "C" int gemm_replay(int T, int n_in, int n_out, int mode, int n_seg, cons
     case GEMM_SMALL: replay_small(r, res); break;
     case GEMM_RELU2_Q8: replay_relu2_q8(r); break;
     case GEMM_RELU2_SMALL: replay_relu2_small(r); break;
+    case GEMM_RELU2_RT: replay_relu2_rt(r); break;
     }
     if (!r.status) {
         if (sums) r.covered(SUMS, r.bytes[SUMS] / 4, (size_t) n_out);

@@ -97,8 +97,11 @@ def test_gemm_kernel_name(nxg):
     assert k(65536, 1024, 2048) == "gemm_k256<false>"
     assert k(65536, 2304, 1024, residual=True) == "gemm_k256<true>"
     assert k(65536, 64, 1024, residual=True) == "gemm_kernel<true, false, false>"
-    assert k(65536, 1024, 2304, relu2=True) == "gemm_relu2_q8<127>"
-    assert k(65536, 1024, 2304, relu2=True, act_max=63) == "gemm_relu2_q8<63>"
+    assert k(65536, 1024, 2304, relu2=True) == "gemm_relu2_rt<127, 4>"
+    assert k(65536, 1024, 2304, relu2=True, act_max=63) == "gemm_relu2_rt<63, 4>"
+    assert k(65536, 256, 512, relu2=True) == "gemm_relu2_rt<127, 1>"
+    assert k(65536, 512, 2304, relu2=True) == "gemm_relu2_q8<127>"
+    assert k(65536, 2304, 1024, relu2=True, act_max=63) == "gemm_relu2_q8<63>"
     assert k(1024, 1024, 2304, relu2=True) == "gemm_relu2_small<127>"
     assert k(1024, 1024, 1024) == "gemm_small<2, false, true>"
     assert k(1024, 320, 64, sums=True) == "gemm_kernel<false, true, false>"

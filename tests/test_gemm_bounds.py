@@ -23,7 +23,7 @@ SRC = ROOT / "tests" / "gemm_replay.cpp"
 
 FP32, RESIDUAL, SUMS, RELU2 = 0, 1, 2, 3
 KINDS = {0: "gemm_kernel", 1: "gemm_kernel sums", 2: "gemm_k256", 3: "gemm_small", 4: "gemm_relu2_q8",
-         5: "gemm_relu2_small"}
+         5: "gemm_relu2_small", 6: "gemm_relu2_rt"}
 
 
 def _build(out_dir: Path, header_text: str = None) -> ctypes.CDLL:
@@ -87,11 +87,19 @@ def test_block_sums_in_bounds(replay, T):
             assert _ok(replay, T, n_in, n_out, SUMS) == "gemm_kernel sums"
 
 
-@pytest.mark.parametrize("T", [1, 15, 17, 129, 1000, 32935])
+@pytest.mark.parametrize("T", [1, 15, 17, 129, 1000, 8191, 32935])
 def test_relu2_int8_in_bounds(replay, T):
-    for n_in in (256, 1024, 2304):
+    for n_in in (256, 512, 1024, 2304):
         for n_out in (32, 96, 288, 2304):
             _ok(replay, T, n_in, n_out, RELU2)
+
+
+def test_relu2_kernel_choice(replay):
+    """n_in 256 and 1024 on the row-tile kernel, other block counts on the 128 x 256 one."""
+    assert _ok(replay, 65536, 1024, 2304, RELU2) == "gemm_relu2_rt"
+    assert _ok(replay, 9000, 256, 1216, RELU2) == "gemm_relu2_rt"
+    assert _ok(replay, 9000, 512, 1216, RELU2) == "gemm_relu2_q8"
+    assert _ok(replay, 9000, 2304, 1024, RELU2) == "gemm_relu2_q8"
 
 
 @pytest.mark.parametrize("T", [1, 17, 129, 5000, 32935])
@@ -115,13 +123,15 @@ def test_encoder_shapes_at_full_size(replay):
 def test_other_grids(replay, cus):
     """Persistent grids of other sizes: walks of many tiles per workgroup, uneven XCDs."""
     for T, n_in, n_out, mode in ((4100, 1024, 2304, RELU2), (4100, 2304, 1024, RESIDUAL), (3000, 320, 260, FP32),
-                                 (3000, 1024, 1000, SUMS), (300, 1024, 2048, FP32), (70, 2304, 2304, RELU2)):
+                                 (3000, 1024, 1000, SUMS), (300, 1024, 2048, FP32), (70, 2304, 2304, RELU2),
+                                 (4100, 512, 2304, RELU2), (777, 256, 320, RELU2)):
         _ok(replay, T, n_in, n_out, mode, cus=cus)
 
 
 def test_every_kernel_replayed(replay):
     for T, n_in, n_out, mode in ((5, 256, 64, FP32), (5, 256, 64, RELU2), (4100, 1024, 2304, RELU2),
-                                 (4100, 1024, 1024, FP32), (300, 320, 6, FP32), (300, 320, 6, SUMS)):
+                                 (4100, 512, 2304, RELU2), (4100, 1024, 1024, FP32), (300, 320, 6, FP32),
+                                 (300, 320, 6, SUMS)):
         _ok(replay, T, n_in, n_out, mode)
     assert set(KINDS.values()) <= SEEN
 
@@ -146,6 +156,12 @@ PLANTS = [
     ("clamp_col4", r"return imin\(n, N - 4\);", "return n;", (4100, 1024, 1000, RESIDUAL), "res bytes"),
     # residual rows past T in the last row tile
     ("clamp_row", r"return imin\(t, T - 1\);", "return t;", (4100, 1024, 1024, RESIDUAL), "res bytes"),
+    # the row-tile relu^2 kernel: fragment rows and sx groups past the last ones, spans that overlap
+    ("a_frag_rt", r"return imin\(mt \* \(RM / 16\) \+ i, MF - 1\);", "return mt * (RM / 16) + i;",
+     (4100, 1024, 2304, RELU2), "a bytes"),
+    ("sx_group_index_rt", r"imin\(mt \* \(RM / 4\) \+ g, MF \* 4 - 1\)", "(mt * (RM / 4) + g)",
+     (4100, 1024, 2304, RELU2), "sx bytes"),
+    ("tile_span", r"count = \(int\) \(b - a\);", "count = (int) (b - a) + 1;", (4100, 1024, 2304, RELU2), "spans tiles"),
     # a split boundary off by one segment: columns land in the wrong buffer
     ("out_col_of", r"if \(n_seg > 1 && n >= seg_end\[0\]\)", "if (n_seg > 1 && n > seg_end[0])",
      (4100, 1024, 2048, FP32, (1024, 512, 512)), "seg"),

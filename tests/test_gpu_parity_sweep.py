@@ -2,8 +2,8 @@
 
 Rows, inputs and outputs are drawn so that every kernel the launcher can pick is reached:
 the few-row pieces (gemm_small, gemm_relu2_small), the 128 x 128 tiles with and without a
-per-tile schedule (gemm_k256, gemm_kernel) and the 128 x 256 relu^2 tiles (gemm_relu2_q8),
-with ragged rows, partial column tiles, residuals and both activation ranges. Each case prints
+per-tile schedule (gemm_k256, gemm_kernel), the 128 x 256 relu^2 tiles (gemm_relu2_q8) and
+the 64 x 256 relu^2 tiles over an LDS-resident row tile (gemm_relu2_rt), with ragged rows, partial column tiles, residuals and both activation ranges. Each case prints
 its index, shape and kernel before it touches the GPU.
 """
 from __future__ import annotations
@@ -19,7 +19,8 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 ROOT = Path(__file__).resolve().parents[1]
-KINDS = {0: "gemm_kernel", 2: "gemm_k256", 3: "gemm_small", 4: "gemm_relu2_q8", 5: "gemm_relu2_small"}
+KINDS = {0: "gemm_kernel", 2: "gemm_k256", 3: "gemm_small", 4: "gemm_relu2_q8", 5: "gemm_relu2_small",
+         6: "gemm_relu2_rt"}
 
 
 def say(msg):

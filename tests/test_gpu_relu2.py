@@ -2,7 +2,8 @@
 
 The fp32 GEMM is checked in full against the oracle at shapes of at least 256 tiles
 (persistent workgroups walking several tiles each: full, ragged and partial tiles, one
-and several 256-input blocks). The relu^2 output runs on 128 x 256 tiles; it is compared
+and several 256-input blocks). The relu^2 output runs on 64 x 256 tiles over an
+LDS-resident row tile (n_in 256 or 1024) or on 128 x 256 tiles; it is compared
 bit for bit with the CPU oracle (linear, then relu^2, then quantize_row) and, raw buffers
 with padding included, with the two-step GPU path (fp32 linear, then relu^2 quantize).
 """
@@ -91,9 +92,11 @@ def test_quantize_relu2_matches_oracle(nxg, orc, torch, dev, act_max):
 
 
 # (T, n_in, n_out) for c_fc -> relu^2 -> int8; n_out % 32 == 0, n_in % 256 == 0
-RELU2_SHAPES = [(4096, 1024, 2304),   # the MLP's c_fc, 4 blocks, 9 column tiles
-                (9000, 512, 1216),    # 2 blocks, ragged rows, a 192-column last tile, several tiles per workgroup
-                (9000, 256, 1216),    # the same with one block per tile (its own tile walk)
+RELU2_SHAPES = [(4096, 1024, 2304),   # the MLP's c_fc, 4 blocks, 9 column tiles (64 x 256 row-tile kernel)
+                (5000, 1024, 1216),   # row-tile kernel: a partial last row tile (8 rows), a 192-column last tile
+                (20000, 1024, 320),   # row-tile kernel: spans that start inside a row tile, 2 column tiles
+                (9000, 512, 1216),    # 2 blocks (128 x 256 kernel), ragged rows, a 192-column last tile
+                (9000, 256, 1216),    # one block (row-tile kernel, its 1-block instance)
                 (777, 512, 320),      # ragged rows, a 64-column last tile, KSo = 5
                 (33, 256, 96),        # one row tile, n_out % 64 = 32
                 (1, 1024, 256)]
@@ -123,10 +126,11 @@ def test_linear_relu2_q8(nxg, orc, torch, dev, T, n_in, n_out):
         assert (bits(sx.cpu().numpy()) == bits(rsx_ref)).all()
 
 
-def test_linear_relu2_q8_packed_batch(nxg, orc, torch, dev):
-    say("linear_relu2_q8 with cu_offsets")
+@pytest.mark.parametrize("lengths", [[300, 17, 1000, 129],       # few-row kernel
+                                     [3000, 17, 5000, 129]])     # row-tile kernel; sequence 2 alone: few-row
+def test_linear_relu2_q8_packed_batch(nxg, orc, torch, dev, lengths):
+    say(f"linear_relu2_q8 with cu_offsets {lengths}")
     rng = np.random.default_rng(8)
-    lengths = [300, 17, 1000, 129]
     cu = nxg.cu_offsets_of(lengths)
     T, n_in, n_out = int(cu[-1]), 1024, 512
     x = rng.standard_normal((T, n_in)).astype(np.float32)
@@ -151,14 +155,16 @@ def test_linear_relu2_q8_packed_batch(nxg, orc, torch, dev):
     assert (bits(sa_m[s0:s1]) == bits(sc_m)).all() and sa_m.shape[1] == n_blk
 
 
-def test_linear_relu2_q8_overflowing_rows(nxg, orc, torch, dev):
+@pytest.mark.parametrize("n_in", [1024, 512])
+def test_linear_relu2_q8_overflowing_rows(nxg, orc, torch, dev, n_in):
     """Rows whose fp32 sums overflow: relu^2 gives +Inf, the row maximum is infinite and the
     quantization takes the reference's NaN path (x * 0 for the infinite values). Waves that
     hold such a row use the full CVTPS2DQ statement, the others the packed conversion; both
-    against the oracle chain, on 128 x 256 tiles (T >= 8192 keeps the many-row kernel)."""
-    say("linear_relu2_q8 with overflowing rows")
+    against the oracle chain, on the many-row kernels (T >= 8192): the row-tile kernel
+    (n_in 1024) and the 128 x 256 one (n_in 512)."""
+    say(f"linear_relu2_q8 with overflowing rows, n_in={n_in}")
     rng = np.random.default_rng(11)
-    T, n_in, n_out = 8200, 1024, 512
+    T, n_out = 8200, 512
     x = rng.standard_normal((T, n_in)).astype(np.float32)
     x[5, :] *= np.float32(3e37)          # every block of the row: sums reach the fp32 limit
     x[4100, ::3] = np.float32(-2e38)     # a row of mixed signs in another tile
@@ -180,17 +186,19 @@ def test_linear_relu2_q8_overflowing_rows(nxg, orc, torch, dev):
         assert ((bits(s) == bits(rsx_ref)) | (np.isnan(s) & np.isnan(rsx_ref))).all(), f"act_max={act_max}"
 
 
-def test_linear_relu2_q8_tiny_row_maxima(nxg, orc, torch, dev):
+@pytest.mark.parametrize("n_in", [1024, 512])
+def test_linear_relu2_q8_tiny_row_maxima(nxg, orc, torch, dev, n_in):
     """Rows whose relu^2 maximum is positive but below ACT_MAX / FLT_MAX (normal and
     denormal), so that inv = ACT_MAX / amax overflows to +Inf: the reference's CVTPS2DQ then
     gives 0x80000000 for every value of the row (u8 0). Rows are scaled by powers of two, which
     scale the quantized activations' sx and every fold step exactly, so the maxima land where
     chosen (2^-62: just above the bound, inv finite; 2^-64, 2^-65: normal maxima below it;
-    2^-70: a denormal maximum; 2^-80: relu^2 underflows to 0). T >= 8192 keeps the
-    128 x 256 kernel; checked against the oracle chain and against the two-step path."""
-    say("linear_relu2_q8 with tiny row maxima")
+    2^-70: a denormal maximum; 2^-80: relu^2 underflows to 0). T >= 8192 keeps the many-row
+    kernels (the row-tile one at n_in 1024, the 128 x 256 one at 512); checked against the
+    oracle chain and against the two-step path."""
+    say(f"linear_relu2_q8 with tiny row maxima, n_in={n_in}")
     rng = np.random.default_rng(12)
-    T, n_in, n_out = 8200, 1024, 512
+    T, n_out = 8200, 512
     x = rng.standard_normal((T, n_in)).astype(np.float32)
     scaled = {5: -62, 6: -65, 70: -64, 3000: -70, 3001: -62, 6000: -80, 8195: -65}
     for t, e in scaled.items():
