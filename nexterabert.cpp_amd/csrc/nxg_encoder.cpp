@@ -775,6 +775,24 @@ int32_t load_into(nxg_encoder & e, const char * path, const nxg_encoder_params &
                     hp.n_embd, hp.lily_rank, hp.n_inter, hp.hra_block);
     }
 
+    // Every encoder linear must take the int8 path (the placement rule of
+    // src/nexterabert.cpp:1663-1667): the reference would run the others on ggml_mul_mat
+    // (:1140-1142), which this engine does not have. Checked on the tensor table, before
+    // the GPU is touched, so that an F32 / F16 file is refused with this reason anywhere.
+    for (const need & nd : needed(hp)) {
+        if (nd.n_out < 0) continue;
+        const int64_t ti = nxg_gguf_find_tensor(g, nd.name.c_str());
+        if (ti < 0) return fail(NXG_EINVAL, "encoder: missing tensor '%s'", nd.name.c_str());
+        int32_t type = 0, ndim = 0;
+        int64_t ne[4];
+        NXG_TRY(nxg_gguf_tensor_info(g, ti, &type, &ndim, ne, nullptr, nullptr));
+        if (!nxg_weight_is_int8(nd.name.c_str(), ndim, type, ne[0], ndim > 1 ? ne[1] : 1, 1)) {
+            return fail(NXG_EINVAL, "encoder: '%s' (ggml type %d) is not on the int8 path: this engine runs every encoder "
+                        "linear as an int8 GEMM and has no ggml_mul_mat fallback (F32/F16/BF16 linears are refused)",
+                        nd.name.c_str(), type);
+        }
+    }
+
     // tensors: the int8 linears expanded and uploaded, the rest decoded to fp32 and uploaded
     NXG_TRY(nxg_init());
     const int64_t n_tensors = nxg_gguf_n_tensors(g);

@@ -3,6 +3,7 @@
 the GPU is touched; a valid file on a machine without the GPU fails with NXG_EDEVICE."""
 from __future__ import annotations
 
+import numpy as np
 import pytest
 
 
@@ -12,7 +13,7 @@ def synth(nxg):
     return S
 
 
-def write(nxg, synth, path, meta_edit=None, **dims):
+def write(nxg, synth, path, meta_edit=None, type_of=None, **dims):
     d = synth.Dims(n_vocab=100, n_embd=128, n_inter=256, n_head=2, n_kv_head=1, lily_rank=64,
                    block_types=["lily", "attn"], **dims)
     import nexterabert_cpp_amd.gguf_writer as W
@@ -22,9 +23,11 @@ def write(nxg, synth, path, meta_edit=None, **dims):
         meta = meta_edit(meta)
     entries = []
     for name in sorted(t):
-        ty = synth.file_type_of(name, t[name], "Q8_0")
+        ty = (type_of or {}).get(name, synth.file_type_of(name, t[name], "Q8_0"))
         ne = tuple(reversed(t[name].shape)) if t[name].ndim == 2 else (t[name].size,)
-        entries.append((name, ty, ne, synth.encode_tensor(nxg, t[name], ty)))
+        data = (np.ascontiguousarray(t[name], np.float16).tobytes() if ty == synth.F16
+                else synth.encode_tensor(nxg, t[name], ty))
+        entries.append((name, ty, ne, data))
     W.write_gguf(path, meta, entries)
     return path
 
@@ -74,3 +77,16 @@ def test_missing_file_and_no_gpu(nxg, synth, tmp_path):
     p = write(nxg, synth, tmp_path / "g.gguf")
     ei = load_error(nxg, p)
     assert ei.type is nxg.NxgError          # NXG_EDEVICE: the metadata passed, no gfx950 GPU here
+
+
+@pytest.mark.parametrize("linear,type_name", [("blocks.1.mlp.c_fc.weight", "F16"), ("blocks.0.attn.x_proj.weight", "F32")])
+def test_refuses_linears_off_the_int8_path(nxg, synth, tmp_path, linear, type_name):
+    """An F16 or F32 encoder linear (which the reference would run on ggml_mul_mat,
+    src/nexterabert.cpp:1140-1142) is refused from the tensor table, before the GPU is
+    touched, with the reason."""
+    ty = getattr(synth, type_name)
+    p = write(nxg, synth, tmp_path / "h.gguf", type_of={linear: ty})
+    ei = load_error(nxg, p)
+    assert ei.type is ValueError
+    msg = str(ei.value)
+    assert f"'{linear}' (ggml type {ty}) is not on the int8 path" in msg and "no ggml_mul_mat fallback" in msg

@@ -58,6 +58,8 @@ def oracle_linear(orc, W, q_ref, sx_ref, res=None):
 FEW_ROW_SHAPES = [
     (1000, 1024, 1024),   # 32 x 32 pieces (1024 waves), 4 blocks
     (1000, 1024, 1000),   # 32 x 32, last feature piece partly past n_out
+    (333, 768, 260),      # 32 x 32, 3 blocks, ragged rows and columns
+    (700, 1280, 1000),    # 32 x 32, 5 blocks (an odd block count: the one-block tail of the ring)
     (1000, 320, 1024),    # 32 x 32, n_in % 256 != 0: last block of one k-step
     (1000, 2304, 512),    # 32 x 32, 9 blocks: the odd last block
     (1000, 1024, 2048),   # 32 x 64 pieces (2048 > 1024 32 x 32 pieces)

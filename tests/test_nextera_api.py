@@ -107,6 +107,22 @@ def test_load_refusals_return_null_with_a_reason(nxg, lib, tmp_path, capfd):
     assert not _load(lib, good, use_int8=0)
     assert "use_int8 = 0" in capfd.readouterr().err
 
+    # an F16 encoder linear: refused with the reason, before any device work (also without a GPU)
+    from nexterabert_cpp_amd import synth as S
+    f16 = tmp_path / "f16.gguf"
+    d = S.Dims(n_vocab=100, n_embd=128, n_inter=256, n_head=2, n_kv_head=1, lily_rank=64, block_types=["lily", "attn"])
+    t = S.model_tensors(d, seed=0)
+    entries = []
+    for name in sorted(t):
+        ty = S.F16 if name == "blocks.1.attn.c_q.weight" else S.file_type_of(name, t[name], "Q8_0")
+        ne = tuple(reversed(t[name].shape)) if t[name].ndim == 2 else (t[name].size,)
+        data = np.ascontiguousarray(t[name], np.float16).tobytes() if ty == S.F16 else S.encode_tensor(nxg, t[name], ty)
+        entries.append((name, ty, ne, data))
+    W.write_gguf(f16, S.metadata(d, "Q8_0"), entries)
+    assert not _load(lib, f16)
+    err = capfd.readouterr().err
+    assert "'blocks.1.attn.c_q.weight' (ggml type 1) is not on the int8 path" in err, err
+
     bad_task = tmp_path / "task.gguf"
     _model(nxg, bad_task, extra_metadata=[("nexterabert.classifier.task", W.STRING, "regression")])
     assert not _load(lib, bad_task)
