@@ -56,7 +56,9 @@ NXG_API int32_t nxg_encoder_n_vocab(const nxg_encoder * e);
 NXG_API int32_t nxg_encoder_n_layer(const nxg_encoder * e);
 NXG_API int32_t nxg_encoder_n_token_types(const nxg_encoder * e);
 
-/* Device memory the context holds: weights, tables and the current work buffers. */
+/* Device memory the context holds: weights, tables and the current work buffers. Not
+ * counted: the NXG_NOALLOC_SCRATCH_BYTES array (nxg_linear.h) that loading the library
+ * reserves on each GPU the process uses. */
 NXG_API size_t nxg_encoder_device_bytes(const nxg_encoder * e);
 
 /* Caps the work buffers at `bytes` (0: no cap; the default). The work area holds the

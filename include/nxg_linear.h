@@ -213,8 +213,9 @@ NXG_API int32_t nxg_attention_ws(const float * q, const float * k, const float *
 /* nxg_attention_ws without a caller's workspace and without allocating: no counterpart in
  * the reference; for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). The workspace is a static
- * device array of NXG_NOALLOC_SCRATCH_BYTES in the library, one per GPU, held until the
- * process ends; the call uses as many of its slots (16 * max_keys floats each) as fit, and
+ * device array of NXG_NOALLOC_SCRATCH_BYTES in the library's code object, one per GPU, held
+ * until the process ends -- by every process that loads the library, on each GPU it uses,
+ * whether or not it calls this entry point; the call uses as many of its slots (16 * max_keys floats each) as fit, and
  * refuses (NXG_EINVAL) a max_keys whose single slot would not fit (more than 1,048,576 keys).
  * Same arguments and results as nxg_attention. Calls that overlap on one GPU race (they
  * share the array); calls in one stream, or synchronized, do not. */
