@@ -33,7 +33,7 @@
 #define NXG_SMALL_MAX_WAVES_PER_CU 4       // gemm_small while its waves number at most this many per CU
 #endif
 #ifndef NXG_RELU2_SMALL_MAX_WAVES_PER_CU
-#define NXG_RELU2_SMALL_MAX_WAVES_PER_CU 6 // gemm_relu2_small likewise
+#define NXG_RELU2_SMALL_MAX_WAVES_PER_CU 4 // gemm_relu2_small likewise (its workgroups: one per CU)
 #endif
 #ifndef NXG_RELU2_RT
 #define NXG_RELU2_RT 1                     // relu^2 -> int8 with n_in 256 or 1024 on gemm_relu2_rt (0: gemm_relu2_q8)

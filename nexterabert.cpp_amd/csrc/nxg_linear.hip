@@ -2245,11 +2245,17 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
                     if (!(last && s == 3)) rd((s + 1) & 3, (s + 1) & 1);
                     mm(s & 1, s == 0, 3, 4);
                 };
+                // Wave priority: k-steps 2, fold 1, output 0 (s_setprio). A SIMD holds one wave
+                // of each of the CU's two workgroups; when both have an instruction ready, the
+                // one feeding the matrix core issues first, and a workgroup writing its output
+                // yields to the other's k-loop.
+                __builtin_amdgcn_s_setprio(2);
                 step(std::integral_constant<int, 0>{});
                 step(std::integral_constant<int, 1>{});
                 step(std::integral_constant<int, 2>{});
                 step(std::integral_constant<int, 3>{});
                 if (RES && last) load_res(0);
+                __builtin_amdgcn_s_setprio(1);
 
                 // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
                 const float * scl = reinterpret_cast<const float *>(ring + 3 * SLOT + SLOT_AB);
@@ -2278,6 +2284,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void gemm_k256(gemm_params p) {
                 for (int B = 1; B < nb - 1; ++B) run_block(B, std::false_type{}, std::false_type{});
                 run_block(nb - 1, std::true_type{}, std::false_type{});
             }
+            __builtin_amdgcn_s_setprio(0);
 
             // Output through LDS, whole 128-byte lines per store. Slot 3 is free once
             // every wave has passed this barrier (the next tile's k-step 3 is loaded only
@@ -2945,10 +2952,12 @@ __global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
         // Block B: k-steps 4B .. 4B + 3 (k-step ks's weights in ob[ks % 4], RDEPTH == 4), each
         // slot refilled with the k-step 4 later (REFILL: every block but the tile's last),
         // then the block's fold. Blocks past the first run in a loop that is not unrolled,
-        // so that the compiler keeps one block's load addresses at a time.
+        // so that the compiler keeps one block's load addresses at a time. Wave priority as
+        // in gemm_k256: k-steps 2, fold 1, row maxima, quantization and stores 0.
         static_assert(D == 4, "one block of weight k-steps in flight");
         auto block = [&](int B, auto first_tag, auto refill_tag) {
             constexpr bool first = decltype(first_tag)::value, refill = decltype(refill_tag)::value;
+            __builtin_amdgcn_s_setprio(2);
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 kstep(s, s == 0, s < 3 || refill ? 4 * B + s + 1 : -1);
@@ -2956,6 +2965,7 @@ __global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
                 if (refill) ldw(nt, 4 * B + 4 + s, s);
                 else if (s == 0 && more) ldw(nt_next, 0, 0);  // the tile's last block: the next tile's k-step 0
             }
+            __builtin_amdgcn_s_setprio(1);
             // f = fma((float) s * sx[t, B], sw[B, n], f): the reference's per-block step.
             const int ln = lane_here();
             float sxv[4];
@@ -2990,6 +3000,7 @@ __global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
             block(NB - 1, std::false_type{}, std::false_type{});
         }
 
+        __builtin_amdgcn_s_setprio(0);
         // Row maxima of relu(f) = max(f, 0) (maxNum: a NaN counts as 0): over this lane's 16
         // values, the wave's 4 lanes of the row, then the 4 waves through LDS, am[cur][row][w].
         // The block amax of relu(f)^2 (values >= 0, no NaN: the reference's MAXPS fold is the

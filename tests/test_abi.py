@@ -102,7 +102,8 @@ def test_gemm_kernel_name(nxg):
     assert k(65536, 256, 512, relu2=True) == "gemm_relu2_rt<127, 1>"
     assert k(65536, 512, 2304, relu2=True) == "gemm_relu2_q8<127>"
     assert k(65536, 2304, 1024, relu2=True, act_max=63) == "gemm_relu2_q8<63>"
-    assert k(1024, 1024, 2304, relu2=True) == "gemm_relu2_small<127>"
+    assert k(768, 1024, 2304, relu2=True) == "gemm_relu2_small<127>"     # 216 workgroups: one per CU
+    assert k(1024, 1024, 2304, relu2=True) == "gemm_relu2_rt<127, 4>"    # 288 would be: the row tiles
     assert k(1024, 1024, 1024) == "gemm_small<2, false, true>"
     assert k(1024, 320, 64, sums=True) == "gemm_kernel<false, true, false>"
     L = nxg.load_library()
