@@ -38,6 +38,9 @@
 #ifndef NXG_RELU2_RT
 #define NXG_RELU2_RT 1                     // relu^2 -> int8 with n_in 256 or 1024 on gemm_relu2_rt (0: gemm_relu2_q8)
 #endif
+#ifndef NXG_FSK_MAX_TILES_PER_CU
+#define NXG_FSK_MAX_TILES_PER_CU 2         // gemm_fsk while its 64-row tiles number at most this many per CU (0: never)
+#endif
 #ifndef NXG_SMALL_FN
 #define NXG_SMALL_FN 0                     // weight fragments per wave of gemm_small (0: chosen per launch)
 #endif
@@ -57,6 +60,7 @@ constexpr int WTHREADS = 512;    // relu^2 -> int8 GEMM: 8 waves, 2 x 4, each 64
 constexpr int N_XCD = 8;         // MI355X: 8 XCDs, workgroups dispatched round-robin
 constexpr int SDT = 2;           // few-row GEMMs: activation fragments (16 tokens each) per wave
 constexpr int SNB_MAX = 16;      // few-row GEMMs: 256-input blocks (n_in <= 4096), sw kept in LDS
+constexpr int FSK_NB = 9;        // few-row split-block GEMM: 256-input blocks (one wave each, n_in <= 2304)
 
 // LDS ring of gemm_kernel / gemm_k256: four slots of one 64-input k-step each, 8 A
 // fragments, 8 B fragments, then 1 KiB for a block's scales (sx of the tile's 128 rows
@@ -141,6 +145,13 @@ NXG_HD int a_frag(int mt, int i, int MF) { return imin(mt * (BM / 16) + i, MF - 
 NXG_HD int w_frag(int nt, int width, int i) { return nt * (width / 16) + i; }
 // gemm_relu2_rt: activation fragment row i (0 .. 3) of 64-row tile mt, clamped likewise.
 NXG_HD int a_frag_rt(int mt, int i, int MF) { return imin(mt * (RM / 16) + i, MF - 1); }
+// gemm_fsk: activation fragment row i (0 .. 3) of 64-row tile mt, clamped likewise; float
+// index of the 4 sx of row group g (0 .. 15) of 64-row tile mt, block B, groups past the last
+// one re-reading it.
+NXG_HD int fsk_a_frag(int mt, int i, int MF) { return imin(mt * 4 + i, MF - 1); }
+NXG_HD size_t fsk_sx_group(int mt, int g, int MF, int n_blk, int B) {
+    return ((size_t) imin(mt * 16 + g, MF * 4 - 1) * n_blk + B) * 4;
+}
 // Few-row GEMMs: activation fragment row j (0 .. SDT - 1) of piece row mt, clamped likewise.
 NXG_HD int small_a_frag(int mt, int j, int MF) { return imin(mt * SDT + j, MF - 1); }
 // Byte offset of lane `lane`'s 16 bytes of k-step ks of fragment row r.
@@ -229,13 +240,14 @@ enum gemm_kind : int {
     GEMM_SMALL = 3,      // gemm_small: few rows, one wave per 32 x 16fn piece
     GEMM_RELU2_Q8 = 4,   // gemm_relu2_q8: relu^2 -> int8, 128 x 256 tiles, one workgroup per CU
     GEMM_RELU2_SMALL = 5,// gemm_relu2_small: relu^2 -> int8 for few rows
-    GEMM_RELU2_RT = 6    // gemm_relu2_rt: relu^2 -> int8, 64 x 256 tiles, row tile in LDS, n_in 256 or 1024
+    GEMM_RELU2_RT = 6,   // gemm_relu2_rt: relu^2 -> int8, 64 x 256 tiles, row tile in LDS, n_in 256 or 1024
+    GEMM_FSK = 7         // gemm_fsk: few rows, one 64 x fn tile per workgroup, one wave per 256-input block
 };
 
 struct gemm_plan {
     gemm_kind kind;
     bool k256;           // n_in % 256 == 0
-    int fn;              // gemm_small: weight fragments per wave
+    int fn;              // gemm_small: weight fragments per wave; gemm_fsk: tile columns (64 or 32)
     int grid, block;     // workgroups, threads per workgroup
     int T, N, NP, KS, n_blk, MF, n_mt, n_nt, G, KSo;
 };
@@ -296,6 +308,23 @@ inline bool plan_gemm(int T, int n_in, int n_out, bool sums, bool relu2, int cus
     const long long G = (long long) pl.n_mt * pl.n_nt;
     if (G > INT32_MAX / 2) return false;
     pl.G = (int) G;
+    // Few rows with n_in % 256 == 0: one 64 x 64 tile per workgroup (64 x 32 from 5 blocks),
+    // one wave per 256-input block, while the tiles number at most NXG_FSK_MAX_TILES_PER_CU
+    // per CU.
+    if (!sums && pl.k256 && pl.N % 4 == 0 && pl.n_blk <= FSK_NB) {
+        const int tn = pl.n_blk <= 4 ? 64 : 32;
+        const long long G_fsk = (long long) ceil_div(T, 64) * ceil_div(pl.N, tn);
+        if (G_fsk <= (long long) NXG_FSK_MAX_TILES_PER_CU * cus) {
+            pl.kind = GEMM_FSK;
+            pl.fn = tn;
+            pl.n_mt = ceil_div(T, 64);
+            pl.n_nt = ceil_div(pl.N, tn);
+            pl.G = (int) G_fsk;
+            pl.grid = pl.G;
+            pl.block = 64 * (pl.n_blk > 4 ? pl.n_blk : 4);
+            return true;
+        }
+    }
     // Few rows, one wave per piece: 32 x 32 pieces while they number at most
     // NXG_SMALL_MAX_WAVES_PER_CU per CU, else 32 x 64 pieces (fewer bytes per output
     // through each CU) while those do; beyond that the 128 x 128 tiles, which read each

@@ -2543,6 +2543,111 @@ __global__ __launch_bounds__(64) void gemm_small(gemm_params p) {
     }
 }
 
+// fp32 rows out of a few-row GEMM with its 256-input blocks split over the waves of a
+// workgroup: one workgroup per 64 x TN output tile (TN = 64, or 32 for n_blk = 9), wave b
+// computes block b alone. Its 4 k-steps of the tile's 4 activation and TN / 16 weight
+// fragments are loaded straight into registers at once, so a launch spends one memory round
+// trip on its operands however long the input is, and a CU takes each operand byte once per
+// 64 x TN tile. The block's exact int32 sums go to LDS with the block's scales; after one
+// barrier, wave w (< 4) folds row group w of the tile over the blocks in order with the
+// reference's step f = fma((float) s * sx[t, b], sw[b, n], f) from +0, which gives the same
+// bits whatever wave computed a block (the int32 sums are exact), then adds the residual and
+// stores 16 bytes per lane and fragment. Workgroups of max(n_blk, 4) waves; n_in % 256 == 0,
+// n_blk <= NBM, N % 4 == 0. Instances: TN 64 for up to 4 blocks (64 KiB of LDS: two
+// workgroups per CU), TN 32 for up to 9 (9 waves, at most 168 registers each).
+template <int TN, int NBM, bool RES>
+__global__ __launch_bounds__(64 * (NBM > 4 ? NBM : 4)) void gemm_fsk(gemm_params p) {
+    constexpr int NJ = TN / 16;                      // weight fragments (16 columns each)
+    __shared__ __attribute__((aligned(16))) int32_t sums[NBM * 64 * TN];         // [b][(i NJ + j) 64 + lane][4]
+    __shared__ __attribute__((aligned(16))) float sxl[NBM * 64];                  // [b][row of the tile]
+    __shared__ __attribute__((aligned(16))) float swl[NBM * TN];                  // [b][column of the tile]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int) threadIdx.x >> 6);
+    const int mt = blockIdx.x / p.n_nt, nt = blockIdx.x - mt * p.n_nt;
+    const int nb = p.n_blk;
+    const size_t frow = (size_t) p.KS * FRAG;
+    if (wave < nb) {
+        const int b = wave;
+        // activation fragment rows 4 mt + i (past the last one: the last one, never stored),
+        // weight fragment rows nt NJ + j (NP is a multiple of 256: they exist)
+        const int8_t * abase[4];
+        const int8_t * wbase[NJ];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) abase[i] = p.a + (size_t) fsk_a_frag(mt, i, p.MF) * frow + (size_t) lane * 16;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) wbase[j] = p.w + (size_t) (nt * NJ + j) * frow + (size_t) lane * 16;
+        v4i oa[4][4], ob[4][NJ];                     // [k-step][fragment]
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const size_t ko = (size_t) (4 * b + s) * FRAG;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) oa[s][i] = *reinterpret_cast<const v4i *>(abase[i] + ko);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) ob[s][j] = *reinterpret_cast<const v4i *>(wbase[j] + ko);
+        }
+        // the block's scales: sx of the tile's 16 row groups of 4 (lanes 0..15; groups past the
+        // last one re-read it), sw of its TN columns (lanes 16..16 + TN / 4)
+        if (lane < 16) {
+            const v4f sx4 = *reinterpret_cast<const v4f *>(p.sx + fsk_sx_group(mt, lane, p.MF, nb, b));
+            *reinterpret_cast<v4f *>(sxl + b * 64 + 4 * lane) = sx4;
+        } else if (lane < 16 + TN / 4) {
+            const int c = 4 * (lane - 16);
+            *reinterpret_cast<v4f *>(swl + b * TN + c) = *reinterpret_cast<const v4f *>(p.sw + sw_index(b, p.NP, nt * TN + c));
+        }
+        v4i acc[4][NJ];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ob[s][j], oa[s][i], s == 0 ? v4i{0, 0, 0, 0} : acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+                *reinterpret_cast<v4i *>(sums + ((size_t) b * 64 * TN) + ((i * NJ + j) * 64 + lane) * 4) = acc[i][j];
+    }
+    __syncthreads();
+    if (wave >= 4) return;
+    // wave w: row group w, lane: token 64 mt + 16 w + lane % 16, columns 16 j + 4 (lane / 16) + r
+    const int t = mt * 64 + wave * 16 + (lane & 15);
+    const int c0 = 4 * (lane >> 4);
+    v4f rv[NJ];
+    if (RES) {
+        const int tr = clamp_row(t, p.T);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+            rv[j] = *reinterpret_cast<const v4f *>(p.res + (size_t) tr * p.N + clamp_col4(nt * TN + 16 * j + c0, p.N));
+    }
+    float f[NJ][4];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) f[j][r] = 0.0f;                  // the reference's f = 0 before block 0
+    for (int b = 0; b < nb; ++b) {
+        const float sxv = sxl[b * 64 + wave * 16 + (lane & 15)];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const v4i s4 = *reinterpret_cast<const v4i *>(sums + ((size_t) b * 64 * TN) + ((wave * NJ + j) * 64 + lane) * 4);
+            const v4f sw4 = *reinterpret_cast<const v4f *>(swl + b * TN + 16 * j + c0);
+            const float swr[4] = { sw4.x, sw4.y, sw4.z, sw4.w };
+#pragma unroll
+            for (int r = 0; r < 4; ++r) f[j][r] = __builtin_fmaf((float) s4[r] * sxv, swr[r], f[j][r]);
+        }
+    }
+    if (t >= p.T) return;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int n = nt * TN + 16 * j + c0;
+        if (n >= p.N) continue;
+        v4f y = { f[j][0], f[j][1], f[j][2], f[j][3] };
+        if (RES) y = rv[j] + y;
+        const out_map om = out_of(p, n);
+        *reinterpret_cast<v4f *>(om.base + (size_t) t * om.ld + om.col) = y;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Wide GEMM with the relu^2 -> int8 output: 128 x 256 tiles, n_in % 256 == 0
 // ---------------------------------------------------------------------------
@@ -3834,7 +3939,7 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     if (T == 0) return NXG_OK;
     const bool k256 = W->KS % 4 == 0;
     if (o.n_seg) {
-        // split output: n_in % 256 == 0 (gemm_k256 / gemm_small), boundaries at multiples of 64
+        // split output: n_in % 256 == 0 (gemm_k256 / gemm_small / gemm_fsk), boundaries at multiples of 64
         if (o.n_seg < 1 || o.n_seg > 4 || !o.seg_cols || !o.seg_out || o.residual || o.sums || o.qo) {
             return fail(NXG_EINVAL, "linear_split: n_seg=%d (1..4, no residual)", o.n_seg);
         }
@@ -3929,6 +4034,12 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
             else     { if (pl.k256) gemm_small<4, false, true><<<grid, block, 0, s>>>(p); else gemm_small<4, false, false><<<grid, block, 0, s>>>(p); }
         }
         return launch_check("gemm_small");
+    case GEMM_FSK:
+        if (!pl.k256 || p.n_blk > FSK_NB || p.n_nt * pl.fn < p.N || p.n_nt * pl.fn > p.NP)
+            return fail(NXG_EINVAL, "linear: plan/shape mismatch (split-block few-row GEMM)");
+        if (pl.fn == 64) { if (res) gemm_fsk<64, 4, true><<<grid, block, 0, s>>>(p); else gemm_fsk<64, 4, false><<<grid, block, 0, s>>>(p); }
+        else             { if (res) gemm_fsk<32, FSK_NB, true><<<grid, block, 0, s>>>(p); else gemm_fsk<32, FSK_NB, false><<<grid, block, 0, s>>>(p); }
+        return launch_check("gemm_fsk");
     case GEMM_SUMS:
         if (pl.k256) gemm_kernel<false, true, true><<<grid, block, 0, s>>>(p);
         else         gemm_kernel<false, true, false><<<grid, block, 0, s>>>(p);
@@ -4033,6 +4144,9 @@ const char * nxg_gemm_kernel_name(int32_t T, int32_t n_in, int32_t n_out, int32_
               { "gemm_small<4, true, false>", "gemm_small<4, true, true>" } } };
         return names[pl.fn == 4][res][pl.k256];
     }
+    case GEMM_FSK:
+        if (pl.fn == 64) return res ? "gemm_fsk<64, 4, true>" : "gemm_fsk<64, 4, false>";
+        return res ? "gemm_fsk<32, 9, true>" : "gemm_fsk<32, 9, false>";
     case GEMM_SUMS:  return pl.k256 ? "gemm_kernel<false, true, true>" : "gemm_kernel<false, true, false>";
     case GEMM_K256:  return res ? "gemm_k256<true>" : "gemm_k256<false>";
     case GEMM_GENERAL: break;

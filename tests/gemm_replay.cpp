@@ -373,6 +373,67 @@ void replay_small(replay & r, bool res) {
     }
 }
 
+// gemm_fsk: one workgroup per 64 x TN tile (TN = p.fn), wave b < n_blk loads block b's 4
+// k-steps of the tile's 4 activation and TN / 16 weight fragments and the block's scales into
+// LDS; waves 0..3 fold one row group each and store.
+void replay_fsk(replay & r, bool res) {
+    const gemm_plan & p = r.pl;
+    const int TN = p.fn, NJ = TN / 16, nb = p.n_blk;
+    if (!p.k256 || nb > FSK_NB || (TN != 64 && TN != 32) || (TN == 64 && nb > 4)) {
+        r.failf(1, "gemm_fsk: n_blk %d, TN %d", nb, TN);
+        return;
+    }
+    const int NBM = TN == 64 ? 4 : FSK_NB;
+    const size_t frow = (size_t) p.KS * FRAG;
+    const size_t sums = (size_t) NBM * 64 * TN * 4, sxl = (size_t) NBM * 64 * 4, swl = (size_t) NBM * TN * 4;
+    const int seg_ids[4] = { SEG0, SEG1, SEG2, SEG3 };
+    if (p.block != 64 * (nb > 4 ? nb : 4)) r.failf(1, "gemm_fsk: %d threads for %d blocks", p.block, nb);
+    for (int wg = 0; wg < p.grid && !r.status; ++wg) {
+        const int mt = wg / p.n_nt, nt = wg - mt * p.n_nt;
+        for (int b = 0; b < nb; ++b)
+            for (int lane = 0; lane < 64; ++lane) {
+                for (int s = 0; s < 4; ++s) {
+                    const size_t ko = (size_t) (4 * b + s) * FRAG + (size_t) lane * 16;
+                    for (int i = 0; i < 4; ++i)
+                        r.load(A, (size_t) fsk_a_frag(mt, i, p.MF) * frow + ko, 16, wg, b, lane, "gemm_fsk A fragment");
+                    for (int j = 0; j < NJ; ++j)
+                        r.load(W, (size_t) (nt * NJ + j) * frow + ko, 16, wg, b, lane, "gemm_fsk B fragment");
+                }
+                if (lane < 16) {
+                    r.load(SX, fsk_sx_group(mt, lane, p.MF, nb, b) * 4, 16, wg, b, lane, "gemm_fsk sx");
+                    r.lds(((size_t) b * 64 + 4 * lane) * 4, 16, sxl, wg, b, lane, "gemm_fsk sx");
+                } else if (lane < 16 + TN / 4) {
+                    const int c = 4 * (lane - 16);
+                    r.load(SW, sw_index(b, p.NP, nt * TN + c) * 4, 16, wg, b, lane, "gemm_fsk sw");
+                    r.lds(((size_t) b * TN + c) * 4, 16, swl, wg, b, lane, "gemm_fsk sw");
+                }
+                for (int i = 0; i < 4; ++i)
+                    for (int j = 0; j < NJ; ++j)
+                        r.lds(((size_t) b * 64 * TN + (size_t) ((i * NJ + j) * 64 + lane) * 4) * 4, 16, sums, wg, b, lane,
+                              "gemm_fsk sums");
+            }
+        for (int w = 0; w < 4; ++w)
+            for (int lane = 0; lane < 64; ++lane) {
+                const int t = mt * 64 + w * 16 + (lane & 15), c0 = 4 * (lane >> 4);
+                for (int j = 0; j < NJ; ++j) {
+                    if (res)
+                        r.load(RES, ((size_t) clamp_row(t, p.T) * p.N + clamp_col4(nt * TN + 16 * j + c0, p.N)) * 4, 16, wg, w,
+                               lane, "gemm_fsk residual");
+                    for (int b = 0; b < nb; ++b) {
+                        r.lds(((size_t) b * 64 * TN + (size_t) ((w * NJ + j) * 64 + lane) * 4) * 4, 16, sums, wg, w, lane,
+                              "gemm_fsk fold");
+                        r.lds(((size_t) b * TN + 16 * j + c0) * 4, 16, swl, wg, w, lane, "gemm_fsk fold sw");
+                        r.lds(((size_t) b * 64 + w * 16 + (lane & 15)) * 4, 4, sxl, wg, w, lane, "gemm_fsk fold sx");
+                    }
+                    const int n = nt * TN + 16 * j + c0;
+                    if (t >= p.T || n >= p.N) continue;
+                    const out_col<int> om = out_col_of<int>(n, p.N, r.n_seg, r.seg_end, (int) OUT, seg_ids);
+                    r.store(om.base, ((size_t) t * om.ld + om.col) * 4, 16, wg, w, lane, "gemm_fsk output");
+                }
+            }
+    }
+}
+
 // --- relu^2 -> int8 outputs -----------------------------------------------------------
 
 // The stores of fragment row rf, fragment column kf (one wave's 64 lanes), and with
@@ -600,7 +661,7 @@ extern "C" int gemm_replay(int T, int n_in, int n_out, int mode, int n_seg, cons
     }
     const gemm_plan & p = r.pl;
     *kind = (int) p.kind;
-    if (n_seg > 0 && (p.kind != GEMM_K256 && p.kind != GEMM_SMALL)) {
+    if (n_seg > 0 && (p.kind != GEMM_K256 && p.kind != GEMM_SMALL && p.kind != GEMM_FSK)) {
         snprintf(err, (size_t) err_len, "split output on kernel %d", (int) p.kind);
         return 3;
     }
@@ -629,6 +690,7 @@ extern "C" int gemm_replay(int T, int n_in, int n_out, int mode, int n_seg, cons
     case GEMM_GENERAL: replay_general(r, res, false); break;
     case GEMM_SUMS: replay_general(r, false, true); break;
     case GEMM_SMALL: replay_small(r, res); break;
+    case GEMM_FSK: replay_fsk(r, res); break;
     case GEMM_RELU2_Q8: replay_relu2_q8(r); break;
     case GEMM_RELU2_SMALL: replay_relu2_small(r); break;
     case GEMM_RELU2_RT: replay_relu2_rt(r); break;

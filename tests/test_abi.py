@@ -104,7 +104,10 @@ def test_gemm_kernel_name(nxg):
     assert k(65536, 2304, 1024, relu2=True, act_max=63) == "gemm_relu2_q8<63>"
     assert k(768, 1024, 2304, relu2=True) == "gemm_relu2_small<127>"     # 216 workgroups: one per CU
     assert k(1024, 1024, 2304, relu2=True) == "gemm_relu2_rt<127, 4>"    # 288 would be: the row tiles
-    assert k(1024, 1024, 1024) == "gemm_small<2, false, true>"
+    assert k(1024, 1024, 1024) == "gemm_fsk<64, 4, false>"               # 256 tiles of 64 x 64
+    assert k(1024, 2304, 1024, residual=True) == "gemm_fsk<32, 9, true>"  # 9 blocks: 64 x 32 tiles
+    assert k(1024, 1024, 3072) == "gemm_k256<false>"                      # 768 tiles: more than 2 per CU
+    assert k(1024, 320, 1024) == "gemm_small<2, false, false>"           # n_in % 256 != 0
     assert k(1024, 320, 64, sums=True) == "gemm_kernel<false, true, false>"
     L = nxg.load_library()
     assert L.nxg_gemm_kernel_name(64, 1024, 2304, nxg.GEMM_RELU2 | nxg.GEMM_RESIDUAL, 256) is None

@@ -23,7 +23,7 @@ SRC = ROOT / "tests" / "gemm_replay.cpp"
 
 FP32, RESIDUAL, SUMS, RELU2 = 0, 1, 2, 3
 KINDS = {0: "gemm_kernel", 1: "gemm_kernel sums", 2: "gemm_k256", 3: "gemm_small", 4: "gemm_relu2_q8",
-         5: "gemm_relu2_small", 6: "gemm_relu2_rt"}
+         5: "gemm_relu2_small", 6: "gemm_relu2_rt", 7: "gemm_fsk"}
 
 
 def _build(out_dir: Path, header_text: str = None) -> ctypes.CDLL:
@@ -148,7 +148,10 @@ PLANTS = [
     ("a_frag", r"return imin\(mt \* \(BM / 16\) \+ i, MF - 1\);", "return mt * (BM / 16) + i;",
      (4100, 1024, 1024, FP32), "a bytes"),
     # few-row pieces' fragment rows
-    ("small_a_frag", r"return imin\(mt \* SDT \+ j, MF - 1\);", "return mt * SDT + j;", (33, 256, 260, FP32), "past its"),
+    ("small_a_frag", r"return imin\(mt \* SDT \+ j, MF - 1\);", "return mt * SDT + j;", (33, 320, 260, FP32), "past its"),
+    # the split-block few-row tiles' fragment rows and sx groups
+    ("fsk_a_frag", r"return imin\(mt \* 4 \+ i, MF - 1\);", "return mt * 4 + i;", (33, 1024, 260, RESIDUAL), "a bytes"),
+    ("fsk_sx_group", r"imin\(mt \* 16 \+ g, MF \* 4 - 1\)", "(mt * 16 + g)", (33, 2304, 260, FP32), "sx bytes"),
     # the sx groups of a partial row tile
     ("sx_group_index", r"imin\(mt \* \(BM / 4\) \+ g, MF \* 4 - 1\)", "(mt * (BM / 4) + g)", (4100, 1024, 1024, FP32),
      "sx bytes"),

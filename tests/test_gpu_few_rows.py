@@ -1,12 +1,13 @@
-"""GPU: the few-row GEMMs (gemm_small with 32 x 32 and 32 x 64 pieces, gemm_relu2_small)
-give the reference's bits, and a sequence's rows are the same whichever kernel a batch
-size selects.
+"""GPU: the few-row GEMMs (gemm_fsk with 64 x 64 and 64 x 32 tiles, gemm_small with 32 x 32
+and 32 x 64 pieces, gemm_relu2_small) give the reference's bits, and a sequence's rows are the
+same whichever kernel a batch size selects.
 
-The kernel is chosen per launch from the number of one-wave pieces per CU: 32 x 32
-pieces while they number at most 4 per CU, else 32 x 64 pieces while those do, else the
-128 x 128 tiles; for c_fc -> relu^2 -> int8, the few-row kernel while its waves number at
-most 6 per CU. The shapes below are picked for MI355X's 256 CUs (noted per case); on
-another device they still run, through whichever kernel it selects."""
+The kernel is chosen per launch: for n_in % 256 == 0 and at most 9 blocks, gemm_fsk (one
+wave per 256-input block) while its 64-row tiles number at most 2 per CU; else one-wave
+pieces, 32 x 32 while they number at most 4 per CU, 32 x 64 while those do, else the
+128 x 128 tiles; for c_fc -> relu^2 -> int8, the few-row kernel while its workgroups fit
+one per CU. The shapes below are picked for MI355X's 256 CUs (noted per case); on another
+device they still run, through whichever kernel it selects."""
 from __future__ import annotations
 
 import numpy as np
@@ -56,17 +57,20 @@ def oracle_linear(orc, W, q_ref, sx_ref, res=None):
 
 # (T, n_in, n_out): route on 256 CUs
 FEW_ROW_SHAPES = [
-    (1000, 1024, 1024),   # 32 x 32 pieces (1024 waves), 4 blocks
-    (1000, 1024, 1000),   # 32 x 32, last feature piece partly past n_out
-    (333, 768, 260),      # 32 x 32, 3 blocks, ragged rows and columns
-    (700, 1280, 1000),    # 32 x 32, 5 blocks (an odd block count: the one-block tail of the ring)
-    (1000, 320, 1024),    # 32 x 32, n_in % 256 != 0: last block of one k-step
-    (1000, 2304, 512),    # 32 x 32, 9 blocks: the odd last block
-    (1000, 1024, 2048),   # 32 x 64 pieces (2048 > 1024 32 x 32 pieces)
-    (1000, 2304, 2000),   # 32 x 64, 9 blocks, last piece partly past n_out
-    (1000, 96, 2048),     # 32 x 64, one partial block of 2 k-steps
-    (5, 64, 4),           # one piece, one k-step
-    (1, 4096, 64),        # 16 blocks: the most whose sw the few-row kernels keep in LDS
+    (1000, 1024, 1024),   # gemm_fsk 64 x 64 tiles (256), 4 blocks
+    (1000, 1024, 1000),   # gemm_fsk, last column tile partly past n_out
+    (333, 768, 260),      # gemm_fsk, 3 blocks (a fold-only wave), ragged rows and columns
+    (1000, 256, 1024),    # gemm_fsk, one block
+    (300, 512, 520),      # gemm_fsk, 2 blocks, a last column tile of 8
+    (700, 1280, 1000),    # gemm_fsk 64 x 32 tiles, 5 blocks
+    (1000, 2304, 512),    # gemm_fsk 64 x 32 tiles, 9 blocks
+    (2000, 1024, 1024),   # gemm_fsk, 512 tiles: 2 per CU
+    (1000, 1024, 2048),   # gemm_fsk, 512 tiles
+    (1000, 320, 1024),    # gemm_small 32 x 32, n_in % 256 != 0: last block of one k-step
+    (1000, 2304, 2000),   # gemm_small 32 x 64, 9 blocks (1008 gemm_fsk tiles), last piece partly past n_out
+    (1000, 96, 2048),     # gemm_small 32 x 64, one partial block of 2 k-steps
+    (5, 64, 4),           # gemm_small, one piece, one k-step
+    (1, 4096, 64),        # gemm_small, 16 blocks: the most whose sw the few-row kernels keep in LDS
     (100, 4352, 256),     # 17 blocks: the 128 x 128 kernel
 ]
 

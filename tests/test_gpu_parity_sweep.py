@@ -3,7 +3,9 @@
 Rows, inputs and outputs are drawn so that every kernel the launcher can pick is reached:
 the few-row pieces (gemm_small, gemm_relu2_small), the 128 x 128 tiles with and without a
 per-tile schedule (gemm_k256, gemm_kernel), the 128 x 256 relu^2 tiles (gemm_relu2_q8) and
-the 64 x 256 relu^2 tiles over an LDS-resident row tile (gemm_relu2_rt), with ragged rows, partial column tiles, residuals and both activation ranges. Each case prints
+the 64 x 256 relu^2 tiles over an LDS-resident row tile (gemm_relu2_rt), with ragged rows,
+partial column tiles, residuals and both activation ranges; two relu^2 shapes of 17,000 to
+30,000 rows give workgroups spans that cross row tiles. Each case prints
 its index, shape and kernel before it touches the GPU.
 """
 from __future__ import annotations
@@ -20,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 ROOT = Path(__file__).resolve().parents[1]
 KINDS = {0: "gemm_kernel", 2: "gemm_k256", 3: "gemm_small", 4: "gemm_relu2_q8", 5: "gemm_relu2_small",
-         6: "gemm_relu2_rt"}
+         6: "gemm_relu2_rt", 7: "gemm_fsk"}
 
 
 def say(msg):
@@ -47,6 +49,12 @@ def _cases(n=24, seed=2024):
             n_in = int(rng.choice([32, 64, 96, 256, 320, 512, 1024, 1280, 2304]))
             n_out = int(rng.choice([4 * int(rng.integers(1, 640)), int(rng.integers(1, 300))]))
         out.append((i, max(T, 1), n_in, n_out, relu2, bool(rng.integers(0, 2)), int(rng.choice([127, 63]))))
+    # relu^2 at 17,000..30,000 rows: spans of several row tiles per workgroup
+    for i in (n, n + 1):
+        T = int(rng.integers(17000, 30001))
+        n_in = int(rng.choice([256, 1024]))
+        n_out = 32 * int(rng.integers(48, 81))
+        out.append((i, T, n_in, n_out, True, False, int(rng.choice([127, 63]))))
     return out
 
 

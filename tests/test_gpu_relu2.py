@@ -92,7 +92,9 @@ def test_quantize_relu2_matches_oracle(nxg, orc, torch, dev, act_max):
 
 
 # (T, n_in, n_out) for c_fc -> relu^2 -> int8; n_out % 32 == 0, n_in % 256 == 0
-RELU2_SHAPES = [(4096, 1024, 2304),   # the MLP's c_fc, 4 blocks, 9 column tiles (64 x 256 row-tile kernel)
+RELU2_SHAPES = [(20000, 1024, 2304),  # the MLP's c_fc, a 32-row last row tile, spans across row tiles
+                (33000, 256, 1216),   # one block; a 40-row last row tile, 192-column last tile
+                (4096, 1024, 2304),   # the MLP's c_fc, 4 blocks, 9 column tiles (64 x 256 row-tile kernel)
                 (5000, 1024, 1216),   # row-tile kernel: a partial last row tile (8 rows), a 192-column last tile
                 (20000, 1024, 320),   # row-tile kernel: spans that start inside a row tile, 2 column tiles
                 (9000, 512, 1216),    # 2 blocks (128 x 256 kernel), ragged rows, a 192-column last tile
@@ -155,16 +157,15 @@ def test_linear_relu2_q8_packed_batch(nxg, orc, torch, dev, lengths):
     assert (bits(sa_m[s0:s1]) == bits(sc_m)).all() and sa_m.shape[1] == n_blk
 
 
-@pytest.mark.parametrize("n_in", [1024, 512])
-def test_linear_relu2_q8_overflowing_rows(nxg, orc, torch, dev, n_in):
+@pytest.mark.parametrize("n_in,T,n_out", [(1024, 20000, 2304), (1024, 8200, 512), (512, 8200, 512)])
+def test_linear_relu2_q8_overflowing_rows(nxg, orc, torch, dev, n_in, T, n_out):
     """Rows whose fp32 sums overflow: relu^2 gives +Inf, the row maximum is infinite and the
     quantization takes the reference's NaN path (x * 0 for the infinite values). Waves that
     hold such a row use the full CVTPS2DQ statement, the others the packed conversion; both
     against the oracle chain, on the many-row kernels (T >= 8192): the row-tile kernel
-    (n_in 1024) and the 128 x 256 one (n_in 512)."""
-    say(f"linear_relu2_q8 with overflowing rows, n_in={n_in}")
+    (n_in 1024, at 20,000 x 2,304 and 8,200 x 512) and the 128 x 256 one (n_in 512)."""
+    say(f"linear_relu2_q8 with overflowing rows, n_in={n_in} T={T} n_out={n_out}")
     rng = np.random.default_rng(11)
-    T, n_out = 8200, 512
     x = rng.standard_normal((T, n_in)).astype(np.float32)
     x[5, :] *= np.float32(3e37)          # every block of the row: sums reach the fp32 limit
     x[4100, ::3] = np.float32(-2e38)     # a row of mixed signs in another tile
@@ -186,8 +187,8 @@ def test_linear_relu2_q8_overflowing_rows(nxg, orc, torch, dev, n_in):
         assert ((bits(s) == bits(rsx_ref)) | (np.isnan(s) & np.isnan(rsx_ref))).all(), f"act_max={act_max}"
 
 
-@pytest.mark.parametrize("n_in", [1024, 512])
-def test_linear_relu2_q8_tiny_row_maxima(nxg, orc, torch, dev, n_in):
+@pytest.mark.parametrize("n_in,T,n_out", [(1024, 20000, 2304), (1024, 8200, 512), (512, 8200, 512)])
+def test_linear_relu2_q8_tiny_row_maxima(nxg, orc, torch, dev, n_in, T, n_out):
     """Rows whose relu^2 maximum is positive but below ACT_MAX / FLT_MAX (normal and
     denormal), so that inv = ACT_MAX / amax overflows to +Inf: the reference's CVTPS2DQ then
     gives 0x80000000 for every value of the row (u8 0). Rows are scaled by powers of two, which
@@ -196,9 +197,8 @@ def test_linear_relu2_q8_tiny_row_maxima(nxg, orc, torch, dev, n_in):
     2^-70: a denormal maximum; 2^-80: relu^2 underflows to 0). T >= 8192 keeps the many-row
     kernels (the row-tile one at n_in 1024, the 128 x 256 one at 512); checked against the
     oracle chain and against the two-step path."""
-    say(f"linear_relu2_q8 with tiny row maxima, n_in={n_in}")
+    say(f"linear_relu2_q8 with tiny row maxima, n_in={n_in} T={T} n_out={n_out}")
     rng = np.random.default_rng(12)
-    T, n_out = 8200, 512
     x = rng.standard_normal((T, n_in)).astype(np.float32)
     scaled = {5: -62, 6: -65, 70: -64, 3000: -70, 3001: -62, 6000: -80, 8195: -65}
     for t, e in scaled.items():
