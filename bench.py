@@ -88,7 +88,7 @@ def time_steps(path, steps: int, warmup: int):
     total_ms = s0.elapsed_time(s1)
     gemm_ms = {}
     for a, b, g, kind, rows, res in gemm_ev:
-        k = "relu2" if kind == "relu2" else "fp32"
+        k = "relu2" if kind in ("relu2", "relu2_f32") else "fp32"
         gemm_ms[k] = gemm_ms.get(k, 0.0) + a.elapsed_time(b) / steps
     quant_ms = sum(e[0].elapsed_time(e[1]) for e in quant_ev)
     return total_ms / steps, wall / steps * 1e3, gemm_ms, quant_ms / steps, gemm_ev, quant_ev
@@ -123,16 +123,17 @@ def roofline_of(kernel: str, n_launch: int, ms_total: float, ops: int, nbytes: i
 def kernel_rooflines(nxg, gemm_ev, quant_ev, steps: int) -> list:
     """One roofline object per kernel the step launches (the GEMM kernel of each launch as
     the launch plan picks it, nxg_gemm_kernel_name; the quantize kernel), most time first."""
-    from nexterabert_cpp_amd.encoder import gemm_bytes, quantize_bytes
+    from nexterabert_cpp_amd.encoder import gemm_bytes, gemm_f32_relu2_bytes, quantize_bytes
     acc = {}
     for a, b, g, kind, rows, res in gemm_ev:
-        relu2 = kind == "relu2"
-        name = nxg.gemm_kernel_name(rows, g.n_in, g.n_out, residual=res, relu2=relu2)
+        relu2, f32_in = kind in ("relu2", "relu2_f32"), kind == "relu2_f32"
+        name = nxg.gemm_kernel_name(rows, g.n_in, g.n_out, residual=res, relu2=relu2, f32_in=f32_in)
         d = acc.setdefault(name, [0, 0.0, 0, 0])
         d[0] += 1
         d[1] += a.elapsed_time(b)
         d[2] += 2 * rows * g.n_in * g.n_out
-        d[3] += gemm_bytes(rows, g.n_in, g.n_out, relu2, res)
+        d[3] += (gemm_f32_relu2_bytes(rows, g.n_in, g.n_out) if f32_in
+                 else gemm_bytes(rows, g.n_in, g.n_out, relu2, res))
     for a, b, rows, n_in, relu2 in quant_ev:
         d = acc.setdefault(f"quantize_kernel<127, {int(relu2)}>", [0, 0.0, 0, 0])
         d[0] += 1
@@ -145,22 +146,23 @@ def kernel_rooflines(nxg, gemm_ev, quant_ev, steps: int) -> list:
 def shape_table(gemm_ev, steps: int) -> list:
     """Per GEMM shape of the step: average launch time, int8 TOPS, and the shape's roofline
     bound min(MFMA peak, AI x HBM peak) with the fraction of it reached."""
-    from nexterabert_cpp_amd.encoder import gemm_bytes
+    from nexterabert_cpp_amd.encoder import gemm_bytes, gemm_f32_relu2_bytes
     acc = {}
     for a, b, g, kind, rows, res in gemm_ev:
-        relu2 = kind == "relu2"
-        k = (rows, g.n_in, g.n_out, bool(res), relu2)
+        relu2, f32_in = kind in ("relu2", "relu2_f32"), kind == "relu2_f32"
+        k = (rows, g.n_in, g.n_out, bool(res), relu2, f32_in)
         d = acc.setdefault(k, [0, 0.0, g.name])
         d[0] += 1
         d[1] += a.elapsed_time(b)
     out = []
-    for (rows, n_in, n_out, res, relu2), (n, ms, name) in acc.items():
+    for (rows, n_in, n_out, res, relu2, f32_in), (n, ms, name) in acc.items():
         ops = 2 * rows * n_in * n_out
-        nb = gemm_bytes(rows, n_in, n_out, relu2, res)
+        nb = gemm_f32_relu2_bytes(rows, n_in, n_out) if f32_in else gemm_bytes(rows, n_in, n_out, relu2, res)
         avg_us = ms * 1e3 / n
         tops = ops / (avg_us * 1e-6) / 1e12
         bound = min(PEAK_INT8_TOPS, ops / nb * PEAK_HBM_GBS / 1e3)
-        out.append({"shape": f"{rows}x{n_in}->{n_out}" + (" +res" if res else "") + (" relu2->int8" if relu2 else ""),
+        out.append({"shape": f"{rows}x{n_in}->{n_out}" + (" +res" if res else "") + (" relu2->int8" if relu2 else "")
+                    + (" from fp32 rows" if f32_in else ""),
                     "example": name.split(".")[-2] if "." in name else name,
                     "launches_per_step": round(n / steps, 2), "avg_us": round(avg_us, 2),
                     "int8_tops": round(tops, 1), "pct_of_mfma_peak": round(100 * tops / PEAK_INT8_TOPS, 2),

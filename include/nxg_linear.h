@@ -374,6 +374,24 @@ NXG_API int32_t nxg_linear_i8_relu2_q8(const nxg_weight * w, const int8_t * q, c
 NXG_API int32_t nxg_linear_i8_relu2_q8_rows(const nxg_weight * w, const int8_t * q, const float * sx, int32_t T,
                                             int32_t act_max, int8_t * q_out, float * sx_out, void * stream);
 
+/* The same from fp32 rows, as op_linear_i8 takes them (src/nexterabert.cpp:969-1007: the
+ * input rows quantized by quantize_row, :378-403, then the int8 GEMM): x device float
+ * [T][n_in], 16-byte aligned; act_max that of the model (the input's quantization and the
+ * output's), 127 or 63. The result equals nxg_quantize_rows(x) followed by
+ * nxg_linear_i8_relu2_q8_rows, bit for bit. Where the row-tile kernel runs (n_in 256 or 1024)
+ * with at least 4 tiles of 64 rows by 256 outputs per workgroup (two workgroups per compute
+ * unit: 16,384 rows of 2,304 outputs on 256 CUs), each row tile is quantized inside the GEMM
+ * and the int8 input never goes to memory; otherwise q_ws, sx_ws (a qact of T rows by n_in, nxg_qact_q_bytes(T, n_in) and
+ * nxg_qact_sx_bytes(T, n_in) bytes) receive nxg_quantize_rows(x) first. */
+NXG_API int32_t nxg_linear_f32_relu2_q8_rows(const nxg_weight * w, const float * x, int32_t T, int32_t act_max,
+                                             int8_t * q_ws, float * sx_ws, int8_t * q_out, float * sx_out,
+                                             void * stream);
+
+/* The same over a packed batch: T = cu_offsets[n_seqs] (host int32, as nxg_linear_i8). */
+NXG_API int32_t nxg_linear_f32_relu2_q8(const nxg_weight * w, const float * x, const int32_t * cu_offsets,
+                                        int32_t n_seqs, int32_t act_max, int8_t * q_ws, float * sx_ws,
+                                        int8_t * q_out, float * sx_out, void * stream);
+
 /* The int32 block sums s_B of the same GEMM: sums device int32 [n_blk][T][n_out],
  * equal to the reference's sum_i w8*u8 + off (src/nexterabert.cpp:892-916). For tests. */
 NXG_API int32_t nxg_linear_i8_block_sums(const nxg_weight * w, const int8_t * q, int32_t T,
@@ -384,12 +402,16 @@ NXG_API int32_t nxg_linear_i8_block_sums(const nxg_weight * w, const int8_t * q,
  * its template instance (e.g. "gemm_k256<true>"), for a device of `cus` compute units
  * (cus <= 0: the current device, which must be a gfx950 GPU). flags: NXG_GEMM_RESIDUAL
  * (nxg_linear_i8 with a residual), NXG_GEMM_RELU2 (nxg_linear_i8_relu2_q8; with
- * NXG_GEMM_ACT63 for act_max 63), NXG_GEMM_SUMS (nxg_linear_i8_block_sums). A static
- * string, or NULL for a shape or flag combination the entry points refuse. */
+ * NXG_GEMM_ACT63 for act_max 63, with NXG_GEMM_F32_IN for nxg_linear_f32_relu2_q8_rows, whose
+ * shapes without the fused row-tile kernel, or with too few row tiles per workgroup, run the
+ * quantize kernel, then the one named),
+ * NXG_GEMM_SUMS (nxg_linear_i8_block_sums). A static string, or NULL for a shape or flag
+ * combination the entry points refuse. */
 #define NXG_GEMM_RESIDUAL 1
 #define NXG_GEMM_RELU2    2
 #define NXG_GEMM_SUMS     4
 #define NXG_GEMM_ACT63    8
+#define NXG_GEMM_F32_IN   16
 NXG_API const char * nxg_gemm_kernel_name(int32_t T, int32_t n_in, int32_t n_out, int32_t flags, int32_t cus);
 
 #ifdef __cplusplus

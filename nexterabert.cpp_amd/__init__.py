@@ -121,6 +121,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nxg_linear_i8_block_sums": ([P, P, i32, P, P], i32),
         "nxg_linear_i8_relu2_q8": ([P, P, P, P, i32, i32, P, P, P], i32),
         "nxg_linear_i8_relu2_q8_rows": ([P, P, P, i32, i32, P, P, P], i32),
+        "nxg_linear_f32_relu2_q8_rows": ([P, P, i32, i32, P, P, P, P, P], i32),
+        "nxg_linear_f32_relu2_q8": ([P, P, P, i32, i32, P, P, P, P, P], i32),
         "nxg_gemm_kernel_name": ([i32, i32, i32, i32, i32], ctypes.c_char_p),
         # include/nxg_gguf.h
         "nxg_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(P)], i32),
@@ -772,15 +774,15 @@ def linear_i8(weight: DeviceWeight, qa: QAct, residual=None, cu_offsets: Optiona
     return out
 
 
-GEMM_RESIDUAL, GEMM_RELU2, GEMM_SUMS, GEMM_ACT63 = 1, 2, 4, 8
+GEMM_RESIDUAL, GEMM_RELU2, GEMM_SUMS, GEMM_ACT63, GEMM_F32_IN = 1, 2, 4, 8, 16
 
 
 def gemm_kernel_name(T: int, n_in: int, n_out: int, residual: bool = False, relu2: bool = False,
-                     act_max: int = 127, sums: bool = False, cus: int = 0) -> str:
+                     act_max: int = 127, sums: bool = False, cus: int = 0, f32_in: bool = False) -> str:
     """The kernel a GEMM of this shape launches, as the profiler names its template instance
-    (nxg_gemm_kernel_name); cus = 0 asks the current device."""
+    (nxg_gemm_kernel_name); cus = 0 asks the current device. f32_in: linear_f32_relu2_q8."""
     flags = ((GEMM_RESIDUAL if residual else 0) | (GEMM_RELU2 if relu2 else 0) | (GEMM_SUMS if sums else 0)
-             | (GEMM_ACT63 if relu2 and act_max == 63 else 0))
+             | (GEMM_ACT63 if relu2 and act_max == 63 else 0) | (GEMM_F32_IN if f32_in else 0))
     name = load_library().nxg_gemm_kernel_name(T, n_in, n_out, flags, cus)
     if name is None:
         raise ValueError(f"gemm_kernel_name: no kernel for T={T} n_in={n_in} n_out={n_out} flags={flags}")
@@ -834,6 +836,36 @@ def linear_i8_relu2_q8(weight: DeviceWeight, qa: QAct, act_max: int = 127,
         rc = L.nxg_linear_i8_relu2_q8_rows(weight.handle, qa.q.data_ptr(), qa.sx.data_ptr(), T, act_max,
                                            res.q.data_ptr(), res.sx.data_ptr(), _stream_ptr(stream))
     _check(rc, "linear_i8_relu2_q8")
+    return res
+
+
+def linear_f32_relu2_q8(weight: DeviceWeight, x, act_max: int = 127, cu_offsets: Optional[Sequence[int]] = None,
+                        out: Optional[QAct] = None, workspace: Optional[QAct] = None, stream=None) -> QAct:
+    """op_linear_i8 from fp32 rows for c_fc -> relu^2 -> int8 (nxg_linear_f32_relu2_q8): the
+    same qact as linear_i8_relu2_q8(weight, quantize_rows(x, act_max), act_max). The row-tile
+    kernel quantizes x inside the GEMM; other shapes quantize into `workspace` (a qact of x's
+    shape, allocated when not given) first."""
+    torch = _torch()
+    if x.dtype != torch.float32 or x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
+        raise ValueError("x: a contiguous float32 CUDA tensor [T][n_in]")
+    T, n_in = int(x.shape[0]), int(x.shape[1])
+    if n_in != weight.n_in:
+        raise ValueError(f"n_in mismatch: activations {n_in}, weight {weight.n_in}")
+    res = out if out is not None else qact_alloc(T, weight.n_out, act_max, x.device)
+    res.T, res.n_in, res.act_max = T, weight.n_out, act_max
+    ws = workspace if workspace is not None else qact_alloc(T, n_in, act_max, x.device)
+    _order_on(stream, res.q, res.sx, x, ws.q, ws.sx)
+    L = load_library()
+    if cu_offsets is not None:
+        cu = np.ascontiguousarray(cu_offsets, dtype=np.int32)
+        if cu.size < 2 or int(cu[-1]) != T:
+            raise ValueError(f"cu_offsets must end at T={T}")
+        rc = L.nxg_linear_f32_relu2_q8(weight.handle, x.data_ptr(), _np_ptr(cu), cu.size - 1, act_max, ws.q.data_ptr(),
+                                       ws.sx.data_ptr(), res.q.data_ptr(), res.sx.data_ptr(), _stream_ptr(stream))
+    else:
+        rc = L.nxg_linear_f32_relu2_q8_rows(weight.handle, x.data_ptr(), T, act_max, ws.q.data_ptr(), ws.sx.data_ptr(),
+                                            res.q.data_ptr(), res.sx.data_ptr(), _stream_ptr(stream))
+    _check(rc, "linear_f32_relu2_q8")
     return res
 
 

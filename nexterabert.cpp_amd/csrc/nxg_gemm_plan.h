@@ -41,6 +41,9 @@
 #ifndef NXG_FSK_MAX_TILES_PER_CU
 #define NXG_FSK_MAX_TILES_PER_CU 2         // gemm_fsk while its 64-row tiles number at most this many per CU (0: never)
 #endif
+#ifndef NXG_RELU2_FQ_MIN_TILES_PER_WG
+#define NXG_RELU2_FQ_MIN_TILES_PER_WG 4    // fp32 input rows quantized inside gemm_relu2_rt from this many tiles per workgroup
+#endif
 #ifndef NXG_SMALL_FN
 #define NXG_SMALL_FN 0                     // weight fragments per wave of gemm_small (0: chosen per launch)
 #endif
@@ -145,6 +148,9 @@ NXG_HD int a_frag(int mt, int i, int MF) { return imin(mt * (BM / 16) + i, MF - 
 NXG_HD int w_frag(int nt, int width, int i) { return nt * (width / 16) + i; }
 // gemm_relu2_rt: activation fragment row i (0 .. 3) of 64-row tile mt, clamped likewise.
 NXG_HD int a_frag_rt(int mt, int i, int MF) { return imin(mt * (RM / 16) + i, MF - 1); }
+// gemm_relu2_rt quantizing fp32 rows: the input row that row r (0 .. 63) of row tile mt reads,
+// the last row for rows past T (quantized as zeros, never stored).
+NXG_HD int rt_x_row(int mt, int r, int T) { return imin(mt * RM + r, T - 1); }
 // gemm_fsk: activation fragment row i (0 .. 3) of 64-row tile mt, clamped likewise; float
 // index of the 4 sx of row group g (0 .. 15) of 64-row tile mt, block B, groups past the last
 // one re-reading it.
@@ -351,6 +357,17 @@ inline bool plan_gemm(int T, int n_in, int n_out, bool sums, bool relu2, int cus
     pl.block = NTHREADS;
     pl.kind = sums ? GEMM_SUMS : (persistent && pl.N % 4 == 0) ? GEMM_K256 : GEMM_GENERAL;
     return true;
+}
+
+// nxg_linear_f32_relu2_q8: whether the row-tile kernel quantizes the fp32 input rows itself.
+// Each workgroup then reads its row tiles' fp32 rows (4 bytes per input instead of 1) with
+// no other work to hide them under; from about four tiles per workgroup the quantize launch
+// this saves outweighs that (measured on MI355X, one encoder forward's linear path with the
+// 18 c_fc GEMMs of 1024 -> 2304: 4.5 tiles per workgroup at 16,384 rows 5.51 -> 5.46 ms,
+// 18 tiles at 65,536 rows 18.45 -> 18.01 ms; 2.25 tiles at 8,192 rows 3.43 -> 3.49 ms).
+// Below it, the rows are quantized into the workspace first.
+NXG_HD bool relu2_fuses_quant(const gemm_plan & pl) {
+    return pl.kind == GEMM_RELU2_RT && (long long) pl.G >= (long long) NXG_RELU2_FQ_MIN_TILES_PER_WG * pl.grid;
 }
 
 } // namespace nxg_gemm

@@ -144,42 +144,28 @@ struct src_rms {
     }
 };
 
-// quantize_row of one (16-row group g, 256-input block B) by a workgroup of 4 waves.
-// Wave w quantizes rows 4w..4w+3; the 16 lanes of a row read its 256 inputs as 4
-// contiguous 256-byte pieces, so lane c holds inputs 64i + 4c + e (i, e = 0..3). The
-// int8 results are gathered in LDS in fragment order and each wave stores one 1 KiB
-// fragment. Ends with the stage buffer still being read by the stores: callers looping
-// over blocks sync before reuse.
-template <int ACT_MAX, typename Src>
-__device__ __forceinline__ void quantize_block(const Src & src, int T, int n_in, int KS, int n_blk,
-                                               int8_t * __restrict__ q, float * __restrict__ sx, int g, int B,
-                                               int * stage) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rl = wave * 4 + (lane >> 4);     // row within the 16-row group
-    const int t = g * 16 + rl;
-    const int c = lane & 15;
-    const int kb = B * BLK;                    // first input of the block
-
-    float xv[4][4];                            // [i][e]: input kb + 64i + 4c + e
-    bool present[4];
-    const auto rs = src.row(min(t, T - 1));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        present[i] = t < T && kb + 64 * i + 4 * c < n_in;
-        if (present[i]) {
-            src.load(rs, t, kb + 64 * i + 4 * c, xv[i]);
-        } else {
-            xv[i][0] = xv[i][1] = xv[i][2] = xv[i][3] = 0.0f;
-        }
-    }
+// quantize_row (src/nexterabert.cpp:378-403) of one row's 256-input block on a 16-lane group,
+// lane c = lane % 16 holding inputs 64i + 4c + e (i, e = 0..3) in xv[i][e] (0 where
+// !present[i]; a padding row, row_ok false, is all 0). Returns the block's amax; packed[i]
+// gets input 64i + 4c + e at byte e: the reference's u8 minus ACT_OFF, as a signed byte (0
+// where !present[i]). amax reproduces MAXPS: a plain maximum when the wave holds no NaN,
+// otherwise the ordered fold (nan, tail) over the 8 AVX lanes and the reference's horizontal
+// tree. The conversion is CVTPS2DQ (RNE; NaN or out of int32 range -> 0x80000000), + ACT_OFF
+// with 32-bit wrap, then the two saturating packs (quant1); when the wave holds no NaN and
+// every amax and inv = ACT_MAX / amax of it is finite, |x * inv| <= ACT_MAX + 1/2 and that
+// reduces to rint(x * inv) + ACT_OFF packed by v_cvt_pk_u8_f32, which this path uses.
+template <int ACT_MAX>
+__device__ __forceinline__ float quantize_group16(const float (&xv)[4][4], const bool (&present)[4], bool row_ok,
+                                                  int c, int (&packed)[4]) {
     bool any_nan = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) any_nan |= __builtin_isnan(xv[i][e]);
+    const bool wave_nan = __any(any_nan);
 
     float amax;
-    if (!__any(any_nan)) {
+    if (!wave_nan) {
         // No NaN in this wave: the fold is the plain maximum.
         float m = 0.0f;
 #pragma unroll
@@ -190,7 +176,7 @@ __device__ __forceinline__ void quantize_block(const Src & src, int T, int n_in,
         for (int sft = 1; sft < 16; sft <<= 1) m = fmaxf(m, __shfl_xor(m, sft));
         amax = m;
     } else {
-        // Exact MAXPS semantics. Input kb + k is AVX lane k % 8 at position k / 8; for
+        // Exact MAXPS semantics. Input k of the block is AVX lane k % 8 at position k / 8; for
         // this lane k = 64i + 4c + e: AVX lane 4(c%2) + e, position 8i + c/2. Fold the
         // 8 lanes of one parity for each i (ordered by c/2), then the four i in order.
         fold acc[4];
@@ -226,23 +212,68 @@ __device__ __forceinline__ void quantize_block(const Src & src, int T, int n_in,
             m[e] = (c & 1) ? maxps1(other, acc[e].tail) : maxps1(acc[e].tail, other);
         }
         amax = maxps1(maxps1(m[0], m[2]), maxps1(m[1], m[3]));
-        if (t >= T) amax = 0.0f;
+        if (!row_ok) amax = 0.0f;
     }
 
-    const float scale = amax / (float) ACT_MAX;
     const float inv = amax > 0.0f ? (float) ACT_MAX / amax : 0.0f;
-
-    // Quantize and place in LDS: input kb + 64i + 4c + e goes to fragment i, lane
-    // rl + 16 (c/4), byte 4 (c%4) + e. Padding (absent inputs, rows >= T) is 0.
+    const bool fast = __builtin_amdgcn_ballot_w64(wave_nan || !(amax < INFINITY) || !(inv < INFINITY)) == 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        int packed = 0;
+        int v = 0;
         if (present[i]) {
-            packed = (quant1<ACT_MAX>(xv[i][0], inv) & 0xff) | ((quant1<ACT_MAX>(xv[i][1], inv) & 0xff) << 8)
-                   | ((quant1<ACT_MAX>(xv[i][2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(xv[i][3], inv) & 0xff) << 24);
+            if (fast) {
+                unsigned u = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_rintf(xv[i][0] * inv) + (float) (ACT_MAX + 1), 0, 0u);
+                u = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_rintf(xv[i][1] * inv) + (float) (ACT_MAX + 1), 1, u);
+                u = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_rintf(xv[i][2] * inv) + (float) (ACT_MAX + 1), 2, u);
+                u = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_rintf(xv[i][3] * inv) + (float) (ACT_MAX + 1), 3, u);
+                // u8 - ACT_OFF per byte: ACT_OFF = ACT_MAX + 1 is 128 or 64
+                v = ACT_MAX == 127 ? (int) (u ^ 0x80808080u) : (int) (((u | 0x80808080u) - 0x40404040u) ^ 0x80808080u);
+            } else {
+                v = (quant1<ACT_MAX>(xv[i][0], inv) & 0xff) | ((quant1<ACT_MAX>(xv[i][1], inv) & 0xff) << 8)
+                  | ((quant1<ACT_MAX>(xv[i][2], inv) & 0xff) << 16) | ((quant1<ACT_MAX>(xv[i][3], inv) & 0xff) << 24);
+            }
         }
-        stage[(i * FRAG + (rl + 16 * (c >> 2)) * 16) / 4 + (c & 3)] = packed;
+        packed[i] = v;
     }
+    return amax;
+}
+
+// quantize_row of one (16-row group g, 256-input block B) by a workgroup of 4 waves.
+// Wave w quantizes rows 4w..4w+3; the 16 lanes of a row read its 256 inputs as 4
+// contiguous 256-byte pieces, so lane c holds inputs 64i + 4c + e (i, e = 0..3). The
+// int8 results are gathered in LDS in fragment order and each wave stores one 1 KiB
+// fragment. Ends with the stage buffer still being read by the stores: callers looping
+// over blocks sync before reuse.
+template <int ACT_MAX, typename Src>
+__device__ __forceinline__ void quantize_block(const Src & src, int T, int n_in, int KS, int n_blk,
+                                               int8_t * __restrict__ q, float * __restrict__ sx, int g, int B,
+                                               int * stage) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rl = wave * 4 + (lane >> 4);     // row within the 16-row group
+    const int t = g * 16 + rl;
+    const int c = lane & 15;
+    const int kb = B * BLK;                    // first input of the block
+
+    float xv[4][4];                            // [i][e]: input kb + 64i + 4c + e
+    bool present[4];
+    const auto rs = src.row(min(t, T - 1));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        present[i] = t < T && kb + 64 * i + 4 * c < n_in;
+        if (present[i]) {
+            src.load(rs, t, kb + 64 * i + 4 * c, xv[i]);
+        } else {
+            xv[i][0] = xv[i][1] = xv[i][2] = xv[i][3] = 0.0f;
+        }
+    }
+    int packed[4];
+    const float amax = quantize_group16<ACT_MAX>(xv, present, t < T, c, packed);
+    const float scale = amax / (float) ACT_MAX;
+
+    // Place in LDS: input kb + 64i + 4c + e goes to fragment i, lane rl + 16 (c/4), byte
+    // 4 (c%4) + e. Padding (absent inputs, rows >= T) is 0.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) stage[(i * FRAG + (rl + 16 * (c >> 2)) * 16) / 4 + (c & 3)] = packed[i];
     if (c == 0) {
         sx[((size_t) (t >> 2) * n_blk + B) * 4 + (t & 3)] = t < T ? scale : 0.0f;
     }
@@ -1774,6 +1805,8 @@ struct gemm_params {
     int8_t *       qo;    // MF x KSo fragments
     float *        sxo;   // [MP/4][n_nt][4]
     int KSo;              // ceil(N / 64)
+    // fp32 input rows [T][n_in] quantized inside the relu^2 row-tile kernel (instead of a, sx)
+    const float *  xf;
     // split output (0: none): columns [seg_end[k-1], seg_end[k]) go to seg_out[k], a dense
     // [T][seg_end[k] - seg_end[k-1]] array; every boundary is a multiple of 64
     int n_seg;
@@ -2958,7 +2991,11 @@ __global__ __launch_bounds__(WTHREADS, 1) void gemm_relu2_q8(gemm_params p) {
 // tile; the next tile's first weight k-steps are loaded before this tile's stores, so that
 // their waits do not wait for the stores. A new row tile is loaded after that barrier,
 // under the tile's quantization and stores, and published by a second barrier.
-template <int ACT_MAX, int NB>
+// With FQ the input is fp32 rows (p.xf): each row tile is quantized into LDS as quantize_row
+// does it (quantize_group16: the same int8 values and scales as nxg_quantize_rows), its row
+// scales kept in LDS for the tile's column tiles, so the activations never go to memory as
+// int8; a new row tile is quantized after the previous tile's stores.
+template <int ACT_MAX, int NB, bool FQ>
 __global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
     constexpr int KS = 4 * NB;                       // k-steps of a tile (p.KS)
     constexpr int D = RDEPTH;
@@ -2966,6 +3003,7 @@ __global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
     __shared__ __attribute__((aligned(1024))) int8_t arow[KS * (RM / 16) * FRAG];   // [ks][row group] fragments
     __shared__ __attribute__((aligned(16))) float scl[2][RSCALE / 4];             // two tiles' scales
     __shared__ __attribute__((aligned(16))) float am[2][RM * 4];                  // row maxima [row][wave]
+    __shared__ __attribute__((aligned(16))) float sxr[FQ ? RM * NB : 4];         // FQ: the row tile's sx [row/4][B][row%4]
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -2983,6 +3021,49 @@ __global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
         for (int ks = 0; ks < KS; ++ks)
             dma16s(uniform_ptr(src + (size_t) ks * FRAG), lane16, arow_lds + (uint32_t) ((ks * 4 + wave) * FRAG));
     };
+    // FQ: row tile mt quantized into LDS. Wave w takes row group w (rows 16w .. 16w + 15 of
+    // the tile) in 4 NB stages of (4 rows, one block): lane row 4 (s / NB) + lane / 16, c =
+    // lane % 16 reading inputs 256 B + 64i + 4c .. + 3 of block B = s % NB; four stages of
+    // loads in flight. Input 256B + 64i + 4c + e goes to k-step 4B + i, fragment lane
+    // (row % 16) + 16 (c / 4), byte 4 (c % 4) + e. Rows past T are zeros with scale 0.
+    const float * const xf = p.xf;
+    const int T = p.T;
+    auto quantize_rows = [&](int mt) __attribute__((always_inline)) {
+        constexpr int NS = 4 * NB, DQ = 4;
+        const int ln = lane_here();
+        const int c = ln & 15, rl = ln >> 4;
+        float xs[DQ][4][4];                          // stage s in xs[s % DQ]: [i][e]
+        auto load_stage = [&](int st, float (&d)[4][4]) {
+            const float * xr = xf + (size_t) rt_x_row(mt, wave * 16 + 4 * (st / NB) + rl, T) * (size_t) (256 * NB)
+                             + 256 * (st % NB) + 4 * c;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(xr + 64 * i));
+                d[i][0] = v.x; d[i][1] = v.y; d[i][2] = v.z; d[i][3] = v.w;
+            }
+        };
+#pragma unroll
+        for (int st = 0; st < DQ && st < NS; ++st) load_stage(st, xs[st]);
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            const int B = st % NB;
+            const int r = wave * 16 + 4 * (st / NB) + rl;    // row within the tile
+            const bool row_ok = mt * RM + r < T;
+            const bool present[4] = { row_ok, row_ok, row_ok, row_ok };
+            float x4[4][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x4[i][e] = row_ok ? xs[st % DQ][i][e] : 0.0f;
+            if (st + DQ < NS) load_stage(st + DQ, xs[st % DQ]);
+            int packed[4];
+            const float amax = quantize_group16<ACT_MAX>(x4, present, row_ok, c, packed);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<int *>(arow + ((4 * B + i) * 4 + wave) * FRAG + ((r & 15) + 16 * (c >> 2)) * 16 + 4 * (c & 3)) = packed[i];
+            if (c == 0) sxr[((r >> 2) * NB + B) * 4 + (r & 3)] = row_ok ? amax / (float) ACT_MAX : 0.0f;
+        }
+    };
     // A tile's scales into buffer b: wave w < NB the sw of block w (1 KiB: lane l columns
     // 4l..4l+3); wave 0 lanes l < 16 NB the sx of row group l / NB, block l % NB.
     // Scalar bases and 32-bit lane offsets (computed here, not kept across the tile loop).
@@ -2994,7 +3075,7 @@ __global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
             const int8_t * sw_row = uniform_ptr(reinterpret_cast<const int8_t *>(p.sw + sw_index(wave, p.NP, nt * WBN)));
             dma16s(sw_row, (uint32_t) ln * 16, base + RSX_BYTES + wave * (WBN * 4));
         }
-        if (wave == 0 && ln < 16 * NB) {
+        if (!FQ && wave == 0 && ln < 16 * NB) {
             dma16s(uniform_ptr(reinterpret_cast<const int8_t *>(p.sx)),
                    (uint32_t) (sx_group_index_rt(mt, ln / NB, p.MF, NB, ln % NB) * sizeof(float)), base);
         }
@@ -3038,7 +3119,8 @@ __global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
 
     int tile = span.first;
     int mt = tile / p.n_nt, nt = tile - mt * p.n_nt;
-    load_rows(mt);
+    if (FQ) quantize_rows(mt);
+    else    load_rows(mt);
     load_scales(tile, 0);
     wait_vm<0>();
     lds_barrier();
@@ -3077,7 +3159,7 @@ __global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi) {
                 const int r = mi * 16 + (ln & 15);
-                sxv[mi] = sc[((r >> 2) * NB + B) * 4 + (r & 3)];
+                sxv[mi] = FQ ? sxr[((r >> 2) * NB + B) * 4 + (r & 3)] : sc[((r >> 2) * NB + B) * 4 + (r & 3)];
             }
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni) {
@@ -3134,7 +3216,7 @@ __global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
             ++tile;
             mt = tile / p.n_nt;
             nt = tile - mt * p.n_nt;
-            if (reload) load_rows(mt);
+            if (reload && !FQ) load_rows(mt);
         }
 
         // Lane l takes row l of the tile: the row's maximum over the 4 waves, its scale
@@ -3220,6 +3302,7 @@ __global__ __launch_bounds__(RTHREADS, 2) void gemm_relu2_rt(gemm_params p) {
         if (reload) {
             // the new row tile (and the weight loads and stores before it) landed, then
             // published to every wave
+            if (FQ) quantize_rows(mt);
             wait_vm<0>();
             lds_barrier();
         }
@@ -3930,6 +4013,7 @@ struct gemm_out {
     int           n_seg = 0;                 // split output: column counts and buffers
     const int32_t * seg_cols = nullptr;
     float * const * seg_out = nullptr;
+    const float * xf = nullptr;              // relu^2 output only: fp32 input rows quantized in the GEMM
 };
 
 static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float * sx, int32_t T,
@@ -3959,10 +4043,11 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
             end += o.seg_cols[k];
         }
         if (end != W->n_out) return fail(NXG_EINVAL, "linear_split: segments cover %d columns, the weight has %d", end, W->n_out);
-    } else if (!q || (!o.sums && !sx) || (!o.sums && !o.qo && !o.out) || (o.qo && !o.sxo)) {
+    } else if ((!o.xf && (!q || (!o.sums && !sx))) || (!o.sums && !o.qo && !o.out) || (o.qo && !o.sxo)) {
         return fail(NXG_EINVAL, "linear: null buffer");
     }
-    if (!q || (!o.sums && !sx)) return fail(NXG_EINVAL, "linear: null buffer");
+    if (!o.xf && (!q || (!o.sums && !sx))) return fail(NXG_EINVAL, "linear: null buffer");
+    if (o.xf && (!o.qo || !aligned16(o.xf))) return fail(NXG_EINVAL, "linear_f32: fp32 rows need the relu^2 output and 16-byte alignment");
     if (o.qo) {
         if (!k256 || W->n_out % 32 != 0) {
             return fail(NXG_EINVAL, "linear_relu2_q8: needs n_in %% 256 == 0 and n_out %% 32 == 0 (n_in=%d n_out=%d)",
@@ -3996,6 +4081,7 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     p.n_mt = pl.n_mt;
     p.n_nt = pl.n_nt;
     p.G = pl.G;
+    p.xf = o.xf;
     p.n_seg = o.n_seg;
     for (int k = 0, end = 0; k < 4; ++k) {
         if (k < o.n_seg) end += o.seg_cols[k];
@@ -4006,6 +4092,7 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
     hipStream_t s = (hipStream_t) stream;
     const dim3 grid((unsigned) pl.grid), block((unsigned) pl.block);
     const bool res = o.residual != nullptr;
+    if (o.xf && pl.kind != GEMM_RELU2_RT) return fail(NXG_EINVAL, "linear_f32: no fused kernel for this shape");
     switch (pl.kind) {
     case GEMM_RELU2_SMALL:
         if (o.act_max == 127) gemm_relu2_small<127><<<grid, block, 0, s>>>(p);
@@ -4017,12 +4104,20 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
         return launch_check("gemm_relu2_q8");
     case GEMM_RELU2_RT:
         if ((p.n_blk != 1 && p.n_blk != RNB_MAX) || p.KS != 4 * p.n_blk) return fail(NXG_EINVAL, "linear_relu2_q8: plan/shape mismatch");
-        if (o.act_max == 127) {
-            if (p.n_blk == 1) gemm_relu2_rt<127, 1><<<grid, block, 0, s>>>(p);
-            else              gemm_relu2_rt<127, 4><<<grid, block, 0, s>>>(p);
+        if (o.xf) {
+            if (o.act_max == 127) {
+                if (p.n_blk == 1) gemm_relu2_rt<127, 1, true><<<grid, block, 0, s>>>(p);
+                else              gemm_relu2_rt<127, 4, true><<<grid, block, 0, s>>>(p);
+            } else {
+                if (p.n_blk == 1) gemm_relu2_rt<63, 1, true><<<grid, block, 0, s>>>(p);
+                else              gemm_relu2_rt<63, 4, true><<<grid, block, 0, s>>>(p);
+            }
+        } else if (o.act_max == 127) {
+            if (p.n_blk == 1) gemm_relu2_rt<127, 1, false><<<grid, block, 0, s>>>(p);
+            else              gemm_relu2_rt<127, 4, false><<<grid, block, 0, s>>>(p);
         } else {
-            if (p.n_blk == 1) gemm_relu2_rt<63, 1><<<grid, block, 0, s>>>(p);
-            else              gemm_relu2_rt<63, 4><<<grid, block, 0, s>>>(p);
+            if (p.n_blk == 1) gemm_relu2_rt<63, 1, false><<<grid, block, 0, s>>>(p);
+            else              gemm_relu2_rt<63, 4, false><<<grid, block, 0, s>>>(p);
         }
         return launch_check("gemm_relu2_rt");
     case GEMM_SMALL:
@@ -4111,6 +4206,43 @@ int32_t nxg_linear_i8_relu2_q8_rows(const nxg_weight * W, const int8_t * q, cons
     return launch_gemm(W, q, sx, T, o, stream);
 }
 
+int32_t nxg_linear_f32_relu2_q8_rows(const nxg_weight * W, const float * x, int32_t T, int32_t act_max,
+                                     int8_t * q_ws, float * sx_ws, int8_t * q_out, float * sx_out, void * stream) {
+    if (!W) return fail(NXG_EINVAL, "linear_f32_relu2_q8: null weight");
+    if (T < 0) return fail(NXG_EINVAL, "linear_f32_relu2_q8: T=%d", T);
+    if (T == 0) return NXG_OK;
+    if (!x || !q_out || !sx_out || !q_ws || !sx_ws) return fail(NXG_EINVAL, "linear_f32_relu2_q8: null buffer");
+    if (W->n_in % 256 != 0 || W->n_out % 32 != 0) {
+        return fail(NXG_EINVAL, "linear_f32_relu2_q8: needs n_in %% 256 == 0 and n_out %% 32 == 0 (n_in=%d n_out=%d)",
+                    W->n_in, W->n_out);
+    }
+    if (act_max != 127 && act_max != 63) return fail(NXG_EINVAL, "linear_f32_relu2_q8: act_max must be 127 or 63, got %d", act_max);
+    int rc = check_device();
+    if (rc) return rc;
+    gemm_plan pl;
+    if (!plan_gemm(T, W->n_in, W->n_out, false, true, device_cus(), pl)) return fail(NXG_EINVAL, "linear: T=%d too large", T);
+    if (relu2_fuses_quant(pl)) {
+        gemm_out o;
+        o.qo = q_out;
+        o.sxo = sx_out;
+        o.act_max = act_max;
+        o.xf = x;
+        return launch_gemm(W, nullptr, nullptr, T, o, stream);
+    }
+    // quantize_row into the workspace, then the GEMM: shapes without the row-tile kernel,
+    // or too few row tiles per workgroup to hide reading the fp32 rows
+    rc = nxg_quantize_rows(x, T, W->n_in, act_max, q_ws, sx_ws, stream);
+    return rc ? rc : nxg_linear_i8_relu2_q8_rows(W, q_ws, sx_ws, T, act_max, q_out, sx_out, stream);
+}
+
+int32_t nxg_linear_f32_relu2_q8(const nxg_weight * W, const float * x, const int32_t * cu_offsets, int32_t n_seqs,
+                                int32_t act_max, int8_t * q_ws, float * sx_ws, int8_t * q_out, float * sx_out,
+                                void * stream) {
+    int32_t T = 0;
+    const int32_t rc = packed_rows(cu_offsets, n_seqs, T);
+    return rc ? rc : nxg_linear_f32_relu2_q8_rows(W, x, T, act_max, q_ws, sx_ws, q_out, sx_out, stream);
+}
+
 int32_t nxg_linear_i8_relu2_q8(const nxg_weight * W, const int8_t * q, const float * sx,
                                const int32_t * cu_offsets, int32_t n_seqs, int32_t act_max,
                                int8_t * q_out, float * sx_out, void * stream) {
@@ -4121,7 +4253,9 @@ int32_t nxg_linear_i8_relu2_q8(const nxg_weight * W, const int8_t * q, const flo
 
 const char * nxg_gemm_kernel_name(int32_t T, int32_t n_in, int32_t n_out, int32_t flags, int32_t cus) {
     const bool res = flags & NXG_GEMM_RESIDUAL, relu2 = flags & NXG_GEMM_RELU2, sums = flags & NXG_GEMM_SUMS;
+    const bool f32_in = flags & NXG_GEMM_F32_IN;
     if (T <= 0 || n_in <= 0 || n_in % 32 != 0 || n_out <= 0 || (relu2 && (res || sums)) || (res && sums)) return nullptr;
+    if (f32_in && !relu2) return nullptr;
     if (relu2 && (n_in % 256 != 0 || n_out % 32 != 0)) return nullptr;
     if (cus <= 0) {
         if (check_device() != NXG_OK) return nullptr;
@@ -4133,9 +4267,14 @@ const char * nxg_gemm_kernel_name(int32_t T, int32_t n_in, int32_t n_out, int32_
     switch (pl.kind) {
     case GEMM_RELU2_SMALL: return a63 ? "gemm_relu2_small<63>" : "gemm_relu2_small<127>";
     case GEMM_RELU2_Q8:    return a63 ? "gemm_relu2_q8<63>" : "gemm_relu2_q8<127>";
-    case GEMM_RELU2_RT:
-        if (pl.n_blk == 1) return a63 ? "gemm_relu2_rt<63, 1>" : "gemm_relu2_rt<127, 1>";
-        return a63 ? "gemm_relu2_rt<63, 4>" : "gemm_relu2_rt<127, 4>";
+    case GEMM_RELU2_RT: {
+        static const char * const names[2][2][2] = {       // [f32 input][n_blk == 4][act_max 63]
+            { { "gemm_relu2_rt<127, 1, false>", "gemm_relu2_rt<63, 1, false>" },
+              { "gemm_relu2_rt<127, 4, false>", "gemm_relu2_rt<63, 4, false>" } },
+            { { "gemm_relu2_rt<127, 1, true>", "gemm_relu2_rt<63, 1, true>" },
+              { "gemm_relu2_rt<127, 4, true>", "gemm_relu2_rt<63, 4, true>" } } };
+        return names[f32_in && relu2_fuses_quant(pl)][pl.n_blk != 1][a63];
+    }
     case GEMM_SMALL: {
         static const char * const names[2][2][2] = {
             { { "gemm_small<2, false, false>", "gemm_small<2, false, true>" },

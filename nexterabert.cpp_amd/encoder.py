@@ -35,6 +35,14 @@ def gemm_bytes(rows: int, n_in: int, n_out: int, relu2: bool, residual: bool) ->
     return b + 4 * rows * n_out * (2 if residual else 1)
 
 
+def gemm_f32_relu2_bytes(rows: int, n_in: int, n_out: int) -> int:
+    """Algorithmic HBM bytes of the relu^2 GEMM that quantizes its fp32 input rows itself:
+    the fp32 rows, int8 weights and their scales, the next linear's int8 activations and
+    scales."""
+    nb, nb_out = (n_in + 255) // 256, (n_out + 255) // 256
+    return 4 * rows * n_in + n_out * n_in + 4 * n_out * nb + rows * n_out + 4 * rows * nb_out
+
+
 def quantize_bytes(rows: int, n_in: int) -> int:
     """Algorithmic HBM bytes of one quantize_row pass: fp32 in, int8 and the scales out."""
     return 5 * rows * n_in + 4 * rows * ((n_in + 255) // 256)
@@ -47,6 +55,9 @@ class EncoderLinearPath:
     fuse      run linears that share an input as one GEMM
     fuse_mlp  c_fc -> relu^2 -> int8 in one kernel (else fp32 rows, then
               quantize_rows_relu2)
+    fuse_quant  c_fc reads its fp32 input rows and quantizes them itself
+              (linear_f32_relu2_q8: quantize_row inside the GEMM, for the shapes where the
+              library's row-tile kernel does so) instead of a quantize_rows launch before it
     weights   device weights from an earlier path (same fuse setting), reused
     gguf      an open nxg.GGUF holding the encoder's int8 tensors (else random weights)
     kinds     the block kind of each layer to run (default: the 18 blocks of the model);
@@ -57,7 +68,7 @@ class EncoderLinearPath:
 
     def __init__(self, nxg, lengths: Sequence[int], fuse: bool = True, weights=None, seed: int = 0,
                  fuse_mlp: bool = True, gguf=None, kinds: Optional[Sequence[str]] = None,
-                 preset: str = "Q8_0"):
+                 preset: str = "Q8_0", fuse_quant: bool = True):
         import torch
         lengths = [int(n) for n in lengths]
         if not lengths or min(lengths) <= 0:
@@ -83,6 +94,8 @@ class EncoderLinearPath:
         self.gemm_bytes = 0       # algorithmic HBM bytes of the fp32-output GEMMs
         self.relu2_bytes = 0      # ... of the c_fc -> relu^2 -> int8 GEMMs
         self.quant_bytes = 0      # ... of the standalone quantizations
+        self.relu2_f32_bytes = 0  # ... of the relu^2 GEMMs quantizing their fp32 input rows
+        self.fuse_quant = fuse_quant and fuse_mlp
         M = self.M
         self.preset = preset
         for l, kind in enumerate(model.BLOCK_TYPES if kinds is None else kinds):
@@ -120,10 +133,17 @@ class EncoderLinearPath:
                 first = key not in seen and key not in made
                 seen.add(key)
                 res = g.residual
+                if (gkind == "relu2" and first and self.fuse_quant
+                        and nxg.gemm_kernel_name(rows, g.n_in, g.n_out, relu2=True,
+                                                 f32_in=True).endswith("true>")):
+                    gkind = "relu2_f32"
                 steps.append((key, first, wname, okey, res, g, gkind))
                 ops = 2 * rows * g.n_in * g.n_out
                 self.ops += ops
-                if gkind == "relu2":
+                if gkind == "relu2_f32":
+                    self.ops_relu2 += ops
+                    self.relu2_f32_bytes += gemm_f32_relu2_bytes(rows, g.n_in, g.n_out)
+                elif gkind == "relu2":
                     self.ops_relu2 += ops
                     self.relu2_bytes += gemm_bytes(rows, g.n_in, g.n_out, relu2=True, residual=False)
                 else:
@@ -131,12 +151,14 @@ class EncoderLinearPath:
                     self.gemm_bytes += gemm_bytes(rows, g.n_in, g.n_out, relu2=False, residual=res)
                 if gkind == "relu2_unfused":      # fp32 rows, then relu^2 + quantize_row
                     self.quant_bytes += quantize_bytes(rows, g.n_out)
-                if first:
+                if first and gkind != "relu2_f32":
                     self.quant_bytes += quantize_bytes(rows, g.n_in)
             self.layers.append(steps)
         self.n_gemm = sum(len(s) for s in self.layers)
-        self.n_relu2 = sum(1 for s in self.layers for st in s if st[6] == "relu2")
-        self.n_quant = sum(1 for s in self.layers for st in s if st[1] or st[6] == "relu2_unfused")
+        self.n_relu2 = sum(1 for s in self.layers for st in s if st[6] in ("relu2", "relu2_f32"))
+        self.n_relu2_f32 = sum(1 for s in self.layers for st in s if st[6] == "relu2_f32")
+        self.n_quant = sum(1 for s in self.layers for st in s
+                           if (st[1] and st[6] != "relu2_f32") or st[6] == "relu2_unfused")
 
     @staticmethod
     def _expand(nxg, spec, rng, gguf, types, preset):
@@ -178,6 +200,12 @@ class EncoderLinearPath:
                 qa = self.qacts[key]
                 w = self.dev_weights[wname]
                 cu = self.cu_block if g.block_rows else self.cu
+                if gkind == "relu2_f32":
+                    # quantize_row inside the GEMM (or into qa first where no fused kernel runs)
+                    self._timed(gemm_events, lambda: nxg.linear_f32_relu2_q8(w, self.inputs[key], cu_offsets=cu,
+                                                                             out=self.qacts[okey], workspace=qa),
+                                g, "relu2_f32", qa.T, False)
+                    continue
                 if first:
                     self._timed(quant_events, lambda: nxg.quantize_rows(self.inputs[key], out=qa), qa.T, g.n_in, False)
                 if gkind == "relu2":

@@ -13,7 +13,8 @@
 //
 // Built by the CPU tests with g++ and called through ctypes:
 //   gemm_replay(T, n_in, n_out, mode, n_seg, seg_cols, cus, &kind, &accesses, err, err_len)
-//   mode 0 fp32 rows, 1 fp32 rows + residual, 2 per-block int32 sums, 3 relu^2 -> int8
+//   mode 0 fp32 rows, 1 fp32 rows + residual, 2 per-block int32 sums, 3 relu^2 -> int8,
+//   4 relu^2 -> int8 from fp32 input rows (nxg_linear_f32_relu2_q8_rows)
 //   returns 0 (all in bounds and covered), 1 (an access out of bounds), 2 (an output
 //   written zero or several times), 3 (no plan for the shape)
 #include <cstdarg>
@@ -28,12 +29,13 @@ using namespace nxg_gemm;
 
 namespace {
 
-enum buf_id { A, SX, W, SW, RES, OUT, SEG0, SEG1, SEG2, SEG3, SUMS, QO, SXO, N_BUF };
+enum buf_id { A, SX, W, SW, RES, OUT, SEG0, SEG1, SEG2, SEG3, SUMS, QO, SXO, XF, N_BUF };
 const char * const BUF_NAME[N_BUF] = { "a", "sx", "w", "sw", "res", "out", "seg0", "seg1", "seg2", "seg3",
-                                       "sums", "qo", "sxo" };
+                                       "sums", "qo", "sxo", "xf" };
 
 struct replay {
     gemm_plan pl{};
+    bool xf = false;                         // relu^2 row-tile kernel quantizing fp32 rows itself
     size_t bytes[N_BUF] = {};
     int n_seg = 0;
     int seg_end[4] = {};
@@ -536,6 +538,7 @@ void replay_relu2_rt(replay & r) {
     }
     const size_t frow = (size_t) KS * FRAG;
     const size_t arow = (size_t) KS * (RM / 16) * FRAG, scl = 2 * (size_t) RSCALE, am = 2 * RM * 4 * sizeof(float);
+    const size_t sxr = (size_t) RM * NB * sizeof(float);
     for (int wg = 0; wg < p.grid && !r.status; ++wg) {
         const tile_span span(wg, p.grid, p.G);
         if (span.count < 0 || (span.count > 0 && (span.first < 0 || span.first + span.count > p.G))) {
@@ -545,6 +548,25 @@ void replay_relu2_rt(replay & r) {
         if (span.count == 0) continue;
         for (int wave = 0; wave < RTHREADS / 64; ++wave) {
             auto load_rows = [&](int mt) {
+                if (r.xf) {
+                    // fp32 rows quantized into LDS: stage st = (4 rows, block st % NB), lane row
+                    // 16 wave + 4 (st / NB) + lane / 16, c = lane % 16
+                    for (int st = 0; st < 4 * NB; ++st)
+                        for (int lane = 0; lane < 64; ++lane) {
+                            const int c = lane & 15, rr = wave * 16 + 4 * (st / NB) + (lane >> 4), B = st % NB;
+                            const int t = rt_x_row(mt, rr, p.T);
+                            for (int i = 0; i < 4; ++i) {
+                                r.load(XF, ((size_t) t * 256 * NB + 256 * B + 64 * i + 4 * c) * 4, 16, wg, wave, lane,
+                                       "gemm_relu2_rt fp32 rows");
+                                r.lds((size_t) ((4 * B + i) * 4 + wave) * FRAG + (size_t) ((rr & 15) + 16 * (c >> 2)) * 16 + 4 * (c & 3),
+                                      4, arow, wg, wave, lane, "gemm_relu2_rt quantized row tile");
+                            }
+                            if (c == 0)
+                                r.lds((((size_t) (rr >> 2) * NB + B) * 4 + (rr & 3)) * 4, 4, sxr, wg, wave, lane,
+                                      "gemm_relu2_rt row scales");
+                        }
+                    return;
+                }
                 for (int ks = 0; ks < KS; ++ks)
                     for (int lane = 0; lane < 64; ++lane) {
                         r.load(A, (size_t) a_frag_rt(mt, wave, p.MF) * frow + (size_t) ks * FRAG + (size_t) lane * 16, 16,
@@ -561,7 +583,7 @@ void replay_relu2_rt(replay & r) {
                         r.lds((size_t) b * RSCALE + RSX_BYTES + (size_t) wave * WBN * 4 + (size_t) lane * 16, 16, scl, wg,
                               wave, lane, "gemm_relu2_rt sw");
                     }
-                    if (wave == 0 && lane < 16 * NB) {
+                    if (!r.xf && wave == 0 && lane < 16 * NB) {
                         r.load(SX, sx_group_index_rt(mt, lane / NB, p.MF, NB, lane % NB) * 4, 16, wg, wave, lane,
                                "gemm_relu2_rt sx");
                         r.lds((size_t) b * RSCALE + (size_t) lane * 16, 16, scl, wg, wave, lane, "gemm_relu2_rt sx");
@@ -595,8 +617,12 @@ void replay_relu2_rt(replay & r) {
                     for (int lane = 0; lane < 64; ++lane) {
                         for (int mi = 0; mi < 4; ++mi) {
                             const int rr = mi * 16 + (lane & 15);
-                            r.lds((size_t) cur * RSCALE + (((size_t) (rr >> 2) * NB + B) * 4 + (rr & 3)) * 4, 4, scl, wg, wave,
-                                  lane, "gemm_relu2_rt sx read");
+                            if (r.xf)
+                                r.lds((((size_t) (rr >> 2) * NB + B) * 4 + (rr & 3)) * 4, 4, sxr, wg, wave, lane,
+                                      "gemm_relu2_rt row scale read");
+                            else
+                                r.lds((size_t) cur * RSCALE + (((size_t) (rr >> 2) * NB + B) * 4 + (rr & 3)) * 4, 4, scl, wg,
+                                      wave, lane, "gemm_relu2_rt sx read");
                         }
                         for (int ni = 0; ni < 4; ++ni)
                             r.lds((size_t) cur * RSCALE + RSX_BYTES + ((size_t) B * WBN + wave * 64 + ni * 16 + 4 * (lane >> 4)) * 4,
@@ -654,7 +680,7 @@ extern "C" int gemm_replay(int T, int n_in, int n_out, int mode, int n_seg, cons
     r.err = err;
     r.err_len = err_len;
     if (err_len > 0) err[0] = 0;
-    const bool sums = mode == 2, relu2 = mode == 3, res = mode == 1;
+    const bool sums = mode == 2, relu2 = mode == 3 || mode == 4, res = mode == 1;
     if (T <= 0 || n_in <= 0 || n_in % 32 != 0 || n_out <= 0 || !plan_gemm(T, n_in, n_out, sums, relu2, cus, r.pl)) {
         snprintf(err, (size_t) err_len, "no plan for T=%d n_in=%d n_out=%d", T, n_in, n_out);
         return 3;
@@ -675,6 +701,12 @@ extern "C" int gemm_replay(int T, int n_in, int n_out, int mode, int n_seg, cons
     r.bytes[SUMS] = sums ? (size_t) p.n_blk * T * n_out * sizeof(int32_t) : 0;
     r.bytes[QO] = relu2 ? MP * p.KSo * 64 : 0;         // nxg_qact_q_bytes(T, n_out)
     r.bytes[SXO] = relu2 ? MP * (size_t) ceil_div(n_out, BLK) * sizeof(float) : 0;   // nxg_qact_sx_bytes(T, n_out)
+    // mode 4: the row-tile kernel of nxg_linear_f32_relu2_q8_rows reading the fp32 rows [T][n_in]
+    // itself, replayed at every shape that plans it (the library launches it only from
+    // NXG_RELU2_FQ_MIN_TILES_PER_WG tiles per workgroup); other kernels run on a qact
+    r.xf = mode == 4 && p.kind == GEMM_RELU2_RT;
+    r.bytes[XF] = r.xf ? (size_t) T * n_in * sizeof(float) : 0;
+    if (r.xf) r.bytes[A] = r.bytes[SX] = 0;
     r.n_seg = n_seg;
     for (int k = 0, end = 0; k < 4; ++k) {
         if (k < n_seg) {

@@ -97,13 +97,18 @@ def test_gemm_kernel_name(nxg):
     assert k(65536, 1024, 2048) == "gemm_k256<false>"
     assert k(65536, 2304, 1024, residual=True) == "gemm_k256<true>"
     assert k(65536, 64, 1024, residual=True) == "gemm_kernel<true, false, false>"
-    assert k(65536, 1024, 2304, relu2=True) == "gemm_relu2_rt<127, 4>"
-    assert k(65536, 1024, 2304, relu2=True, act_max=63) == "gemm_relu2_rt<63, 4>"
-    assert k(65536, 256, 512, relu2=True) == "gemm_relu2_rt<127, 1>"
+    assert k(65536, 1024, 2304, relu2=True) == "gemm_relu2_rt<127, 4, false>"
+    assert k(65536, 1024, 2304, relu2=True, act_max=63) == "gemm_relu2_rt<63, 4, false>"
+    assert k(65536, 256, 512, relu2=True) == "gemm_relu2_rt<127, 1, false>"
+    assert k(65536, 1024, 2304, relu2=True, f32_in=True) == "gemm_relu2_rt<127, 4, true>"
+    assert k(65536, 256, 512, relu2=True, act_max=63, f32_in=True) == "gemm_relu2_rt<63, 1, true>"
+    assert k(65536, 512, 2304, relu2=True, f32_in=True) == "gemm_relu2_q8<127>"      # after the quantize kernel
+    assert k(16384, 1024, 2304, relu2=True, f32_in=True) == "gemm_relu2_rt<127, 4, true>"    # 4.5 tiles per workgroup
+    assert k(8192, 1024, 2304, relu2=True, f32_in=True) == "gemm_relu2_rt<127, 4, false>"    # 2.25: quantize first
     assert k(65536, 512, 2304, relu2=True) == "gemm_relu2_q8<127>"
     assert k(65536, 2304, 1024, relu2=True, act_max=63) == "gemm_relu2_q8<63>"
     assert k(768, 1024, 2304, relu2=True) == "gemm_relu2_small<127>"     # 216 workgroups: one per CU
-    assert k(1024, 1024, 2304, relu2=True) == "gemm_relu2_rt<127, 4>"    # 288 would be: the row tiles
+    assert k(1024, 1024, 2304, relu2=True) == "gemm_relu2_rt<127, 4, false>"    # 288 would be: the row tiles
     assert k(1024, 1024, 1024) == "gemm_fsk<64, 4, false>"               # 256 tiles of 64 x 64
     assert k(1024, 2304, 1024, residual=True) == "gemm_fsk<32, 9, true>"  # 9 blocks: 64 x 32 tiles
     assert k(1024, 1024, 3072) == "gemm_k256<false>"                      # 768 tiles: more than 2 per CU
@@ -113,6 +118,7 @@ def test_gemm_kernel_name(nxg):
     assert L.nxg_gemm_kernel_name(64, 1024, 2304, nxg.GEMM_RELU2 | nxg.GEMM_RESIDUAL, 256) is None
     assert L.nxg_gemm_kernel_name(64, 96, 2304, nxg.GEMM_RELU2, 256) is None      # n_in % 256
     assert L.nxg_gemm_kernel_name(64, 48, 64, 0, 256) is None
+    assert L.nxg_gemm_kernel_name(64, 1024, 2304, nxg.GEMM_F32_IN, 256) is None     # fp32 input: relu^2 only
     assert L.nxg_gemm_kernel_name(0, 64, 64, 0, 256) is None
 
 

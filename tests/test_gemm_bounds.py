@@ -21,7 +21,7 @@ ROOT = Path(__file__).resolve().parents[1]
 CSRC = ROOT / "nexterabert.cpp_amd" / "csrc"
 SRC = ROOT / "tests" / "gemm_replay.cpp"
 
-FP32, RESIDUAL, SUMS, RELU2 = 0, 1, 2, 3
+FP32, RESIDUAL, SUMS, RELU2, RELU2_F32 = 0, 1, 2, 3, 4
 KINDS = {0: "gemm_kernel", 1: "gemm_kernel sums", 2: "gemm_k256", 3: "gemm_small", 4: "gemm_relu2_q8",
          5: "gemm_relu2_small", 6: "gemm_relu2_rt", 7: "gemm_fsk"}
 
@@ -92,6 +92,16 @@ def test_relu2_int8_in_bounds(replay, T):
     for n_in in (256, 512, 1024, 2304):
         for n_out in (32, 96, 288, 2304):
             _ok(replay, T, n_in, n_out, RELU2)
+
+
+@pytest.mark.parametrize("T", [1, 17, 1000, 8191, 8250, 32935])
+def test_relu2_fp32_rows_in_bounds(replay, T):
+    """nxg_linear_f32_relu2_q8_rows: the row-tile kernel reading and quantizing fp32 rows (n_in
+    256 and 1024) at every shape that plans it, also those where the library quantizes into the
+    workspace first for want of row tiles per workgroup; the other kernels after that quantization."""
+    for n_in in (256, 512, 1024):
+        for n_out in (32, 288, 2304):
+            _ok(replay, T, n_in, n_out, RELU2_F32)
 
 
 def test_relu2_kernel_choice(replay):
@@ -165,6 +175,8 @@ PLANTS = [
     ("sx_group_index_rt", r"imin\(mt \* \(RM / 4\) \+ g, MF \* 4 - 1\)", "(mt * (RM / 4) + g)",
      (4100, 1024, 2304, RELU2), "sx bytes"),
     ("tile_span", r"count = \(int\) \(b - a\);", "count = (int) (b - a) + 1;", (4100, 1024, 2304, RELU2), "spans tiles"),
+    # its fp32 input rows past T in a partial last row tile
+    ("rt_x_row", r"return imin\(mt \* RM \+ r, T - 1\);", "return mt * RM + r;", (8250, 1024, 2304, RELU2_F32), "xf bytes"),
     # a split boundary off by one segment: columns land in the wrong buffer
     ("out_col_of", r"if \(n_seg > 1 && n >= seg_end\[0\]\)", "if (n_seg > 1 && n > seg_end[0])",
      (4100, 1024, 2048, FP32, (1024, 512, 512)), "seg"),

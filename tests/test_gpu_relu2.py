@@ -225,6 +225,59 @@ def test_linear_relu2_q8_tiny_row_maxima(nxg, orc, torch, dev, n_in, T, n_out):
         assert torch.equal(fused.q, two.q) and torch.equal(fused.sx.view(torch.int32), two.sx.view(torch.int32))
 
 
+# (T, n_in, n_out) from fp32 rows: the row-tile kernel quantizing each row tile in LDS (n_in
+# 1024 and 256, ragged last row tiles), and shapes that quantize into the workspace first
+F32_SHAPES = [(20000, 1024, 2304),   # c_fc at 20k rows, fused (5.5 tiles per workgroup): a 32-row last row tile
+              (40000, 256, 1216),    # one block, fused: a 192-column last tile
+              (8250, 256, 1216),     # 1.3 tiles per workgroup: the rows quantized first
+              (4100, 1024, 2304),
+              (700, 1024, 2304),     # few rows: gemm_relu2_small after a quantization
+              (9000, 512, 1216)]     # 2 blocks: the 128 x 256 kernel after a quantization
+
+
+@pytest.mark.parametrize("T,n_in,n_out", F32_SHAPES)
+def test_linear_f32_relu2_q8(nxg, orc, torch, dev, T, n_in, n_out):
+    """nxg_linear_f32_relu2_q8_rows equals quantize_rows then linear_i8_relu2_q8, raw buffers
+    with padding, bit for bit, on rows that take every branch of quantize_row: NaN (alone and
+    among values), +-Inf, denormals, zero rows, maxima whose ACT_MAX / amax overflows, and
+    ordinary rows; and the oracle chain on the rows without NaN."""
+    rng = np.random.default_rng(T + n_in + 7 * n_out)
+    x = rng.standard_normal((T, n_in)).astype(np.float32)
+    special = {3: np.nan, 4: np.inf, 5: -np.inf, 6: 0.0, 7: 1e-40, 8: 3e-39, T - 1: np.nan}
+    for t, v in special.items():
+        if t in (6, 7, 8):
+            x[t] = v
+        else:
+            x[t, 17] = v
+    x[9, 200:] = np.float32(2.0 ** -126) * np.float32(0.25)       # a block of denormals after normal values
+    x[10, :] *= np.float32(2.0 ** -130)                            # amax below ACT_MAX / FLT_MAX: inv overflows
+    x[11, ::5] = np.float32(3e38)
+    W = make_weight(nxg, rng, n_in, n_out, std=0.05)
+    dw = nxg.DeviceWeight(W)
+    xd = torch.from_numpy(x).cuda()
+    for act_max in (127, 63):
+        say(f"linear_f32_relu2_q8 T={T} n_in={n_in} n_out={n_out} act_max={act_max} "
+            f"-> {nxg.gemm_kernel_name(T, n_in, n_out, relu2=True, act_max=act_max, f32_in=True)}")
+        fused = nxg.linear_f32_relu2_q8(dw, xd, act_max)
+        two = nxg.linear_i8_relu2_q8(dw, nxg.quantize_rows(xd, act_max), act_max)
+        torch.cuda.synchronize()
+        assert torch.equal(fused.q, two.q), "activation tiles (padding included) differ from quantize + GEMM"
+        assert torch.equal(fused.sx.view(torch.int32), two.sx.view(torch.int32)), "scales differ from quantize + GEMM"
+    # the oracle chain (act_max 127) on the rows without NaN or Inf
+    q_ref, sx_ref = orc.quantize_rows(x)
+    y_ref = orc.linear(W.w, W.scale, W.off, q_ref, sx_ref, simd=bool(orc.vnni_flavour()),
+                       n_threads=orc.default_threads())
+    r_ref, rsx_ref = orc.quantize_rows(orc.relu2(y_ref))
+    fused = nxg.linear_f32_relu2_q8(dw, xd, 127)
+    u8, sx = nxg.export_qact(fused)
+    u8 = u8.cpu().numpy()
+    sxm = orc.sx_matrix(sx.cpu().numpy(), T, n_out)
+    rsm = orc.sx_matrix(rsx_ref, T, n_out)
+    ok = np.isfinite(x).all(axis=1)
+    assert (u8[ok] == r_ref[ok]).all()
+    assert (bits(sxm[ok]) == bits(rsm[ok])).all()
+
+
 @pytest.mark.parametrize("n_in_fc", [1024, 96])
 def test_builder_mlp(nxg, orc, torch, dev, n_in_fc):
     """x + c_proj(relu(c_fc(h))^2): fused when n_in % 256 == 0, fp32 then quantize otherwise."""
