@@ -9,7 +9,10 @@ each distinct activation a linear reads is quantized once (the reference's
 quantize_row), then every projection runs the W8A8 GEMM with the per-block fp32
 epilogue (+ residual where the reference adds one). Projections that read the same
 activation are concatenated along N into one GEMM (exact per output column), so
-the 140 linears run as 92 GEMMs. HRA q/k/v run on M/4 block rows. Weights are
+the 140 linears run as 92 GEMMs. HRA q/k/v run on M/4 block rows. The MLP's c_fc
+reads its fp32 input rows and quantizes them itself where the library's row-tile
+kernel does so (from 4 tiles per workgroup; --no-fuse-quant: a quantize launch
+first, as for the other inputs); `quantize_first` times that variant of the step. Weights are
 N(0, 0.02), Q8_0-encoded, expanded to int8 on the host; activations N(0, 1); all
 inputs are resident in HBM before timing starts.
 
@@ -466,7 +469,8 @@ def counter_pass(args) -> int:
     nxg = __graft_entry__.load_package()
     torch.cuda.set_device(0)
     nxg.init()
-    path = LinearPath(nxg, args.rows, fuse=not args.no_fuse, fuse_mlp=not args.no_fuse_mlp)
+    path = LinearPath(nxg, args.rows, fuse=not args.no_fuse, fuse_mlp=not args.no_fuse_mlp,
+                      fuse_quant=not args.no_fuse_quant)
     for _ in range(3):
         path.step()
     torch.cuda.synchronize()
@@ -548,6 +552,8 @@ def mfma_counters(args, timeout_s: int = 240) -> dict:
         child.append("--no-fuse")
     if args.no_fuse_mlp:
         child.append("--no-fuse-mlp")
+    if args.no_fuse_quant:
+        child.append("--no-fuse-quant")
     cmd = [rocprof, "--pmc", *MFMA_COUNTERS, "--output-format", "csv", "-d", str(out), "-o", "pmc", "--", *child]
     res = {"command": "rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + " --output-format csv -d DIR -o pmc -- "
                       "python3 bench.py --counter-pass --rows " + str(args.rows)}
@@ -639,6 +645,9 @@ def main() -> int:
     ap.add_argument("--no-fuse", action="store_true", help="one GEMM per linear (140) instead of 92")
     ap.add_argument("--no-fuse-mlp", action="store_true",
                     help="c_fc writes fp32 rows, then relu^2 + quantize (instead of the int8 epilogue)")
+    ap.add_argument("--no-fuse-quant", action="store_true",
+                    help="every input quantized by its own launch (else c_fc quantizes its fp32 rows itself "
+                         "where the library's row-tile kernel does so)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=8192)
     ap.add_argument("--cpu-reps", type=int, default=3)
@@ -688,7 +697,8 @@ def main() -> int:
         del a, b
 
     t0 = time.perf_counter()
-    path = LinearPath(nxg, args.rows, fuse=not args.no_fuse, fuse_mlp=not args.no_fuse_mlp)
+    path = LinearPath(nxg, args.rows, fuse=not args.no_fuse, fuse_mlp=not args.no_fuse_mlp,
+                      fuse_quant=not args.no_fuse_quant)
     torch.cuda.synchronize()
     log(f"setup {time.perf_counter() - t0:.1f} s: M={args.rows}, {path.n_gemm} GEMMs ({path.n_relu2} with the "
         f"relu^2 -> int8 output) + {path.n_quant} quantizations per step, {path.ops / 1e12:.3f} T int8 ops")
@@ -704,7 +714,7 @@ def main() -> int:
     # One roofline per kernel; `roofline` is the GEMM kernel with the largest share of the step.
     kernels = kernel_rooflines(nxg, gemm_ev, quant_ev, args.steps)
     tr = json.loads(TRAFFIC_FILE.read_text()) if TRAFFIC_FILE.exists() else {}
-    use_traffic = args.rows == 65536 and not args.no_fuse and not args.no_fuse_mlp
+    use_traffic = args.rows == 65536 and not args.no_fuse and not args.no_fuse_mlp and not args.no_fuse_quant
     for r in kernels:
         by = (tr.get("by_kernel") or {}).get(r["kernel"])
         if use_traffic and by:
@@ -722,9 +732,24 @@ def main() -> int:
     shapes = shape_table(gemm_ev, args.steps)
     log(f"dominant kernel {roof['kernel']}: {roof['per_launch']['avg_us']} us/launch, frac {roof['frac']}")
 
+    # The same step with c_fc reading a qact written by its own quantize launch: the relu^2
+    # GEMM's roofline without the input quantization inside it.
+    qfirst = None
+    if not args.no_extra_lines and path.n_relu2_f32:
+        pq = LinearPath(nxg, args.rows, fuse=not args.no_fuse, weights=path.dev_weights,
+                        fuse_mlp=not args.no_fuse_mlp, fuse_quant=False)
+        ql = path_line(nxg, pq, args.steps, args.warmup, "the same step, every input quantized by its own launch")
+        qfirst = {k: ql[k] for k in ("workload", "ms_per_step", "int8_tops", "quantize_launches",
+                                     "gemm_ms_per_step", "quantize_ms_per_step")}
+        qfirst["roofline_relu2_q8"] = next((r for r in ql["kernels"] if r["kernel"].startswith("gemm_relu2")), None)
+        log(f"quantize first: {qfirst['ms_per_step']} ms/step, relu2 kernel frac "
+            f"{(qfirst['roofline_relu2_q8'] or {}).get('frac')}")
+        del pq
+
     m8k = None
     if not args.no_extra_lines and args.rows != 8192:
-        p8 = LinearPath(nxg, 8192, fuse=not args.no_fuse, weights=path.dev_weights, fuse_mlp=not args.no_fuse_mlp)
+        p8 = LinearPath(nxg, 8192, fuse=not args.no_fuse, weights=path.dev_weights, fuse_mlp=not args.no_fuse_mlp,
+                        fuse_quant=not args.no_fuse_quant)
         m8k = path_line(nxg, p8, max(args.steps, 20), args.warmup,
                         "all 140 encoder int8 projections, one 8192-token sequence (one GPU's share of 65,536 "
                         "rows over 8 GPUs)")
@@ -738,7 +763,8 @@ def main() -> int:
 
     enc = None
     if not args.no_encoder1024:
-        p1k = LinearPath(nxg, 1024, fuse=not args.no_fuse, weights=path.dev_weights, fuse_mlp=not args.no_fuse_mlp)
+        p1k = LinearPath(nxg, 1024, fuse=not args.no_fuse, weights=path.dev_weights, fuse_mlp=not args.no_fuse_mlp,
+                         fuse_quant=not args.no_fuse_quant)
         p1k.host_weights = path.host_weights
         ms1k = time_graph(p1k, max(args.steps, 20), args.warmup)
         enc = {"tokens_per_s": round(1024 / (ms1k * 1e-3), 1), "ms_per_step": round(ms1k, 4),
@@ -774,7 +800,8 @@ def main() -> int:
         "config": {"workload": f"all 140 encoder int8 projections, one {args.rows}-token sequence",
                    "rows": args.rows, "gemm_launches": path.n_gemm, "quantize_launches": path.n_quant,
                    "fused_shared_inputs": not args.no_fuse,
-                   "mlp_relu2_int8_epilogue": path.n_relu2 > 0, "weights": "Q8_0 expanded to int8",
+                   "mlp_relu2_int8_epilogue": path.n_relu2 > 0,
+                   "c_fc_quantizes_fp32_rows": path.n_relu2_f32, "weights": "Q8_0 expanded to int8",
                    "parallelism": "single GPU"},
         "pct_of_mfma_peak": round(100 * value / PEAK_INT8_TOPS, 2),
         "mfma_counters": counters,
@@ -788,6 +815,7 @@ def main() -> int:
         "encoder": full,
         "roofline": roof,
         "roofline_relu2_q8": roof_relu2,
+        "quantize_first": qfirst,
         "rooflines_by_kernel": kernels,
         "shapes": shapes,
         "linear_path_8192": m8k,

@@ -3676,12 +3676,20 @@ static int scratch_of_device(void ** out) {
     return NXG_OK;
 }
 
+// Workgroups of the long attention kernel resident at once on the current device (its
+// compute units x occupancy), each needing one workspace slot. Cached per thread for the
+// device it was computed on, like check_device's device check.
 static long long attention_long_slots() {
-    static long long slots = 0;
-    static bool done = false;
-    if (!done) {
-        int dev = 0, cus = 0, per_cu = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
+    static thread_local long long slots = 0;
+    static thread_local int slots_dev = -1;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void) hipGetLastError();
+        dev = -1;
+    }
+    if (dev < 0 || dev != slots_dev) {
+        int cus = 0, per_cu = 0;
+        if (dev >= 0 &&
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attention_stored_kernel, 256, 0) == hipSuccess &&
             cus > 0 && per_cu > 0) {
@@ -3690,7 +3698,7 @@ static long long attention_long_slots() {
             (void) hipGetLastError();
             slots = 256;
         }
-        done = true;
+        slots_dev = dev;
     }
     return slots;
 }
