@@ -2,7 +2,7 @@
 the library's static device array), called through the C ABI with ctypes: its outputs equal
 nxg_attention_ws's (with a workspace of its own) bit for bit on two calls in a row, the second
 with a smaller input, for documents long enough to keep their scores in the workspace and for
-short ones; the first call is also checked against the oracle. A max_keys whose one slot would
+short ones; both calls are also checked against the oracle. A max_keys whose one slot would
 not fit in the static array is refused before any device work."""
 from __future__ import annotations
 
@@ -68,8 +68,8 @@ def test_noalloc_equals_workspace_entry_point(nxg, orc, lib, torch, lengths, hal
         call_noalloc(lib, torch, qd, kd, vd, cu, sd, T, H, G, half, max_keys, y)
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int32), y_ws.view(torch.int32)), f"call {call}: differs from nxg_attention_ws"
-        if call == 0:
-            assert (bits(y.cpu().numpy()) == bits(orc.attention(q, k, v, cu_h, scale, H, G, half))).all()
+        assert (bits(y.cpu().numpy()) == bits(orc.attention(q, k, v, cu_h, scale, H, G, half))).all(), \
+            f"call {call}: differs from the oracle"
 
 
 def test_noalloc_refuses_keys_beyond_the_scratch(nxg, lib, torch):
