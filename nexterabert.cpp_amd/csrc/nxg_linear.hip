@@ -901,9 +901,10 @@ __device__ __forceinline__ void fmac_bcast4_16(float (&acc)[4], const float (&w)
 //   scores    the 8 FMA chains (a_l = q[l] k[l], then fma(q[8c+l], k[8c+l], a_l) for
 //             c = 1..7) and the HADD tree (keys of whole groups of 8) or hsum256's (the last
 //             n % 8 keys) in registers, times the scale; kept in LDS, [pair][key - the pair's
-//             first key]. One thread per (pair, key), or with PAIR2 per (2 pairs, key), so
-//             that each staged key row is read from LDS once for both pairs: twice the query
-//             registers, chosen when the scores' LDS already limits a CU to two workgroups
+//             first key]. One thread per (pair, key), or with PAIR2 chain-parallel: 8 lanes
+//             per key, each one chain of all 16 pairs (att_chain_tree), so that a staged key
+//             row is read from LDS once for the 16 pairs; 128 query registers, chosen when the
+//             scores' LDS already limits a CU to two workgroups
 //   softmax   16 threads per pair: the maximum (a NaN first score wins), exp256 / the C
 //             library's expf in place, then threads l < 8 add the keys 8i + l in order of i
 //             (the 8 lanes of softmax_exp's accumulator) and hsum256 over them, the tail keys
@@ -914,6 +915,77 @@ __device__ __forceinline__ void fmac_bcast4_16(float (&acc)[4], const float (&w)
 //             (readlane on partial tiles), so the key loop reads only v_j[d] from LDS.
 // Keys are staged ATT_KT at a time ([key][ATT_KS] floats; the padding puts the 16 rows one
 // wave reads on different banks). Pairs whose keys exceed smax get NaN, as attention_kernel.
+// One key's score for a query held in registers, before the scale (scores_d64,
+// src/nexterabert.cpp:704-731): the 8 chains a_l = q_l k_l, fma(q[8c+l], k[8c+l], a_l) for
+// c = 1..7, then the HADD tree for a key of a whole group of 8, hsum256's for a tail key.
+__device__ __forceinline__ float score_d64(const float (&qv)[64], const float * kp, bool grouped) {
+    float a[8];
+    {
+        const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
+        a[0] = qv[0] * k0.x; a[1] = qv[1] * k0.y; a[2] = qv[2] * k0.z; a[3] = qv[3] * k0.w;
+        a[4] = qv[4] * k1.x; a[5] = qv[5] * k1.y; a[6] = qv[6] * k1.z; a[7] = qv[7] * k1.w;
+    }
+#pragma unroll
+    for (int c = 1; c < 8; ++c) {
+        const v4f k0 = *reinterpret_cast<const v4f *>(kp + 8 * c);
+        const v4f k1 = *reinterpret_cast<const v4f *>(kp + 8 * c + 4);
+        a[0] = __builtin_fmaf(qv[8 * c + 0], k0.x, a[0]);
+        a[1] = __builtin_fmaf(qv[8 * c + 1], k0.y, a[1]);
+        a[2] = __builtin_fmaf(qv[8 * c + 2], k0.z, a[2]);
+        a[3] = __builtin_fmaf(qv[8 * c + 3], k0.w, a[3]);
+        a[4] = __builtin_fmaf(qv[8 * c + 4], k1.x, a[4]);
+        a[5] = __builtin_fmaf(qv[8 * c + 5], k1.y, a[5]);
+        a[6] = __builtin_fmaf(qv[8 * c + 6], k1.z, a[6]);
+        a[7] = __builtin_fmaf(qv[8 * c + 7], k1.w, a[7]);
+    }
+    return grouped ? ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))
+                   : ((a[0] + a[4]) + (a[2] + a[6])) + ((a[1] + a[5]) + (a[3] + a[7]));
+}
+
+// Chain-parallel scores: lane L of an 8-lane group computes chain L of one
+// key's dot products with all 16 pairs of the workgroup, a_L = q[L] k[L], then fma(q[8c+L],
+// k[8c+L], a_L) for c = 1..7, and the group adds the 8 chains in the tree
+// ((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7)) by three exchange steps: DPP quad_perm
+// with lane L ^ 1, quad_perm with lane L ^ 2, row_half_mirror with lane 7 - L (the other
+// half of the group). Register i of lane L holds pair i ^ att_chain_g(L): with that
+// assignment every exchange adds the same pair's partial sums from registers of one index
+// (step 1: register i + 8 of the partner to register i, i < 8; step 2: i + 4 to i, i < 4;
+// step 3: i + 2 to i, i < 2), and lane L ends with the scores of pairs att_chain_g(L) and
+// att_chain_g(L) + 1. Each addition is commutative, so the lane order inside a step does not
+// change the bits.
+__device__ __forceinline__ int att_chain_g(int L) { return ((L & 1) ? 8 : 0) ^ ((L & 2) ? 4 : 0) ^ ((L & 4) ? 14 : 0); }
+
+// The tree of the 16 pairs' chain-L values a[i] (pair i ^ att_chain_g(L)) into the two
+// scores of this lane's pairs. The s_nop gives each step's DPP reads their two wait states
+// after the VALU writes of their sources.
+__device__ __forceinline__ void att_chain_tree(const float (&a)[16], float (&s)[2]) {
+    float b[8], c[4];
+    asm("s_nop 1\n\t"
+        "v_add_f32_dpp %0, %16, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %1, %17, %9 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %2, %18, %10 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %3, %19, %11 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %4, %20, %12 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %5, %21, %13 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %6, %22, %14 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %7, %23, %15 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf"
+        : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(b[5]), "=&v"(b[6]), "=&v"(b[7])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),
+          "v"(a[8]), "v"(a[9]), "v"(a[10]), "v"(a[11]), "v"(a[12]), "v"(a[13]), "v"(a[14]), "v"(a[15]));
+    asm("s_nop 1\n\t"
+        "v_add_f32_dpp %0, %8, %4 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %1, %9, %5 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %2, %10, %6 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %3, %11, %7 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf"
+        : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3])
+        : "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(b[4]), "v"(b[5]), "v"(b[6]), "v"(b[7]));
+    asm("s_nop 1\n\t"
+        "v_add_f32_dpp %0, %4, %2 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %1, %5, %3 row_half_mirror row_mask:0xf bank_mask:0xf"
+        : "=&v"(s[0]), "=&v"(s[1])
+        : "v"(c[0]), "v"(c[1]), "v"(c[2]), "v"(c[3]));
+}
+
 constexpr int ATT_P = 16;      // (query, head) pairs per workgroup
 constexpr int ATT_KT = 32;     // keys per staged tile
 constexpr int ATT_KS = 68;     // floats per staged row
@@ -982,68 +1054,93 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
         for (int r = 0; r < 2; ++r) *reinterpret_cast<v4f *>(tile + (st_r + 16 * r) * ATT_KS + st_c) = pre[r];
     };
 
-    // scores, PAIR2: thread (pairs 2 sq and 2 sq + 1, key slot sj of each tile): both query
-    // rows in registers, so each staged key row is read from LDS once for two pairs (twice
-    // the registers: for launches whose LDS admits at most two workgroups per CU anyway)
+    // scores, PAIR2 (launches whose LDS admits at most two workgroups per CU), chain-parallel
+    // (att_chain_tree): thread (chain L, key slot js of each tile) with
+    // element 8c + L of the 16 pairs' queries in registers, so that each key's 8 values read
+    // from LDS serve 16 pairs' FMAs. Keys are staged chain-major (row j: [L][c], element
+    // 8c + L at 8L + c), the queries likewise through the tile before the first key tile.
+    // The scores of keys of whole groups of 8 come out of the tree; a pair's last n % 8 keys
+    // take hsum256's tree, one thread per (pair, key) afterwards.
     if constexpr (PAIR2) {
-        const int sq = tid >> 5, sj = tid & 31;
-        float qv[2][64];
-        int plo[2], np[2], ngp[2];
-        bool ok[2];
-        float scl[2];
+        const int L = tid & 7, js = tid >> 3, gL = att_chain_g(L);
+        {
+            const int pp = tid >> 4, m = tid & 15;
+            const int t = t0 + pp / rep, h = g * rep + pp % rep;
+            const v4f f = *reinterpret_cast<const v4f *>(p.q + (size_t) min(t, p.T - 1) * p.H * 64 + (size_t) h * 64 + 4 * m);
+            const float fe[4] = { f.x, f.y, f.z, f.w };
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int d = 4 * m + u;
+                tile[pp * ATT_KS + (d & 7) * 8 + (d >> 3)] = fe[u];
+            }
+        }
+        __syncthreads();
+        float qr[ATT_P][8];
+#pragma unroll
+        for (int i = 0; i < ATT_P; ++i) {
+            const float * src = tile + (i ^ gL) * ATT_KS + L * 8;
+            const v4f a0 = *reinterpret_cast<const v4f *>(src), a1 = *reinterpret_cast<const v4f *>(src + 4);
+            qr[i][0] = a0.x; qr[i][1] = a0.y; qr[i][2] = a0.z; qr[i][3] = a0.w;
+            qr[i][4] = a1.x; qr[i][5] = a1.y; qr[i][6] = a1.z; qr[i][7] = a1.w;
+        }
+        int lo2[2], ng2[2];
+        bool ok2[2];
+        float sc2[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int pq = 2 * sq + u, t = t0 + pq / rep, h = g * rep + pq % rep;
-            const float * qr = p.q + (size_t) min(t, p.T - 1) * p.H * 64 + (size_t) h * 64;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const v4f f = *reinterpret_cast<const v4f *>(qr + 4 * i);
-                qv[u][4 * i] = f.x; qv[u][4 * i + 1] = f.y; qv[u][4 * i + 2] = f.z; qv[u][4 * i + 3] = f.w;
-            }
-            plo[u] = lo_s[pq];
-            np[u] = hi_s[pq] - plo[u];
-            ngp[u] = np[u] & ~7;
-            ok[u] = np[u] > 0 && np[u] <= smax;
-            scl[u] = scale_s[pq];
+            const int pp = gL + u, n = hi_s[pp] - lo_s[pp];
+            lo2[u] = lo_s[pp];
+            ok2[u] = n > 0 && n <= smax;
+            ng2[u] = n & ~7;
+            sc2[u] = scale_s[pp];
         }
+        auto stage_chain = [&]() {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                float * row = tile + (st_r + 16 * r) * ATT_KS;
+                const float e[4] = { pre[r].x, pre[r].y, pre[r].z, pre[r].w };
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int d = st_c + u;
+                    row[(d & 7) * 8 + (d >> 3)] = e[u];
+                }
+            }
+        };
         if (kl < kh) fetch(kg, kl);
         for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
-            __syncthreads();                               // the previous tile has been read
-            stage();
+            __syncthreads();                               // the previous tile (or the queries) read
+            stage_chain();
             __syncthreads();
             if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
-            const int jr0 = j0 + sj - plo[0], jr1 = j0 + sj - plo[1];
-            const bool in0 = ok[0] && jr0 >= 0 && jr0 < np[0], in1 = ok[1] && jr1 >= 0 && jr1 < np[1];
-            if (!in0 && !in1) continue;
-            const float * kp = tile + sj * ATT_KS;
-            float a[2][8];
-            {
-                const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
-                const float kk[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
+            const float * kp = tile + js * ATT_KS + L * 8;
+            const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
+            const float kk[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
+            float a[ATT_P];
 #pragma unroll
-                for (int u = 0; u < 2; ++u)
+            for (int i = 0; i < ATT_P; ++i) a[i] = qr[i][0] * kk[0];
 #pragma unroll
-                    for (int l = 0; l < 8; ++l) a[u][l] = qv[u][l] * kk[l];
-            }
+            for (int c = 1; c < 8; ++c)
 #pragma unroll
-            for (int c = 1; c < 8; ++c) {
-                const v4f k0 = *reinterpret_cast<const v4f *>(kp + 8 * c);
-                const v4f k1 = *reinterpret_cast<const v4f *>(kp + 8 * c + 4);
-                const float kk[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
-#pragma unroll
-                for (int u = 0; u < 2; ++u)
-#pragma unroll
-                    for (int l = 0; l < 8; ++l) a[u][l] = __builtin_fmaf(qv[u][8 * c + l], kk[l], a[u][l]);
-            }
+                for (int i = 0; i < ATT_P; ++i) a[i] = __builtin_fmaf(qr[i][c], kk[c], a[i]);
+            float s2[2];
+            att_chain_tree(a, s2);
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const int jr = u ? jr1 : jr0;
-                if (!(u ? in1 : in0)) continue;
-                const float (&e)[8] = a[u];
-                const float tot = jr < ngp[u] ? ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]))
-                                              : ((e[0] + e[4]) + (e[2] + e[6])) + ((e[1] + e[5]) + (e[3] + e[7]));
-                S[(size_t) (2 * sq + u) * smax + jr] = tot * scl[u];
+                const int jr = j0 + js - lo2[u];
+                if (ok2[u] && jr >= 0 && jr < ng2[u]) S[(size_t) (gL + u) * smax + jr] = s2[u] * sc2[u];
             }
+        }
+        if (valid && sk < n_p - (n_p & ~7)) {
+            const int jr = (n_p & ~7) + sk;
+            float qv[64];
+            const int t = t0 + sp / rep, h = g * rep + sp % rep;
+            const float * qrow = p.q + (size_t) min(t, p.T - 1) * p.H * 64 + (size_t) h * 64;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const v4f f = *reinterpret_cast<const v4f *>(qrow + 4 * i);
+                qv[4 * i] = f.x; qv[4 * i + 1] = f.y; qv[4 * i + 2] = f.z; qv[4 * i + 3] = f.w;
+            }
+            Sp[jr] = score_d64(qv, kg + (size_t) (lo_s[sp] + jr) * 64, false) * scale_s[sp];
         }
     } else {
         // scores: thread (pair sp, key slots sk and sk + 16 of each tile)
@@ -1172,32 +1269,6 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
     }
 }
 
-// One key's score for a query held in registers, before the scale (scores_d64,
-// src/nexterabert.cpp:704-731): the 8 chains a_l = q_l k_l, fma(q[8c+l], k[8c+l], a_l) for
-// c = 1..7, then the HADD tree for a key of a whole group of 8, hsum256's for a tail key.
-__device__ __forceinline__ float score_d64(const float (&qv)[64], const float * kp, bool grouped) {
-    float a[8];
-    {
-        const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
-        a[0] = qv[0] * k0.x; a[1] = qv[1] * k0.y; a[2] = qv[2] * k0.z; a[3] = qv[3] * k0.w;
-        a[4] = qv[4] * k1.x; a[5] = qv[5] * k1.y; a[6] = qv[6] * k1.z; a[7] = qv[7] * k1.w;
-    }
-#pragma unroll
-    for (int c = 1; c < 8; ++c) {
-        const v4f k0 = *reinterpret_cast<const v4f *>(kp + 8 * c);
-        const v4f k1 = *reinterpret_cast<const v4f *>(kp + 8 * c + 4);
-        a[0] = __builtin_fmaf(qv[8 * c + 0], k0.x, a[0]);
-        a[1] = __builtin_fmaf(qv[8 * c + 1], k0.y, a[1]);
-        a[2] = __builtin_fmaf(qv[8 * c + 2], k0.z, a[2]);
-        a[3] = __builtin_fmaf(qv[8 * c + 3], k0.w, a[3]);
-        a[4] = __builtin_fmaf(qv[8 * c + 4], k1.x, a[4]);
-        a[5] = __builtin_fmaf(qv[8 * c + 5], k1.y, a[5]);
-        a[6] = __builtin_fmaf(qv[8 * c + 6], k1.z, a[6]);
-        a[7] = __builtin_fmaf(qv[8 * c + 7], k1.w, a[7]);
-    }
-    return grouped ? ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))
-                   : ((a[0] + a[4]) + (a[2] + a[6])) + ((a[1] + a[5]) + (a[3] + a[7]));
-}
 
 // attention_tile_kernel's pairs, thread mapping and per-pair order for documents whose
 // scores do not fit in LDS: nothing is kept per key; the scores are computed three times,
