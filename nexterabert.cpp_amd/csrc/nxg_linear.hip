@@ -1333,13 +1333,13 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
     const int plo = lo_s[sp], n_p = hi_s[sp] - plo, ng_p = n_p & ~7;
     const bool valid = n_p > 0 && n_p <= p.max_keys;     // more keys than max_keys: NaN, as the other kernels
     float * const scp = STORED ? sc + ((size_t) blockIdx.x * ATT_P + sp) * (size_t) p.max_keys : nullptr;
+    // this thread's pair's query (STORED: only for its tail keys, loaded there)
     float qv[64];
-    {
-        const int t = t0 + sp / rep, h = g * rep + sp % rep;
-        const float * qr = p.q + (size_t) min(t, p.T - 1) * p.H * 64 + (size_t) h * 64;
+    const float * const qrow = p.q + (size_t) min(t0 + sp / rep, p.T - 1) * p.H * 64 + (size_t) (g * rep + sp % rep) * 64;
+    if constexpr (!STORED) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const v4f f = *reinterpret_cast<const v4f *>(qr + 4 * i);
+            const v4f f = *reinterpret_cast<const v4f *>(qrow + 4 * i);
             qv[4 * i] = f.x; qv[4 * i + 1] = f.y; qv[4 * i + 2] = f.z; qv[4 * i + 3] = f.w;
         }
     }
@@ -1359,7 +1359,108 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
     };
 
     // pass 1: the maximum
-    {
+    if constexpr (STORED) {
+        // the scores chain-parallel, as attention_tile_kernel's PAIR2 path (att_chain_tree),
+        // each written to the workspace; the maxima of a pair's 32 key slots meet in E, then
+        // its 16 lanes; a pair's last n % 8 keys by hsum256's tree, one thread per key
+        const int L = tid & 7, js = tid >> 3, gL = att_chain_g(L);
+        {
+            const int pp = tid >> 4, m = tid & 15;
+            const int t = t0 + pp / rep, h = g * rep + pp % rep;
+            const v4f f = *reinterpret_cast<const v4f *>(p.q + (size_t) min(t, p.T - 1) * p.H * 64 + (size_t) h * 64 + 4 * m);
+            const float fe[4] = { f.x, f.y, f.z, f.w };
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int d = 4 * m + u;
+                tile[pp * ATT_KS + (d & 7) * 8 + (d >> 3)] = fe[u];
+            }
+        }
+        __syncthreads();
+        float qr[ATT_P][8];
+#pragma unroll
+        for (int i = 0; i < ATT_P; ++i) {
+            const float * src = tile + (i ^ gL) * ATT_KS + L * 8;
+            const v4f a0 = *reinterpret_cast<const v4f *>(src), a1 = *reinterpret_cast<const v4f *>(src + 4);
+            qr[i][0] = a0.x; qr[i][1] = a0.y; qr[i][2] = a0.z; qr[i][3] = a0.w;
+            qr[i][4] = a1.x; qr[i][5] = a1.y; qr[i][6] = a1.z; qr[i][7] = a1.w;
+        }
+        int lo2[2], ng2[2];
+        bool ok2[2];
+        float sc2[2], mx2[2];
+        float * sp2[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int pp = gL + u, n = hi_s[pp] - lo_s[pp];
+            lo2[u] = lo_s[pp];
+            ok2[u] = n > 0 && n <= p.max_keys;
+            ng2[u] = n & ~7;
+            sc2[u] = scale_s[pp];
+            mx2[u] = -__builtin_inff();
+            sp2[u] = sc + ((size_t) blockIdx.x * ATT_P + pp) * (size_t) p.max_keys;
+        }
+        auto stage_chain = [&]() {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                float * row = tile + (st_r + 16 * r) * ATT_KS;
+                const float e[4] = { pre[r].x, pre[r].y, pre[r].z, pre[r].w };
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int d = st_c + u;
+                    row[(d & 7) * 8 + (d >> 3)] = e[u];
+                }
+            }
+        };
+        if (kl < kh) fetch(kg, kl);
+        for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
+            __syncthreads();                               // the previous tile (or the queries) read
+            stage_chain();
+            __syncthreads();
+            if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
+            const float * kp = tile + js * ATT_KS + L * 8;
+            const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
+            const float kk[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
+            float a[ATT_P];
+#pragma unroll
+            for (int i = 0; i < ATT_P; ++i) a[i] = qr[i][0] * kk[0];
+#pragma unroll
+            for (int c = 1; c < 8; ++c)
+#pragma unroll
+                for (int i = 0; i < ATT_P; ++i) a[i] = __builtin_fmaf(qr[i][c], kk[c], a[i]);
+            float s2[2];
+            att_chain_tree(a, s2);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int jr = j0 + js - lo2[u];
+                if (ok2[u] && jr >= 0 && jr < ng2[u]) {
+                    const float s = s2[u] * sc2[u];
+                    mx2[u] = fmaxf(mx2[u], s);
+                    sp2[u][jr] = s;
+                    if (jr == 0) s0_s[gL + u] = s;
+                }
+            }
+        }
+        E[gL][js] = mx2[0];
+        E[gL + 1][js] = mx2[1];
+        __syncthreads();
+        float mx = fmaxf(E[sp][sk], E[sp][sk + 16]);
+        if (valid && sk < n_p - ng_p) {
+            const int jr = ng_p + sk;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const v4f f = *reinterpret_cast<const v4f *>(qrow + 4 * i);
+                qv[4 * i] = f.x; qv[4 * i + 1] = f.y; qv[4 * i + 2] = f.z; qv[4 * i + 3] = f.w;
+            }
+            const float s = score_d64(qv, kg + (size_t) (plo + jr) * 64, false) * scale;
+            mx = fmaxf(mx, s);
+            scp[jr] = s;
+            if (jr == 0) s0_s[sp] = s;
+        }
+#pragma unroll
+        for (int sft = 8; sft >= 1; sft >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sft));
+        __syncthreads();                                   // s0_s written
+        if (valid && sk == 0) m_s[sp] = __builtin_isnan(s0_s[sp]) ? s0_s[sp] : mx;
+        __syncthreads();
+    } else {
         float mx = -__builtin_inff();
         if (kl < kh) fetch(kg, kl);
         for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
