@@ -3644,13 +3644,19 @@ static int32_t launch_produce(const char * what, const Src & src, int32_t T, int
 
 // Dynamic LDS the tiled attention kernel may take on the current device: the device's
 // shared memory per workgroup less the kernel's static arrays, with the attribute that
-// allows more than the default raised to it once.
+// allows more than the default raised to it, once per thread and device (as check_device).
 static size_t attention_tile_lds_limit() {
-    static size_t limit = 0;
-    static bool done = false;
-    if (!done) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
+    static thread_local size_t limit = 0;
+    static thread_local int limit_dev = -1;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void) hipGetLastError();
+        dev = -1;
+    }
+    if (dev < 0 || dev != limit_dev) {
+        int v = 0;
+        limit = 0;
+        if (dev >= 0 &&
             hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 1024) {
             const size_t want = (size_t) v - 1024;           // static arrays of the kernel: 4 x ATT_P words
             if (hipFuncSetAttribute((const void *) attention_tile_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -3663,7 +3669,7 @@ static size_t attention_tile_lds_limit() {
                 limit = 65536 - 1024;
             }
         }
-        done = true;
+        limit_dev = dev;
     }
     return limit;
 }
