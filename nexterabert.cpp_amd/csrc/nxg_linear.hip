@@ -901,7 +901,7 @@ __device__ __forceinline__ void fmac_bcast4_16(float (&acc)[4], const float (&w)
 //   scores    the 8 FMA chains (a_l = q[l] k[l], then fma(q[8c+l], k[8c+l], a_l) for
 //             c = 1..7) and the HADD tree (keys of whole groups of 8) or hsum256's (the last
 //             n % 8 keys) in registers, times the scale; kept in LDS, [pair][key - the pair's
-//             first key]. One thread per (pair, key), or with PAIR2 chain-parallel: 8 lanes
+//             first key]. One thread per (pair, key), or with CHAIN chain-parallel: 8 lanes
 //             per key, each one chain of all 16 pairs (att_chain_tree), so that a staged key
 //             row is read from LDS once for the 16 pairs; 128 query registers, chosen when the
 //             scores' LDS already limits a CU to two workgroups
@@ -990,7 +990,7 @@ constexpr int ATT_P = 16;      // (query, head) pairs per workgroup
 constexpr int ATT_KT = 32;     // keys per staged tile
 constexpr int ATT_KS = 68;     // floats per staged row
 
-template <bool PAIR2>
+template <bool CHAIN>
 __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int smax) {
     extern __shared__ __attribute__((aligned(16))) float att_lds[];
     float * S = att_lds;                                   // [ATT_P][smax]
@@ -1054,14 +1054,14 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
         for (int r = 0; r < 2; ++r) *reinterpret_cast<v4f *>(tile + (st_r + 16 * r) * ATT_KS + st_c) = pre[r];
     };
 
-    // scores, PAIR2 (launches whose LDS admits at most two workgroups per CU), chain-parallel
+    // scores, CHAIN (launches whose LDS admits at most two workgroups per CU), chain-parallel
     // (att_chain_tree): thread (chain L, key slot js of each tile) with
     // element 8c + L of the 16 pairs' queries in registers, so that each key's 8 values read
     // from LDS serve 16 pairs' FMAs. Keys are staged chain-major (row j: [L][c], element
     // 8c + L at 8L + c), the queries likewise through the tile before the first key tile.
     // The scores of keys of whole groups of 8 come out of the tree; a pair's last n % 8 keys
     // take hsum256's tree, one thread per (pair, key) afterwards.
-    if constexpr (PAIR2) {
+    if constexpr (CHAIN) {
         const int L = tid & 7, js = tid >> 3, gL = att_chain_g(L);
         {
             const int pp = tid >> 4, m = tid & 15;
@@ -1360,7 +1360,7 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
 
     // pass 1: the maximum
     if constexpr (STORED) {
-        // the scores chain-parallel, as attention_tile_kernel's PAIR2 path (att_chain_tree),
+        // the scores chain-parallel, as attention_tile_kernel's CHAIN path (att_chain_tree),
         // each written to the workspace; the maxima of a pair's 32 key slots meet in E, then
         // its 16 lanes; a pair's last n % 8 keys by hsum256's tree, one thread per key
         const int L = tid & 7, js = tid >> 3, gL = att_chain_g(L);
@@ -3971,7 +3971,7 @@ int32_t nxg_attention_ws(const float * q, const float * k, const float * v, cons
         const long long n_tiles = (long long) n_kv_head * ((T + ATT_P / rep - 1) / (ATT_P / rep));
         const size_t lds_max = attention_tile_lds_limit();
         if (tile_lds <= lds_max) {
-            // fewer than 3 workgroups per CU by LDS (the static 1 KiB included): the two-pair scores
+            // fewer than 3 workgroups per CU by LDS (the static 1 KiB included): chain-parallel scores
             if (3 * (tile_lds + 1024) > lds_max + 1024) {
                 attention_tile_kernel<true><<<dim3((unsigned) n_tiles), dim3(256), tile_lds, (hipStream_t) stream>>>(p, smax);
             } else {
