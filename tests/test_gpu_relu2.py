@@ -278,6 +278,35 @@ def test_linear_f32_relu2_q8(nxg, orc, torch, dev, T, n_in, n_out):
     assert (bits(sxm[ok]) == bits(rsm[ok])).all()
 
 
+@pytest.mark.parametrize("lengths,n_in", [([10000, 7000, 3000], 1024), ([5, 700, 33], 1024), ([30000, 12000], 256)])
+def test_linear_f32_relu2_q8_packed(nxg, orc, torch, dev, lengths, n_in):
+    """nxg_linear_f32_relu2_q8 over a packed batch (cu_offsets) equals the rows entry point on the
+    same rows, bit for bit (fused and quantize-first sizes), and every row equals the oracle chain
+    on a sample of rows."""
+    rng = np.random.default_rng(sum(lengths) + n_in)
+    cu = nxg.cu_offsets_of(lengths)
+    T, n_out = int(cu[-1]), 2304
+    say(f"linear_f32_relu2_q8 packed {lengths} n_in={n_in} -> "
+        f"{nxg.gemm_kernel_name(T, n_in, n_out, relu2=True, f32_in=True)}")
+    x = rng.standard_normal((T, n_in)).astype(np.float32)
+    W = make_weight(nxg, rng, n_in, n_out, std=0.05)
+    dw = nxg.DeviceWeight(W)
+    xd = torch.from_numpy(x).cuda()
+    packed = nxg.linear_f32_relu2_q8(dw, xd, 127, cu_offsets=cu)
+    rows = nxg.linear_f32_relu2_q8(dw, xd, 127)
+    torch.cuda.synchronize()
+    assert torch.equal(packed.q, rows.q)
+    assert torch.equal(packed.sx.view(torch.int32), rows.sx.view(torch.int32))
+    pick = np.unique(np.concatenate([cu[:-1], cu[1:] - 1, rng.choice(T, 64, replace=False)]))
+    q_ref, sx_ref = orc.quantize_rows(x[pick])
+    y_ref = orc.linear(W.w, W.scale, W.off, q_ref, sx_ref, simd=bool(orc.vnni_flavour()),
+                       n_threads=orc.default_threads())
+    r_ref, rsx_ref = orc.quantize_rows(orc.relu2(y_ref))
+    u8, sx = nxg.export_qact(packed)
+    assert (u8.cpu().numpy()[pick] == r_ref).all()
+    assert (bits(orc.sx_matrix(sx.cpu().numpy(), T, n_out)[pick]) == bits(orc.sx_matrix(rsx_ref, len(pick), n_out))).all()
+
+
 @pytest.mark.parametrize("n_in_fc", [1024, 96])
 def test_builder_mlp(nxg, orc, torch, dev, n_in_fc):
     """x + c_proj(relu(c_fc(h))^2): fused when n_in % 256 == 0, fp32 then quantize otherwise."""
