@@ -25,6 +25,8 @@
  *     sx  float, nxg_qact_sx_bytes(T, n_in) bytes, in the reference's layout
  *           [token/4][block][token%4] (src/nexterabert.cpp:368-375), padded to 16 rows.
  *   outputs and residuals: float [T][n_out], row-major (the (n_out, T) ggml tensor).
+ *   Every device buffer above, and the fp32 rows the quantizers and producers read, must be
+ *   16-byte aligned (hipMalloc gives 256); a call given another refuses it with NXG_EINVAL.
  */
 #ifndef NXG_LINEAR_H
 #define NXG_LINEAR_H

@@ -3622,6 +3622,9 @@ struct nxg_weight {
     size_t   bytes = 0;
 };
 
+// Device buffers are read and written 16 bytes per lane (and by LDS DMA): null or 16-byte aligned.
+static bool aligned16(const void * p) { return ((uintptr_t) p & 15u) == 0; }
+
 // A producer's rows quantized for an int8 consumer: shared checks and launch.
 template <typename Src>
 static int32_t launch_produce(const char * what, const Src & src, int32_t T, int32_t n_in, int32_t act_max,
@@ -3631,6 +3634,7 @@ static int32_t launch_produce(const char * what, const Src & src, int32_t T, int
     if (act_max != 127 && act_max != 63) return fail(NXG_EINVAL, "%s: act_max must be 127 or 63, got %d", what, act_max);
     if (T == 0) return NXG_OK;
     if (!q || !sx) return fail(NXG_EINVAL, "%s: null output", what);
+    if (!aligned16(q) || !aligned16(sx)) return fail(NXG_EINVAL, "%s: q and sx must be 16-byte aligned", what);
     int rc = check_device();
     if (rc) return rc;
     const long long n_wg = (long long) (d.MP / 16) * d.n_blk;
@@ -3681,7 +3685,6 @@ static int row_lanes_log2(int C) {
     return lg;
 }
 
-static bool aligned16(const void * p) { return ((uintptr_t) p & 15u) == 0; }
 
 // A producer's rows written as fp32: shared checks and launch.
 template <typename Src>
@@ -3719,6 +3722,7 @@ static int32_t launch_quantize(const float * x, int32_t T, int32_t n_in, int32_t
     if (act_max != 127 && act_max != 63) return fail(NXG_EINVAL, "quantize: act_max must be 127 or 63, got %d", act_max);
     if (T == 0) return NXG_OK;
     if (!x || !q || !sx) return fail(NXG_EINVAL, "quantize: null buffer");
+    if (!aligned16(x) || !aligned16(q) || !aligned16(sx)) return fail(NXG_EINVAL, "quantize: x, q and sx must be 16-byte aligned");
     int rc = check_device();
     if (rc) return rc;
     const long long n_wg = (long long) (d.MP / 16) * d.n_blk;
@@ -3752,7 +3756,9 @@ int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps
     if (act_max != 127 && act_max != 63) return fail(NXG_EINVAL, "rmsnorm_quantize: act_max must be 127 or 63, got %d", act_max);
     if (T == 0) return NXG_OK;
     if (!x || !gain || !q || !sx) return fail(NXG_EINVAL, "rmsnorm_quantize: null buffer");
-    if (!aligned16(x) || !aligned16(gain)) return fail(NXG_EINVAL, "rmsnorm_quantize: x and gain must be 16-byte aligned");
+    if (!aligned16(x) || !aligned16(gain) || !aligned16(q) || !aligned16(sx)) {
+        return fail(NXG_EINVAL, "rmsnorm_quantize: x, gain, q and sx must be 16-byte aligned");
+    }
     int rc = check_device();
     if (rc) return rc;
     hipStream_t s = (hipStream_t) stream;
@@ -3791,6 +3797,7 @@ int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps
 int32_t nxg_gate_quantize_rows(const float * g, const float * y, int32_t T, int32_t n_in, int32_t act_max,
                                int8_t * q, float * sx, void * stream) {
     if (T > 0 && (!g || !y)) return fail(NXG_EINVAL, "gate_quantize: null input");
+    if (!aligned16(g) || !aligned16(y)) return fail(NXG_EINVAL, "gate_quantize: inputs must be 16-byte aligned");
     return launch_produce("gate_quantize", src_gate{g, y, n_in}, T, n_in, act_max, q, sx, stream);
 }
 
@@ -3799,6 +3806,7 @@ int32_t nxg_dwconv_quantize_rows(const float * x, const float * r, const float *
                                  int32_t act_max, int8_t * q, float * sx, void * stream) {
     if (T > 0 && (!x || !taps || !cu_offsets)) return fail(NXG_EINVAL, "dwconv_quantize: null input");
     if (k < 1 || n_seqs < 1) return fail(NXG_EINVAL, "dwconv_quantize: k=%d n_seqs=%d (both must be >= 1)", k, n_seqs);
+    if (!aligned16(x) || !aligned16(r) || !aligned16(taps)) return fail(NXG_EINVAL, "dwconv_quantize: inputs must be 16-byte aligned");
     return launch_produce("dwconv_quantize", src_dwconv{x, r, taps, cu_offsets, n_seqs, T, n_in, k},
                           T, n_in, act_max, q, sx, stream);
 }
@@ -3808,6 +3816,9 @@ int32_t nxg_lily_state_quantize_rows(const float * a, const float * x, const flo
                                      int32_t act_max, int8_t * q, float * sx, void * stream) {
     if (T > 0 && (!a || !x || !b || !taps || !cu_offsets)) return fail(NXG_EINVAL, "lily_state_quantize: null input");
     if (k < 1 || n_seqs < 1) return fail(NXG_EINVAL, "lily_state_quantize: k=%d n_seqs=%d (both must be >= 1)", k, n_seqs);
+    if (!aligned16(a) || !aligned16(x) || !aligned16(b) || !aligned16(taps)) {
+        return fail(NXG_EINVAL, "lily_state_quantize: inputs must be 16-byte aligned");
+    }
     return launch_produce("lily_state_quantize", src_lily_state{a, x, b, taps, cu_offsets, n_seqs, T, n_in, k},
                           T, n_in, act_max, q, sx, stream);
 }
@@ -3820,6 +3831,7 @@ int32_t nxg_block_mean_quantize_rows(const float * h, const float * g, const int
     if (block < 1 || n_seqs < 1 || T < 0) {
         return fail(NXG_EINVAL, "block_mean_quantize: block=%d n_seqs=%d T=%d (block, n_seqs >= 1)", block, n_seqs, T);
     }
+    if (!aligned16(h) || !aligned16(g)) return fail(NXG_EINVAL, "block_mean_quantize: inputs must be 16-byte aligned");
     return launch_produce("block_mean_quantize", src_block_mean{h, g, cu_offsets, cu_blocks, n_seqs, T, n_blocks, n_in, block},
                           n_blocks, n_in, act_max, q, sx, stream);
 }
@@ -4233,6 +4245,10 @@ static int32_t launch_gemm(const nxg_weight * W, const int8_t * q, const float *
         return fail(NXG_EINVAL, "linear: null buffer");
     }
     if (!o.xf && (!q || (!o.sums && !sx))) return fail(NXG_EINVAL, "linear: null buffer");
+    if (!aligned16(q) || !aligned16(sx) || !aligned16(o.out) || !aligned16(o.residual) || !aligned16(o.qo) ||
+        !aligned16(o.sxo) || !aligned16(o.sums)) {
+        return fail(NXG_EINVAL, "linear: device buffers must be 16-byte aligned");
+    }
     if (o.xf && (!o.qo || !aligned16(o.xf))) return fail(NXG_EINVAL, "linear_f32: fp32 rows need the relu^2 output and 16-byte alignment");
     if (o.qo) {
         if (!k256 || W->n_out % 32 != 0) {

@@ -80,6 +80,17 @@ def test_arguments_checked_before_device_work(nxg):
     # RMSNorm's vector loads: x and gain must be 16-byte aligned (no pointer is dereferenced)
     assert L.nxg_rmsnorm_quantize_rows(4, 16, ctypes.c_float(1e-6), 16, 256, 127, 16, 16, None) == nxg.NXG_EINVAL
     assert b"aligned" in L.nxg_last_error()
+    assert L.nxg_rmsnorm_quantize_rows(16, 16, ctypes.c_float(1e-6), 16, 256, 127, 20, 16, None) == nxg.NXG_EINVAL
+    assert b"aligned" in L.nxg_last_error()
+    # every quantizer and producer reads and writes 16 bytes per lane: misaligned buffers are refused
+    assert L.nxg_quantize_rows(4, 16, 256, 127, 16, 16, None) == nxg.NXG_EINVAL
+    assert b"aligned" in L.nxg_last_error()
+    assert L.nxg_quantize_rows(16, 16, 256, 127, 16, 24, None) == nxg.NXG_EINVAL
+    assert L.nxg_quantize_rows_relu2(16, 16, 256, 127, 8, 16, None) == nxg.NXG_EINVAL
+    assert L.nxg_gate_quantize_rows(16, 36, 16, 256, 127, 16, 16, None) == nxg.NXG_EINVAL
+    assert b"aligned" in L.nxg_last_error()
+    assert L.nxg_gate_quantize_rows(16, 16, 16, 256, 127, 16, 4, None) == nxg.NXG_EINVAL
+    assert b"aligned" in L.nxg_last_error()
     # attention's workspace: a size without memory, a negative size or a misaligned one is refused
     args = (None, None, None, None, 1, None, 8, 2, 1, -1, 8, None)
     assert L.nxg_attention_ws(*args, None, 64, None) == nxg.NXG_EINVAL
