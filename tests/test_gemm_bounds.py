@@ -104,6 +104,18 @@ def test_relu2_fp32_rows_in_bounds(replay, T):
             _ok(replay, T, n_in, n_out, RELU2_F32)
 
 
+def test_relu2_fp32_rows_sweep_shapes_in_bounds(replay):
+    """The seeded shapes of the GPU sweep of nxg_linear_f32_relu2_q8 (tests/test_gpu_relu2.py),
+    replayed before any GPU runs them: ragged row tiles, a last column tile past n_out."""
+    import numpy as np
+    rng = np.random.default_rng(20261202)
+    for i in range(8):
+        n_in = (256, 1024)[i % 2]
+        n_out = 32 * int(rng.integers(8, 129))
+        T = int(rng.integers(12000, 70000))
+        assert _ok(replay, T, n_in, n_out, RELU2_F32) == "gemm_relu2_rt"
+
+
 def test_relu2_kernel_choice(replay):
     """n_in 256 and 1024 on the row-tile kernel, other block counts on the 128 x 256 one."""
     assert _ok(replay, 65536, 1024, 2304, RELU2) == "gemm_relu2_rt"

@@ -278,6 +278,36 @@ def test_linear_f32_relu2_q8(nxg, orc, torch, dev, T, n_in, n_out):
     assert (bits(sxm[ok]) == bits(rsm[ok])).all()
 
 
+def _f32_sweep_shapes():
+    rng = np.random.default_rng(20261202)
+    out = []
+    for i in range(8):
+        n_in = (256, 1024)[i % 2]
+        n_out = 32 * int(rng.integers(8, 129))             # 256 .. 4,096, any multiple of 32
+        T = int(rng.integers(12000, 70000))
+        out.append((T, n_in, n_out, (127, 63)[(i // 2) % 2]))
+    return out
+
+
+@pytest.mark.parametrize("T,n_in,n_out,act_max", _f32_sweep_shapes())
+def test_linear_f32_relu2_q8_sweep(nxg, torch, dev, T, n_in, n_out, act_max):
+    """Seeded shapes (ragged row tiles, column tiles past n_out, fused or not by the workgroup
+    count): nxg_linear_f32_relu2_q8 equals quantize_rows then linear_i8_relu2_q8 bit for bit,
+    raw buffers with padding (that path is oracle-checked in the tests above)."""
+    name = nxg.gemm_kernel_name(T, n_in, n_out, relu2=True, act_max=act_max, f32_in=True)
+    say(f"linear_f32_relu2_q8 sweep T={T} n_in={n_in} n_out={n_out} act_max={act_max} -> {name}")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(T + n_out)
+    x = torch.randn(T, n_in, device="cuda", generator=g)
+    rng = np.random.default_rng(T)
+    dw = nxg.DeviceWeight(make_weight(nxg, rng, n_in, n_out, std=0.05))
+    fused = nxg.linear_f32_relu2_q8(dw, x, act_max)
+    two = nxg.linear_i8_relu2_q8(dw, nxg.quantize_rows(x, act_max), act_max)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.q, two.q)
+    assert torch.equal(fused.sx.view(torch.int32), two.sx.view(torch.int32))
+
+
 @pytest.mark.parametrize("lengths,n_in", [([10000, 7000, 3000], 1024), ([5, 700, 33], 1024), ([30000, 12000], 256)])
 def test_linear_f32_relu2_q8_packed(nxg, orc, torch, dev, lengths, n_in):
     """nxg_linear_f32_relu2_q8 over a packed batch (cu_offsets) equals the rows entry point on the
