@@ -901,10 +901,10 @@ __device__ __forceinline__ void fmac_bcast4_16(float (&acc)[4], const float (&w)
 //   scores    the 8 FMA chains (a_l = q[l] k[l], then fma(q[8c+l], k[8c+l], a_l) for
 //             c = 1..7) and the HADD tree (keys of whole groups of 8) or hsum256's (the last
 //             n % 8 keys) in registers, times the scale; kept in LDS, [pair][key - the pair's
-//             first key]. One thread per (pair, key), or with CHAIN chain-parallel: 8 lanes
-//             per key, each one chain of all 16 pairs (att_chain_tree), so that a staged key
-//             row is read from LDS once for the 16 pairs; 128 query registers, chosen when the
-//             scores' LDS already limits a CU to two workgroups
+//             first key]. Chain-parallel: 8 lanes per key, each one chain of 16 pairs
+//             (WIDE, 128 query registers, chosen when the scores' LDS already limits a CU to
+//             two workgroups) or of 8 pairs (64 registers), so that a staged key row is read
+//             from LDS once for 16 or 8 pairs (att_chain_tree)
 //   softmax   16 threads per pair: the maximum (a NaN first score wins), exp256 / the C
 //             library's expf in place, then threads l < 8 add the keys 8i + l in order of i
 //             (the 8 lanes of softmax_exp's accumulator) and hsum256 over them, the tail keys
@@ -986,11 +986,37 @@ __device__ __forceinline__ void att_chain_tree(const float (&a)[16], float (&s)[
         : "v"(c[0]), "v"(c[1]), "v"(c[2]), "v"(c[3]));
 }
 
+// The same for 8 pairs (register i: pair i ^ att_chain_g8(L)): steps of 4, 2 and 1 registers,
+// lane L ending with the score of pair att_chain_g8(L) (0..7, one per lane of the group).
+__device__ __forceinline__ int att_chain_g8(int L) { return ((L & 1) ? 4 : 0) ^ ((L & 2) ? 2 : 0) ^ ((L & 4) ? 7 : 0); }
+__device__ __forceinline__ void att_chain_tree(const float (&a)[8], float (&s)[1]) {
+    float b[4], c[2];
+    asm("s_nop 1\n\t"
+        "v_add_f32_dpp %0, %8, %4 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %1, %9, %5 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %2, %10, %6 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %3, %11, %7 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf"
+        : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]));
+    asm("s_nop 1\n\t"
+        "v_add_f32_dpp %0, %4, %2 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %1, %5, %3 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf"
+        : "=&v"(c[0]), "=&v"(c[1])
+        : "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]));
+    asm("s_nop 1\n\t"
+        "v_add_f32_dpp %0, %2, %1 row_half_mirror row_mask:0xf bank_mask:0xf"
+        : "=&v"(s[0])
+        : "v"(c[0]), "v"(c[1]));
+}
+
+#ifndef NXG_ATT_WIDE
+#define NXG_ATT_WIDE 1         // 16 pairs per lane group where LDS allows two workgroups per CU (0: always 8)
+#endif
 constexpr int ATT_P = 16;      // (query, head) pairs per workgroup
 constexpr int ATT_KT = 32;     // keys per staged tile
 constexpr int ATT_KS = 68;     // floats per staged row
 
-template <bool CHAIN>
+template <bool WIDE>
 __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int smax) {
     extern __shared__ __attribute__((aligned(16))) float att_lds[];
     float * S = att_lds;                                   // [ATT_P][smax]
@@ -1054,15 +1080,23 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
         for (int r = 0; r < 2; ++r) *reinterpret_cast<v4f *>(tile + (st_r + 16 * r) * ATT_KS + st_c) = pre[r];
     };
 
-    // scores, CHAIN (launches whose LDS admits at most two workgroups per CU), chain-parallel
-    // (att_chain_tree): thread (chain L, key slot js of each tile) with
-    // element 8c + L of the 16 pairs' queries in registers, so that each key's 8 values read
-    // from LDS serve 16 pairs' FMAs. Keys are staged chain-major (row j: [L][c], element
-    // 8c + L at 8L + c), the queries likewise through the tile before the first key tile.
-    // The scores of keys of whole groups of 8 come out of the tree; a pair's last n % 8 keys
-    // take hsum256's tree, one thread per (pair, key) afterwards.
-    if constexpr (CHAIN) {
-        const int L = tid & 7, js = tid >> 3, gL = att_chain_g(L);
+    // scores, chain-parallel (att_chain_tree): lane L of an 8-lane group holds element 8c + L
+    // of NPG pairs' queries and computes chain L of one key's dot products with them, so that
+    // each key's 8 values read from LDS serve NPG pairs' FMAs. WIDE: one group per key for all
+    // 16 pairs (128 query registers; for launches whose LDS admits at most two workgroups per
+    // CU); else two groups per key, 8 pairs each (64 registers), each group taking two keys per
+    // tile. Keys are staged chain-major (row j: [L][c], element 8c + L at 8L + c), the queries
+    // likewise through the tile before the first key tile. The scores of keys of whole groups
+    // of 8 come out of the tree; a pair's last n % 8 keys take hsum256's tree, one thread per
+    // (pair, key) afterwards.
+    {
+        constexpr int NPG = WIDE ? ATT_P : ATT_P / 2;          // pairs per 8-lane group
+        constexpr int NO = WIDE ? 2 : 1;                       // scores per lane out of the tree
+        constexpr int NK = WIDE ? 1 : 2;                       // keys per group per tile
+        const int L = tid & 7, gi = tid >> 3;
+        const int gL = WIDE ? att_chain_g(L) : att_chain_g8(L);
+        const int pbase = WIDE ? 0 : NPG * (gi & 1);
+        const int js0 = WIDE ? gi : gi >> 1;
         {
             const int pp = tid >> 4, m = tid & 15;
             const int t = t0 + pp / rep, h = g * rep + pp % rep;
@@ -1075,20 +1109,21 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
             }
         }
         __syncthreads();
-        float qr[ATT_P][8];
+        float qr[NPG][8];
 #pragma unroll
-        for (int i = 0; i < ATT_P; ++i) {
-            const float * src = tile + (i ^ gL) * ATT_KS + L * 8;
+        for (int i = 0; i < NPG; ++i) {
+            const float * src = tile + (pbase + (i ^ gL)) * ATT_KS + L * 8;
             const v4f a0 = *reinterpret_cast<const v4f *>(src), a1 = *reinterpret_cast<const v4f *>(src + 4);
             qr[i][0] = a0.x; qr[i][1] = a0.y; qr[i][2] = a0.z; qr[i][3] = a0.w;
             qr[i][4] = a1.x; qr[i][5] = a1.y; qr[i][6] = a1.z; qr[i][7] = a1.w;
         }
-        int lo2[2], ng2[2];
-        bool ok2[2];
-        float sc2[2];
+        int lo2[NO], ng2[NO], pp2[NO];
+        bool ok2[NO];
+        float sc2[NO];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int pp = gL + u, n = hi_s[pp] - lo_s[pp];
+        for (int u = 0; u < NO; ++u) {
+            const int pp = pbase + gL + u, n = hi_s[pp] - lo_s[pp];
+            pp2[u] = pp;
             lo2[u] = lo_s[pp];
             ok2[u] = n > 0 && n <= smax;
             ng2[u] = n & ~7;
@@ -1112,22 +1147,26 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
             stage_chain();
             __syncthreads();
             if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
-            const float * kp = tile + js * ATT_KS + L * 8;
-            const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
-            const float kk[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
-            float a[ATT_P];
 #pragma unroll
-            for (int i = 0; i < ATT_P; ++i) a[i] = qr[i][0] * kk[0];
+            for (int r = 0; r < NK; ++r) {
+                const int js = js0 + 16 * r;
+                const float * kp = tile + js * ATT_KS + L * 8;
+                const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
+                const float kk[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
+                float a[NPG];
 #pragma unroll
-            for (int c = 1; c < 8; ++c)
+                for (int i = 0; i < NPG; ++i) a[i] = qr[i][0] * kk[0];
 #pragma unroll
-                for (int i = 0; i < ATT_P; ++i) a[i] = __builtin_fmaf(qr[i][c], kk[c], a[i]);
-            float s2[2];
-            att_chain_tree(a, s2);
+                for (int c = 1; c < 8; ++c)
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int jr = j0 + js - lo2[u];
-                if (ok2[u] && jr >= 0 && jr < ng2[u]) S[(size_t) (gL + u) * smax + jr] = s2[u] * sc2[u];
+                    for (int i = 0; i < NPG; ++i) a[i] = __builtin_fmaf(qr[i][c], kk[c], a[i]);
+                float s2[NO];
+                att_chain_tree(a, s2);
+#pragma unroll
+                for (int u = 0; u < NO; ++u) {
+                    const int jr = j0 + js - lo2[u];
+                    if (ok2[u] && jr >= 0 && jr < ng2[u]) S[(size_t) pp2[u] * smax + jr] = s2[u] * sc2[u];
+                }
             }
         }
         if (valid && sk < n_p - (n_p & ~7)) {
@@ -1141,55 +1180,6 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
                 qv[4 * i] = f.x; qv[4 * i + 1] = f.y; qv[4 * i + 2] = f.z; qv[4 * i + 3] = f.w;
             }
             Sp[jr] = score_d64(qv, kg + (size_t) (lo_s[sp] + jr) * 64, false) * scale_s[sp];
-        }
-    } else {
-        // scores: thread (pair sp, key slots sk and sk + 16 of each tile)
-        const int plo = lo_s[sp], ng_p = n_p & ~7;
-        float qv[64];
-        {
-            const int t = t0 + sp / rep, h = g * rep + sp % rep;
-            const float * qr = p.q + (size_t) min(t, p.T - 1) * p.H * 64 + (size_t) h * 64;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const v4f f = *reinterpret_cast<const v4f *>(qr + 4 * i);
-                qv[4 * i] = f.x; qv[4 * i + 1] = f.y; qv[4 * i + 2] = f.z; qv[4 * i + 3] = f.w;
-            }
-        }
-        const float scale = scale_s[sp];
-        if (kl < kh) fetch(kg, kl);
-        for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
-            __syncthreads();                               // the previous tile has been read
-            stage();
-            __syncthreads();
-            if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const int jr = j0 + sk + 16 * r - plo;
-                if (!valid || jr < 0 || jr >= n_p) continue;
-                const float * kp = tile + (sk + 16 * r) * ATT_KS;
-                float a[8];
-                {
-                    const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
-                    a[0] = qv[0] * k0.x; a[1] = qv[1] * k0.y; a[2] = qv[2] * k0.z; a[3] = qv[3] * k0.w;
-                    a[4] = qv[4] * k1.x; a[5] = qv[5] * k1.y; a[6] = qv[6] * k1.z; a[7] = qv[7] * k1.w;
-                }
-#pragma unroll
-                for (int c = 1; c < 8; ++c) {
-                    const v4f k0 = *reinterpret_cast<const v4f *>(kp + 8 * c);
-                    const v4f k1 = *reinterpret_cast<const v4f *>(kp + 8 * c + 4);
-                    a[0] = __builtin_fmaf(qv[8 * c + 0], k0.x, a[0]);
-                    a[1] = __builtin_fmaf(qv[8 * c + 1], k0.y, a[1]);
-                    a[2] = __builtin_fmaf(qv[8 * c + 2], k0.z, a[2]);
-                    a[3] = __builtin_fmaf(qv[8 * c + 3], k0.w, a[3]);
-                    a[4] = __builtin_fmaf(qv[8 * c + 4], k1.x, a[4]);
-                    a[5] = __builtin_fmaf(qv[8 * c + 5], k1.y, a[5]);
-                    a[6] = __builtin_fmaf(qv[8 * c + 6], k1.z, a[6]);
-                    a[7] = __builtin_fmaf(qv[8 * c + 7], k1.w, a[7]);
-                }
-                const float tot = jr < ng_p ? ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))
-                                            : ((a[0] + a[4]) + (a[2] + a[6])) + ((a[1] + a[5]) + (a[3] + a[7]));
-                Sp[jr] = tot * scale;
-            }
         }
     }
     __syncthreads();
@@ -1360,7 +1350,7 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
 
     // pass 1: the maximum
     if constexpr (STORED) {
-        // the scores chain-parallel, as attention_tile_kernel's CHAIN path (att_chain_tree),
+        // the scores chain-parallel, as attention_tile_kernel's WIDE path (att_chain_tree),
         // each written to the workspace; the maxima of a pair's 32 key slots meet in E, then
         // its 16 lanes; a pair's last n % 8 keys by hsum256's tree, one thread per key
         const int L = tid & 7, js = tid >> 3, gL = att_chain_g(L);
@@ -3983,8 +3973,8 @@ int32_t nxg_attention_ws(const float * q, const float * k, const float * v, cons
         const long long n_tiles = (long long) n_kv_head * ((T + ATT_P / rep - 1) / (ATT_P / rep));
         const size_t lds_max = attention_tile_lds_limit();
         if (tile_lds <= lds_max) {
-            // fewer than 3 workgroups per CU by LDS (the static 1 KiB included): chain-parallel scores
-            if (3 * (tile_lds + 1024) > lds_max + 1024) {
+            // fewer than 3 workgroups per CU by LDS (the static 1 KiB included): 16 pairs per lane group
+            if (NXG_ATT_WIDE && 3 * (tile_lds + 1024) > lds_max + 1024) {
                 attention_tile_kernel<true><<<dim3((unsigned) n_tiles), dim3(256), tile_lds, (hipStream_t) stream>>>(p, smax);
             } else {
                 attention_tile_kernel<false><<<dim3((unsigned) n_tiles), dim3(256), tile_lds, (hipStream_t) stream>>>(p, smax);
