@@ -1689,11 +1689,8 @@ __device__ __forceinline__ void qk_prep_elem(const float * __restrict__ x, const
                                              const float * __restrict__ beta, const float * __restrict__ cos_t,
                                              const float * __restrict__ sin_t, const int32_t * __restrict__ cu,
                                              int n_seqs, int T, int H, int D, int n_pos, int head_major,
-                                             float * __restrict__ out, size_t idx) {
+                                             float * __restrict__ out, int t, int h, int i) {
     const int half = D / 2;
-    const int i = (int) (idx % half);
-    const int h = (int) ((idx / half) % H);
-    const int t = (int) (idx / ((size_t) half * H));
     const doc_rows dr = doc_of(cu, n_seqs, t, T);
     const int pos = min(max(t - dr.lo, 0), n_pos - 1);
     const float c = cos_t[(size_t) pos * half + i], s = sin_t[(size_t) pos * half + i];
@@ -1710,30 +1707,31 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const float * __restrict__
                                                       const float * __restrict__ sin_t, const int32_t * __restrict__ cu,
                                                       int n_seqs, int T, int H, int D, int n_pos, int head_major,
                                                       float * __restrict__ out) {
-    const size_t idx = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t) T * H * (D / 2)) return;
-    qk_prep_elem(x, alpha, beta, cos_t, sin_t, cu, n_seqs, T, H, D, n_pos, head_major, out, idx);
+    // workgroup (row t, piece y) of a [T][H * D / 2] index space: no 64-bit divisions
+    const int t = (int) blockIdx.x, half = D / 2;
+    const int r = (int) blockIdx.y * 256 + (int) threadIdx.x;
+    if (r >= H * half) return;
+    qk_prep_elem(x, alpha, beta, cos_t, sin_t, cu, n_seqs, T, H, D, n_pos, head_major, out, t, r / half, r % half);
 }
 
 // op_head_major (src/nexterabert.cpp:620-632): [T][H*D] -> [H][T][D].
 __device__ __forceinline__ void head_major_elem(const float * __restrict__ x, int T, int H, int D,
-                                                float * __restrict__ out, size_t idx) {
-    const int e = (int) (idx % D);
-    const int h = (int) ((idx / D) % H);
-    const int t = (int) (idx / ((size_t) D * H));
-    out[((size_t) h * T + t) * D + e] = x[idx];
+                                                float * __restrict__ out, int t, int h, int e) {
+    out[((size_t) h * T + t) * D + e] = x[((size_t) t * H + h) * D + e];
 }
 
 __global__ __launch_bounds__(256) void head_major_kernel(const float * __restrict__ x, int T, int H, int D,
                                                          float * __restrict__ out) {
-    const size_t idx = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t) T * H * D) return;
-    head_major_elem(x, T, H, D, out, idx);
+    const int t = (int) blockIdx.x;
+    const int r = (int) blockIdx.y * 256 + (int) threadIdx.x;
+    if (r >= H * D) return;
+    head_major_elem(x, T, H, D, out, t, r / D, r % D);
 }
 
 // builder::attention's three ops on one layer's projections (src/nexterabert.cpp:1186-1188) in
 // one launch: qk_prep of the queries (row-major), qk_prep of the keys (head-major) and the
-// values' head-major copy, each thread taking one element of one of them by index range.
+// values' head-major copy. Workgroup (row t, piece y): thread r of the row's
+// H * D / 2 + G * D / 2 + G * D elements takes one of them by index range.
 struct qkv_prep_params {
     const float * q;
     const float * k;
@@ -1751,16 +1749,17 @@ struct qkv_prep_params {
     float * v_out;
 };
 __global__ __launch_bounds__(256) void qkv_prep_kernel(qkv_prep_params p) {
-    const size_t idx = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t nq = (size_t) p.T * p.H * (p.D / 2), nk = (size_t) p.T * p.G * (p.D / 2);
-    const size_t nv = (size_t) p.T * p.G * p.D;
-    if (idx < nq) {
-        qk_prep_elem(p.q, p.q_alpha, p.q_beta, p.cos_t, p.sin_t, p.cu, p.n_seqs, p.T, p.H, p.D, p.n_pos, 0, p.q_out, idx);
-    } else if (idx < nq + nk) {
+    const int t = (int) blockIdx.x, half = p.D / 2;
+    const int r = (int) blockIdx.y * 256 + (int) threadIdx.x;
+    const int nq = p.H * half, nk = p.G * half, nv = p.G * p.D;
+    if (r < nq) {
+        qk_prep_elem(p.q, p.q_alpha, p.q_beta, p.cos_t, p.sin_t, p.cu, p.n_seqs, p.T, p.H, p.D, p.n_pos, 0, p.q_out,
+                     t, r / half, r % half);
+    } else if (r < nq + nk) {
         qk_prep_elem(p.k, p.k_alpha, p.k_beta, p.cos_t, p.sin_t, p.cu, p.n_seqs, p.T, p.G, p.D, p.n_pos, 1, p.k_out,
-                     idx - nq);
-    } else if (idx < nq + nk + nv) {
-        head_major_elem(p.v, p.T, p.G, p.D, p.v_out, idx - nq - nk);
+                     t, (r - nq) / half, (r - nq) % half);
+    } else if (r < nq + nk + nv) {
+        head_major_elem(p.v, p.T, p.G, p.D, p.v_out, t, (r - nq - nk) / p.D, (r - nq - nk) % p.D);
     }
 }
 
@@ -4007,11 +4006,11 @@ int32_t nxg_qk_prep(const float * x, const float * alpha, const float * beta, co
     }
     if (T == 0) return NXG_OK;
     if (!x || !alpha || !beta || !cos_t || !sin_t || !cu_offsets || !out) return fail(NXG_EINVAL, "qk_prep: null buffer");
-    const size_t n = (size_t) T * n_head * (head_dim / 2);
-    if (n / 256 + 1 > (size_t) INT32_MAX) return fail(NXG_EINVAL, "qk_prep: too large");
+    const long long per_row = (long long) n_head * (head_dim / 2);
+    if (per_row > INT32_MAX / 2) return fail(NXG_EINVAL, "qk_prep: too large");
     int rc = check_device();
     if (rc) return rc;
-    qk_prep_kernel<<<(unsigned) ((n + 255) / 256), 256, 0, (hipStream_t) stream>>>(
+    qk_prep_kernel<<<dim3((unsigned) T, (unsigned) ((per_row + 255) / 256)), 256, 0, (hipStream_t) stream>>>(
         x, alpha, beta, cos_t, sin_t, cu_offsets, n_seqs, T, n_head, head_dim, n_pos, head_major ? 1 : 0, out);
     return launch_check("qk_prep_kernel");
 }
@@ -4020,11 +4019,12 @@ int32_t nxg_head_major(const float * x, int32_t T, int32_t n_head, int32_t head_
     if (T < 0 || n_head < 1 || head_dim < 1) return fail(NXG_EINVAL, "head_major: T=%d n_head=%d head_dim=%d", T, n_head, head_dim);
     if (T == 0) return NXG_OK;
     if (!x || !out) return fail(NXG_EINVAL, "head_major: null buffer");
-    const size_t n = (size_t) T * n_head * head_dim;
-    if (n / 256 + 1 > (size_t) INT32_MAX) return fail(NXG_EINVAL, "head_major: too large");
+    const long long per_row = (long long) n_head * head_dim;
+    if (per_row > INT32_MAX / 2) return fail(NXG_EINVAL, "head_major: too large");
     int rc = check_device();
     if (rc) return rc;
-    head_major_kernel<<<(unsigned) ((n + 255) / 256), 256, 0, (hipStream_t) stream>>>(x, T, n_head, head_dim, out);
+    head_major_kernel<<<dim3((unsigned) T, (unsigned) ((per_row + 255) / 256)), 256, 0, (hipStream_t) stream>>>(
+        x, T, n_head, head_dim, out);
     return launch_check("head_major_kernel");
 }
 
@@ -4041,13 +4041,13 @@ int32_t nxg_qkv_prep(const float * q, const float * k, const float * v, const fl
         !k_out || !v_out) {
         return fail(NXG_EINVAL, "qkv_prep: null buffer");
     }
-    const size_t n = (size_t) T * (n_head + n_kv_head) * (head_dim / 2) + (size_t) T * n_kv_head * head_dim;
-    if (n / 256 + 1 > (size_t) INT32_MAX) return fail(NXG_EINVAL, "qkv_prep: too large");
+    const long long per_row = (long long) (n_head + n_kv_head) * (head_dim / 2) + (long long) n_kv_head * head_dim;
+    if (per_row > INT32_MAX / 2) return fail(NXG_EINVAL, "qkv_prep: too large");
     int rc = check_device();
     if (rc) return rc;
     const qkv_prep_params p{ q, k, v, q_alpha, q_beta, k_alpha, k_beta, cos_t, sin_t, cu_offsets, n_seqs, T,
                              n_head, n_kv_head, head_dim, n_pos, q_out, k_out, v_out };
-    qkv_prep_kernel<<<(unsigned) ((n + 255) / 256), 256, 0, (hipStream_t) stream>>>(p);
+    qkv_prep_kernel<<<dim3((unsigned) T, (unsigned) ((per_row + 255) / 256)), 256, 0, (hipStream_t) stream>>>(p);
     return launch_check("qkv_prep_kernel");
 }
 
