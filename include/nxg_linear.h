@@ -384,7 +384,8 @@ NXG_API int32_t nxg_linear_i8_relu2_q8_rows(const nxg_weight * w, const int8_t *
  * with at least 4 tiles of 64 rows by 256 outputs per workgroup (two workgroups per compute
  * unit: 16,384 rows of 2,304 outputs on 256 CUs), each row tile is quantized inside the GEMM
  * and the int8 input never goes to memory; otherwise q_ws, sx_ws (a qact of T rows by n_in, nxg_qact_q_bytes(T, n_in) and
- * nxg_qact_sx_bytes(T, n_in) bytes) receive nxg_quantize_rows(x) first. */
+ * nxg_qact_sx_bytes(T, n_in) bytes) receive nxg_quantize_rows(x) first. The workspace is
+ * required in either case (whether the fused kernel runs depends on the device's CU count). */
 NXG_API int32_t nxg_linear_f32_relu2_q8_rows(const nxg_weight * w, const float * x, int32_t T, int32_t act_max,
                                              int8_t * q_ws, float * sx_ws, int8_t * q_out, float * sx_out,
                                              void * stream);
