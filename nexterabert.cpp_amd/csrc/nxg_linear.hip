@@ -367,16 +367,20 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(const float * __r
 // NaN anywhere in the group's normalized values sends the group through quantize_block,
 // whose fold gives the reference's MAXPS result; without NaN that fold is the plain max.
 // SPLIT (few rows): one workgroup per (row group, block), the dot still over the whole row
-// from registers, only block blockIdx % NB quantized and stored -- NB times the workgroups
-// for launches too small to fill the device.
+// from registers, only one block quantized and stored -- NB times the workgroups for
+// launches too small to fill the device. Workgroup b runs on XCD b % 8, so the NB
+// workgroups of a row group are given the same b % 8 and share that XCD's L2 for the rows
+// they all read (the grid is padded to whole rounds of 8 row groups).
 template <int ACT_MAX, int NB, bool SPLIT>
 __global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float * __restrict__ x, const float * __restrict__ gain,
                                                          float eps, int T, int8_t * __restrict__ q,
                                                          float * __restrict__ sx) {
     constexpr int n_in = NB * BLK, M = n_in / 32, KS = 4 * NB;
     __shared__ __attribute__((aligned(16))) int stage[KS * FRAG / 4];
-    const int g = SPLIT ? (int) (blockIdx.x / NB) : (int) blockIdx.x;
-    const int Bs = SPLIT ? (int) (blockIdx.x % NB) : 0;       // SPLIT: the block of this workgroup
+    const int xcd = (int) (blockIdx.x & 7u), slot = (int) (blockIdx.x >> 3);
+    const int g = SPLIT ? (slot / NB) * 8 + xcd : (int) blockIdx.x;
+    const int Bs = SPLIT ? slot % NB : 0;                      // SPLIT: the block of this workgroup
+    if (SPLIT && g * 16 >= T) return;                          // padding of the grid to whole rounds
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rl = wave * 4 + (lane >> 4), t = g * 16 + rl, c = lane & 15;
     float2 v[M];
@@ -3755,7 +3759,7 @@ int32_t nxg_rmsnorm_quantize_rows(const float * x, const float * gain, float eps
         // the whole row group in registers: n_in = 256, 512, 1024 or 2048
         // fewer row groups than twice the CUs: one workgroup per (row group, block)
         const bool split = (long long) (d.MP / 16) < 2LL * device_cus();
-        const dim3 grid((unsigned) (d.MP / 16)), grid_s((unsigned) (d.MP / 16 * d.n_blk));
+        const dim3 grid((unsigned) (d.MP / 16)), grid_s((unsigned) ((d.MP / 16 + 7) / 8 * 8 * d.n_blk));
 #define NXG_RMS_Q8(NB)                                                                                        \
         case NB:                                                                                              \
             if (split) {                                                                                      \
