@@ -587,12 +587,13 @@ def mfma_counters(args, timeout_s: int = 240) -> dict:
         shutil.rmtree(out, ignore_errors=True)
 
 
-def pmc_summary(fetch_csv: str, write_csv: str, calib_mib: int, out_path: Path) -> dict:
+def pmc_summary(fetch_csv: str, write_csv: str, calib_mib: int, out_path: Path, merge: bool = False) -> dict:
     """HBM traffic per launch of each GEMM and quantize kernel from two rocprofv3 --pmc runs
     of this script (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the
     same counter reads for the calibration copy of calib_mib MiB (a device to device copy,
     dispatched by the HIP runtime as its copy-buffer kernel). Per kernel name, and per class
-    (gemm_fp32, gemm_relu2, quant) as the mean over the class's launches."""
+    (gemm_fp32, gemm_relu2, quant) as the mean over the class's launches. merge: keep the
+    per-kernel entries of the existing file for kernels this run did not launch."""
     import csv
 
     def per_kernel(path, counter):
@@ -632,6 +633,11 @@ def pmc_summary(fetch_csv: str, write_csv: str, calib_mib: int, out_path: Path) 
         wv = [v for n in w if cls(n) == c for v in w[n]]
         if fv and wv:
             res[c] = entry(fv, wv)
+    if merge and out_path.exists():
+        # kernels of another run of the same workload (e.g. --no-fuse-quant) kept beside these
+        old = json.loads(out_path.read_text())
+        for n, e in (old.get("by_kernel") or {}).items():
+            res["by_kernel"].setdefault(n, e)
     out_path.write_text(json.dumps(res, indent=2) + "\n")
     return res
 
@@ -662,12 +668,15 @@ def main() -> int:
     ap.add_argument("--no-counters", action="store_true",
                     help="skip the rocprofv3 MFMA-counter pass (MFMA busy %% of both GEMM kinds)")
     ap.add_argument("--counter-pass", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--pmc-merge", action="store_true",
+                    help="with --pmc-summary: keep the existing file's entries for kernels this run did not launch")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarize two rocprofv3 --pmc counter_collection.csv files of a run with "
                          "--calib-copy-mib into " + str(TRAFFIC_FILE.relative_to(ROOT)) + " and exit")
     args = ap.parse_args()
     if args.pmc_summary:
-        res = pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.calib_copy_mib or 512, TRAFFIC_FILE)
+        res = pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.calib_copy_mib or 512, TRAFFIC_FILE,
+                          merge=args.pmc_merge)
         print(json.dumps(res))
         return 0
     if args.gpus != 1:
@@ -714,16 +723,19 @@ def main() -> int:
     # One roofline per kernel; `roofline` is the GEMM kernel with the largest share of the step.
     kernels = kernel_rooflines(nxg, gemm_ev, quant_ev, args.steps)
     tr = json.loads(TRAFFIC_FILE.read_text()) if TRAFFIC_FILE.exists() else {}
-    use_traffic = args.rows == 65536 and not args.no_fuse and not args.no_fuse_mlp and not args.no_fuse_quant
-    for r in kernels:
-        by = (tr.get("by_kernel") or {}).get(r["kernel"])
-        if use_traffic and by:
-            r["traffic"] = by["hbm_bytes_per_launch"]
-            r["traffic_over_algorithmic"] = round(by["hbm_bytes_per_launch"] / r["per_launch"]["algorithmic_bytes"], 3)
-        for kind in ("fp32", "relu2"):
-            bk = ((counters or {}).get(kind) or {}).get("by_kernel", {}).get(r["kernel"])
-            if bk:
-                r["mfma_busy_pct"] = bk["mfma_busy_pct"]
+    use_traffic = args.rows == 65536 and not args.no_fuse and not args.no_fuse_mlp
+
+    def annotate(rs):
+        for r in rs:
+            by = (tr.get("by_kernel") or {}).get(r["kernel"])
+            if use_traffic and by:
+                r["traffic"] = by["hbm_bytes_per_launch"]
+                r["traffic_over_algorithmic"] = round(by["hbm_bytes_per_launch"] / r["per_launch"]["algorithmic_bytes"], 3)
+            for kind in ("fp32", "relu2"):
+                bk = ((counters or {}).get(kind) or {}).get("by_kernel", {}).get(r["kernel"])
+                if bk:
+                    r["mfma_busy_pct"] = bk["mfma_busy_pct"]
+    annotate(kernels)
     roof = dict(next(r for r in kernels if not r["kernel"].startswith("quantize")))
     if roof.get("traffic") is not None:
         roof["traffic_source"] = (f"{TRAFFIC_FILE.relative_to(ROOT)}: rocprofv3 FETCH_SIZE x {tr['fetch_scale']} + "
@@ -741,6 +753,7 @@ def main() -> int:
         ql = path_line(nxg, pq, args.steps, args.warmup, "the same step, every input quantized by its own launch")
         qfirst = {k: ql[k] for k in ("workload", "ms_per_step", "int8_tops", "quantize_launches",
                                      "gemm_ms_per_step", "quantize_ms_per_step")}
+        annotate(ql["kernels"])
         qfirst["roofline_relu2_q8"] = next((r for r in ql["kernels"] if r["kernel"].startswith("gemm_relu2")), None)
         log(f"quantize first: {qfirst['ms_per_step']} ms/step, relu2 kernel frac "
             f"{(qfirst['roofline_relu2_q8'] or {}).get('frac')}")
@@ -814,7 +827,11 @@ def main() -> int:
         "encoder_1024": enc,
         "encoder": full,
         "roofline": roof,
-        "roofline_relu2_q8": roof_relu2,
+        # the relu^2 GEMM from a qact (the quantize_first step) where the headline step's c_fc
+        # quantizes its fp32 rows itself; that kernel's roofline is roofline_relu2_f32_in
+        "roofline_relu2_q8": dict((qfirst or {}).get("roofline_relu2_q8") or {}, step="quantize_first")
+                             if (qfirst or {}).get("roofline_relu2_q8") else roof_relu2,
+        "roofline_relu2_f32_in": roof_relu2 if path.n_relu2_f32 else None,
         "quantize_first": qfirst,
         "rooflines_by_kernel": kernels,
         "shapes": shapes,
