@@ -593,7 +593,7 @@ def pmc_summary(fetch_csv: str, write_csv: str, calib_mib: int, out_path: Path, 
     same counter reads for the calibration copy of calib_mib MiB (a device to device copy,
     dispatched by the HIP runtime as its copy-buffer kernel). Per kernel name, and per class
     (gemm_fp32, gemm_relu2, quant) as the mean over the class's launches. merge: keep the
-    per-kernel entries of the existing file for kernels this run did not launch."""
+    existing file and add this run's entries for the kernels it does not have."""
     import csv
 
     def per_kernel(path, counter):
@@ -634,10 +634,11 @@ def pmc_summary(fetch_csv: str, write_csv: str, calib_mib: int, out_path: Path, 
         if fv and wv:
             res[c] = entry(fv, wv)
     if merge and out_path.exists():
-        # kernels of another run of the same workload (e.g. --no-fuse-quant) kept beside these
+        # the existing file stays as it is; this run (e.g. --no-fuse-quant) adds the kernels it lacks
         old = json.loads(out_path.read_text())
-        for n, e in (old.get("by_kernel") or {}).items():
-            res["by_kernel"].setdefault(n, e)
+        for n, e in res["by_kernel"].items():
+            old.setdefault("by_kernel", {}).setdefault(n, e)
+        res = old
     out_path.write_text(json.dumps(res, indent=2) + "\n")
     return res
 
@@ -669,7 +670,7 @@ def main() -> int:
                     help="skip the rocprofv3 MFMA-counter pass (MFMA busy %% of both GEMM kinds)")
     ap.add_argument("--counter-pass", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--pmc-merge", action="store_true",
-                    help="with --pmc-summary: keep the existing file's entries for kernels this run did not launch")
+                    help="with --pmc-summary: keep the existing file, adding this run's kernels it lacks")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarize two rocprofv3 --pmc counter_collection.csv files of a run with "
                          "--calib-copy-mib into " + str(TRAFFIC_FILE.relative_to(ROOT)) + " and exit")
