@@ -1301,8 +1301,13 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
 // ([gridDim.x][ATT_P][max_keys] floats, pair-relative key index), and passes 2 and 3 read the
 // scores back instead of recomputing them, the same bits; pass 2 then needs no staged keys
 // (lane l < 8 of a pair adds keys 16b + l and 16b + 8 + l, the second taken from lane l + 8),
-// pass 3 stages only the values. One call is the tile bt = (KV head, query block).
-template <bool STORED>
+// pass 3 stages only the values. ESTORE: pass 2 also writes each e = exp(s - m) over
+// its score and pass 3 takes w = e * (1 / sum) from it (the same bits as recomputing e).
+// One call is the tile bt = (KV head, query block).
+#ifndef NXG_ATT_E_STORE_MIB
+#define NXG_ATT_E_STORE_MIB 192   // the largest workspace in use (all slots) for which pass 2 stores e
+#endif
+template <bool STORED, bool ESTORE = false>
 __device__ __forceinline__ void attention_long_tile(const attn_params & p, float * __restrict__ sc, int bt) {
     __shared__ __attribute__((aligned(16))) float tile[ATT_KT * ATT_KS];
     __shared__ float E[ATT_P][ATT_KT + 1];                 // one tile's e (pass 2) or w (pass 3)
@@ -1522,6 +1527,7 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
                 if (b + 16 * u >= ng) break;               // uniform over the pair's 16 lanes
                 const int jr = b + 16 * u + sk;
                 const float e = jr < ng ? exp_cephes(cur[u] - m) : 0.0f;
+                if (ESTORE && jr < ng) scp[jr] = e;        // pass 3 reads e in place of the score
                 const float e8 = __shfl_down(e, 8, 16);    // key jr + 8, from lane sk + 8
                 if (sk < 8) {
                     ls = ls + e;
@@ -1536,7 +1542,11 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
         ls = ls + __shfl_xor(ls, 1);
         if (valid && sk == 0) {
             float sum = ls;
-            for (int jr = ng_p; jr < n_p; ++jr) sum = sum + expf_libm(scp[jr] - m);
+            for (int jr = ng_p; jr < n_p; ++jr) {
+                const float e = expf_libm(scp[jr] - m);
+                if (ESTORE) scp[jr] = e;
+                sum = sum + e;
+            }
             inv_s[sp] = 1.0f / sum;
         }
         __syncthreads();
@@ -1612,7 +1622,8 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
                 const int kt = sk + 16 * r, jr = j0 + kt - plo;
                 if (!valid || jr < 0 || jr >= n_p) continue;
                 const float s = snx[r];
-                E[sp][kt] = (jr < ng_p ? exp_cephes(s - m) : expf_libm(s - m)) * inv;
+                if (ESTORE) E[sp][kt] = s * inv;          // s holds e = exp(score - m), written by pass 2
+                else E[sp][kt] = (jr < ng_p ? exp_cephes(s - m) : expf_libm(s - m)) * inv;
             }
             __syncthreads();                               // the values and the weights are in LDS
             if (j0 + ATT_KT < kh) {
@@ -1679,13 +1690,14 @@ __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
 }
 
 // The scores kept in the workspace: a persistent grid, one slot of sc per workgroup, which
-// takes tiles blockIdx.x, blockIdx.x + gridDim.x, ...
+// takes tiles blockIdx.x, blockIdx.x + gridDim.x, ... ESTORE: pass 2 stores the exponentials.
+template <bool ESTORE>
 __global__ __launch_bounds__(256) void attention_stored_kernel(attn_params p, float * __restrict__ sc) {
     const int nq = ATT_P / (p.H / p.G);
     const int n_tiles = p.G * ((p.T + nq - 1) / nq);
     for (int bt = (int) blockIdx.x; bt < n_tiles; bt += (int) gridDim.x) {
         __syncthreads();                                   // the previous tile's shared reads are done
-        attention_long_tile<true>(p, sc, bt);
+        attention_long_tile<true, ESTORE>(p, sc, bt);
     }
 }
 
@@ -3895,7 +3907,7 @@ static long long attention_long_slots() {
         int cus = 0, per_cu = 0;
         if (dev >= 0 &&
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attention_stored_kernel, 256, 0) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attention_stored_kernel<false>, 256, 0) == hipSuccess &&
             cus > 0 && per_cu > 0) {
             slots = (long long) cus * per_cu;
         } else {
@@ -4009,7 +4021,15 @@ int32_t nxg_attention_ws(const float * q, const float * k, const float * v, cons
         const attn_plan pl = plan_attention(T, n_head, n_kv_head, max_keys);
         const long long n_slots = std::min({n_tiles, attention_long_slots(), (long long) (workspace_bytes / pl.slot_bytes)});
         if (n_slots >= 1) {
-            attention_stored_kernel<<<dim3((unsigned) n_slots), dim3(256), 0, (hipStream_t) stream>>>(p, (float *) workspace);
+            // e stored by pass 2 (4 more bytes per (pair, key)) pays while the slots in use stay
+            // in the last-level cache: 4,096 keys 2.46 -> 2.40 ms, documents of 3,000 / 5,000 keys
+            // 5.63 -> 5.41 ms; 8,192 keys (256 MiB of slots) even, 16,384 keys 40.8 -> 44.6 ms
+            const bool e_store = (double) n_slots * (double) pl.slot_bytes <= (double) NXG_ATT_E_STORE_MIB * 1048576.0;
+            if (e_store) {
+                attention_stored_kernel<true><<<dim3((unsigned) n_slots), dim3(256), 0, (hipStream_t) stream>>>(p, (float *) workspace);
+            } else {
+                attention_stored_kernel<false><<<dim3((unsigned) n_slots), dim3(256), 0, (hipStream_t) stream>>>(p, (float *) workspace);
+            }
             return launch_check("attention_stored_kernel");
         }
         attention_long_kernel<<<dim3((unsigned) n_tiles), dim3(256), 0, (hipStream_t) stream>>>(p);

@@ -224,8 +224,10 @@ def test_head_major(nxg, torch, dev):
 
 def test_attention_workspace_16384_keys(nxg, torch, dev):
     """One 16,384-token document: nxg_attention_ws with a 3-slot workspace (few workgroups at a
-    time, each over many query tiles) equals the recomputing kernel (no workspace) bit for bit."""
-    say("attention 16,384 keys: 3-slot workspace vs recomputing kernel")
+    time, each over many query tiles; 3 MiB of slots, so pass 2 stores the exponentials for pass
+    3) and with a slot per resident workgroup (512 MiB: pass 3 recomputes them) equals the
+    recomputing kernel (no workspace) bit for bit."""
+    say("attention 16,384 keys: 3-slot and full workspaces vs recomputing kernel")
     H, G, T = 2, 1, 16384
     g = torch.Generator("cuda").manual_seed(16)
     q = torch.randn(T, H * 64, device="cuda", generator=g)
@@ -236,9 +238,11 @@ def test_attention_workspace_16384_keys(nxg, torch, dev):
     slot = 16 * T * 4
     y_rec = nxg.attention(q, k, v, cu, scale, H, G)
     y_ws = nxg.attention(q, k, v, cu, scale, H, G, workspace=torch.empty(3 * slot, dtype=torch.uint8, device="cuda"))
+    y_full = nxg.attention(q, k, v, cu, scale, H, G, workspace="auto")
     torch.cuda.synchronize()
     assert torch.isfinite(y_rec).all()
     assert torch.equal(y_rec.view(torch.int32), y_ws.view(torch.int32))
+    assert torch.equal(y_rec.view(torch.int32), y_full.view(torch.int32))
 
 
 def test_attention_auto_workspace_on_a_side_stream(nxg, orc, torch, dev):
