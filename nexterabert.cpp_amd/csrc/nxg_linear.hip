@@ -1304,6 +1304,9 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
 // pass 3 stages only the values. ESTORE: pass 2 also writes each e = exp(s - m) over
 // its score and pass 3 takes w = e * (1 / sum) from it (the same bits as recomputing e).
 // One call is the tile bt = (KV head, query block).
+#ifndef NXG_ATT_STORED_WIDE
+#define NXG_ATT_STORED_WIDE 0  // attention_stored_kernel's scores: 16 pairs per lane group (0: 8)
+#endif
 #ifndef NXG_ATT_E_STORE_MIB
 #define NXG_ATT_E_STORE_MIB 192   // the largest workspace in use (all slots) for which pass 2 stores e
 #endif
@@ -1380,10 +1383,18 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
 
     // pass 1: the maximum
     if constexpr (STORED) {
-        // the scores chain-parallel, as attention_tile_kernel's WIDE path (att_chain_tree),
-        // each written to the workspace; the maxima of a pair's 32 key slots meet in E, then
-        // its 16 lanes; a pair's last n % 8 keys by hsum256's tree, one thread per key
-        const int L = tid & 7, js = tid >> 3, gL = att_chain_g(L);
+        // the scores chain-parallel, as attention_tile_kernel (att_chain_tree; SW: 16 pairs
+        // per lane group, else 8 pairs and two keys per group and tile), each written to the
+        // workspace; the maxima of a pair's key slots meet in E, then its 16 lanes; a pair's
+        // last n % 8 keys by hsum256's tree, one thread per key
+        constexpr bool SW = NXG_ATT_STORED_WIDE;
+        constexpr int NPG = SW ? ATT_P : ATT_P / 2;            // pairs per 8-lane group
+        constexpr int NO = SW ? 2 : 1;                         // scores per lane out of the tree
+        constexpr int NK = SW ? 1 : 2;                         // keys per group per tile
+        const int L = tid & 7, gi = tid >> 3;
+        const int gL = SW ? att_chain_g(L) : att_chain_g8(L);
+        const int pbase = SW ? 0 : NPG * (gi & 1);
+        const int js0 = SW ? gi : gi >> 1;
         {
             const int pp = tid >> 4, m = tid & 15;
             const int t = t0 + pp / rep, h = g * rep + pp % rep;
@@ -1396,21 +1407,21 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
             }
         }
         __syncthreads();
-        float qr[ATT_P][8];
+        float qr[NPG][8];
 #pragma unroll
-        for (int i = 0; i < ATT_P; ++i) {
-            const float * src = tile + (i ^ gL) * ATT_KS + L * 8;
+        for (int i = 0; i < NPG; ++i) {
+            const float * src = tile + (pbase + (i ^ gL)) * ATT_KS + L * 8;
             const v4f a0 = *reinterpret_cast<const v4f *>(src), a1 = *reinterpret_cast<const v4f *>(src + 4);
             qr[i][0] = a0.x; qr[i][1] = a0.y; qr[i][2] = a0.z; qr[i][3] = a0.w;
             qr[i][4] = a1.x; qr[i][5] = a1.y; qr[i][6] = a1.z; qr[i][7] = a1.w;
         }
-        int lo2[2], ng2[2];
-        bool ok2[2];
-        float sc2[2], mx2[2];
-        float * sp2[2];
+        int lo2[NO], ng2[NO];
+        bool ok2[NO];
+        float sc2[NO], mx2[NO];
+        float * sp2[NO];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int pp = gL + u, n = hi_s[pp] - lo_s[pp];
+        for (int u = 0; u < NO; ++u) {
+            const int pp = pbase + gL + u, n = hi_s[pp] - lo_s[pp];
             lo2[u] = lo_s[pp];
             ok2[u] = n > 0 && n <= p.max_keys;
             ng2[u] = n & ~7;
@@ -1436,33 +1447,39 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
             stage_chain();
             __syncthreads();
             if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
-            const float * kp = tile + js * ATT_KS + L * 8;
-            const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
-            const float kk[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
-            float a[ATT_P];
 #pragma unroll
-            for (int i = 0; i < ATT_P; ++i) a[i] = qr[i][0] * kk[0];
+            for (int r = 0; r < NK; ++r) {
+                const int js = js0 + 16 * r;
+                const float * kp = tile + js * ATT_KS + L * 8;
+                const v4f k0 = *reinterpret_cast<const v4f *>(kp), k1 = *reinterpret_cast<const v4f *>(kp + 4);
+                const float kk[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
+                float a[NPG];
 #pragma unroll
-            for (int c = 1; c < 8; ++c)
+                for (int i = 0; i < NPG; ++i) a[i] = qr[i][0] * kk[0];
 #pragma unroll
-                for (int i = 0; i < ATT_P; ++i) a[i] = __builtin_fmaf(qr[i][c], kk[c], a[i]);
-            float s2[2];
-            att_chain_tree(a, s2);
+                for (int c = 1; c < 8; ++c)
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int jr = j0 + js - lo2[u];
-                if (ok2[u] && jr >= 0 && jr < ng2[u]) {
-                    const float s = s2[u] * sc2[u];
-                    mx2[u] = fmaxf(mx2[u], s);
-                    sp2[u][jr] = s;
-                    if (jr == 0) s0_s[gL + u] = s;
+                    for (int i = 0; i < NPG; ++i) a[i] = __builtin_fmaf(qr[i][c], kk[c], a[i]);
+                float s2[NO];
+                att_chain_tree(a, s2);
+#pragma unroll
+                for (int u = 0; u < NO; ++u) {
+                    const int jr = j0 + js - lo2[u];
+                    if (ok2[u] && jr >= 0 && jr < ng2[u]) {
+                        const float s = s2[u] * sc2[u];
+                        mx2[u] = fmaxf(mx2[u], s);
+                        sp2[u][jr] = s;
+                        if (jr == 0) s0_s[pbase + gL + u] = s;
+                    }
                 }
             }
         }
-        E[gL][js] = mx2[0];
-        E[gL + 1][js] = mx2[1];
+        // SW: pair gL + u's maxima over key slots js0 (0..31); else pair pbase + gL's over
+        // key slots js0 and js0 + 16 in slot js0 (0..15)
+#pragma unroll
+        for (int u = 0; u < NO; ++u) E[pbase + gL + u][js0] = mx2[u];
         __syncthreads();
-        float mx = fmaxf(E[sp][sk], E[sp][sk + 16]);
+        float mx = SW ? fmaxf(E[sp][sk], E[sp][sk + 16]) : E[sp][sk];
         if (valid && sk < n_p - ng_p) {
             const int jr = ng_p + sk;
 #pragma unroll
@@ -1691,8 +1708,14 @@ __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
 
 // The scores kept in the workspace: a persistent grid, one slot of sc per workgroup, which
 // takes tiles blockIdx.x, blockIdx.x + gridDim.x, ... ESTORE: pass 2 stores the exponentials.
+// Three workgroups per CU (at most 168 registers; 8 pairs per lane group in pass 1, as 16 would
+// spill): 16,384 keys 40.9 -> 34.7 ms, 8,192 keys 10.2 -> 8.4 ms against two workgroups per CU with
+// 16 pairs per group (256 registers); four per CU (128 registers) spill and lose 1-10%.
+#ifndef NXG_ATT_STORED_MINB
+#define NXG_ATT_STORED_MINB 3
+#endif
 template <bool ESTORE>
-__global__ __launch_bounds__(256) void attention_stored_kernel(attn_params p, float * __restrict__ sc) {
+__global__ __launch_bounds__(256, NXG_ATT_STORED_MINB) void attention_stored_kernel(attn_params p, float * __restrict__ sc) {
     const int nq = ATT_P / (p.H / p.G);
     const int n_tiles = p.G * ((p.T + nq - 1) / nq);
     for (int bt = (int) blockIdx.x; bt < n_tiles; bt += (int) gridDim.x) {
@@ -4022,8 +4045,9 @@ int32_t nxg_attention_ws(const float * q, const float * k, const float * v, cons
         const long long n_slots = std::min({n_tiles, attention_long_slots(), (long long) (workspace_bytes / pl.slot_bytes)});
         if (n_slots >= 1) {
             // e stored by pass 2 (4 more bytes per (pair, key)) pays while the slots in use stay
-            // in the last-level cache: 4,096 keys 2.46 -> 2.40 ms, documents of 3,000 / 5,000 keys
-            // 5.63 -> 5.41 ms; 8,192 keys (256 MiB of slots) even, 16,384 keys 40.8 -> 44.6 ms
+            // in the last-level cache: 4,096 keys 1.97 -> 1.94 ms, 16,384 keys in bands of 2,601
+            // 5.39 -> 5.32 ms; beyond it even or slower (at two workgroups per CU: 8,192 keys even,
+            // 16,384 keys 40.8 -> 44.6 ms)
             const bool e_store = (double) n_slots * (double) pl.slot_bytes <= (double) NXG_ATT_E_STORE_MIB * 1048576.0;
             if (e_store) {
                 attention_stored_kernel<true><<<dim3((unsigned) n_slots), dim3(256), 0, (hipStream_t) stream>>>(p, (float *) workspace);
