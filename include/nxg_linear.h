@@ -198,12 +198,15 @@ NXG_API int32_t nxg_attention(const float * q, const float * k, const float * v,
                               int32_t n_seqs, const float * scale, int32_t T, int32_t n_head, int32_t n_kv_head,
                               int32_t half, int32_t max_keys, float * out, void * stream);
 
-/* op_attention (src/nexterabert.cpp:785-852) as nxg_attention, with a device workspace for documents whose scores do not fit in LDS (more than
- * ~2,400 keys per query with n_head / n_kv_head dividing 16): each score is computed once and
- * kept in the workspace for the softmax and the values, instead of being recomputed in each of
- * three passes; the outputs are the same bits. The workspace holds one slot of
- * 16 * max_keys floats per resident workgroup; a smaller one (at least one slot) runs fewer
- * workgroups at a time, and none (NULL, 0) the recomputing kernel. Other launches ignore it.
+/* op_attention (src/nexterabert.cpp:785-852) as nxg_attention, with a device workspace for
+ * launches whose scores do not fit in LDS (more than ~2,400 keys per query with
+ * n_head / n_kv_head dividing 16), or fit with room for one workgroup per CU (more than ~1,200
+ * keys), or for two in a launch of more than 4 x the CUs' workgroups (e.g. 2 x 1,024 keys):
+ * each score is computed once and kept in the workspace for the softmax and the values,
+ * instead of kept in LDS or recomputed in each of three passes; the outputs are the same bits.
+ * The workspace holds one slot of 16 * max_keys floats per resident workgroup; a smaller one
+ * (at least one slot) runs fewer workgroups at a time, and none (NULL, 0) the LDS kernel where
+ * its scores fit, else the recomputing kernel. Other launches ignore it.
  * Calls that share a workspace must not overlap.
  *   workspace        device memory, 4-byte aligned, or NULL
  *   workspace_bytes  its size (nxg_attention_workspace_bytes gives the size for every slot) */
@@ -218,7 +221,8 @@ NXG_API int32_t nxg_attention_ws(const float * q, const float * k, const float *
  * device array of NXG_NOALLOC_SCRATCH_BYTES in the library's code object, one per GPU, held
  * until the process ends -- by every process that loads the library, on each GPU it uses,
  * whether or not it calls this entry point; the call uses as many of its slots (16 * max_keys floats each) as fit, and
- * refuses (NXG_EINVAL) a max_keys whose single slot would not fit (more than 1,048,576 keys).
+ * refuses (NXG_EINVAL) a max_keys whose single slot would not fit (more than 1,048,576 keys) where the
+ * scores do not fit in LDS either.
  * Same arguments and results as nxg_attention. Calls that overlap on one GPU race (they
  * share the array); calls in one stream, or synchronized, do not. */
 #define NXG_NOALLOC_SCRATCH_BYTES (64u << 20)

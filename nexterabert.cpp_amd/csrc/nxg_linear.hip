@@ -3942,22 +3942,38 @@ static long long attention_long_slots() {
     return slots;
 }
 
-// The launch nxg_attention_ws makes for (T, heads, max_keys): 0 tile kernel, 1 long kernel,
-// 2 row kernel; for the long kernel, its tiles and the workspace bytes of one slot.
+// The launch nxg_attention_ws makes for (T, heads, max_keys): 0 tile kernel, 1 stored kernel
+// given a workspace slot (else the tile kernel where its LDS fits, else the recomputing long
+// kernel), 2 row kernel; the tiles, the workspace bytes of one slot, and whether the tile
+// kernel's LDS fits.
 struct attn_plan {
     int kind;
     long long n_tiles;
     long long slot_bytes;
+    bool tile_fits;
 };
+
+// The tile kernel keeps its scores in LDS: ATT_P * smax floats beside one staged tile. Where
+// that leaves room for one workgroup per CU, or for two while the launch has more than two
+// rounds of them, attention_stored_kernel (the scores in a workspace slot, three workgroups
+// per CU) is faster: 2,048 keys 970 -> 560 us, 1,536 keys 560 -> 320 us, 2 x 1,024 keys
+// 314 -> 279 us, 8 x 1,024 keys 1,098 -> 1,015 us; one 1,024-key document (1,024 tiles, two
+// rounds) stays 3% faster on the tile kernel.
+static bool attention_tile_first(size_t tile_lds, size_t lds_max, long long n_tiles) {
+    if (tile_lds > lds_max) return false;
+    const size_t per_cu = (lds_max + 1024) / (tile_lds + 1024);   // the static 1 KiB included
+    return per_cu >= 3 || (per_cu == 2 && n_tiles <= 4LL * device_cus());
+}
 
 static attn_plan plan_attention(int32_t T, int32_t n_head, int32_t n_kv_head, int32_t max_keys) {
     const int rep = n_head / n_kv_head;
-    if (ATT_P % rep != 0) return {2, 0, 0};
+    if (ATT_P % rep != 0) return {2, 0, 0, false};
     const long long n_tiles = (long long) n_kv_head * ((T + ATT_P / rep - 1) / (ATT_P / rep));
     const int smax = (max_keys + 3) & ~3;
     const size_t tile_lds = ((size_t) ATT_P * smax + (size_t) ATT_KT * ATT_KS) * sizeof(float);
-    if (tile_lds <= attention_tile_lds_limit()) return {0, n_tiles, 0};
-    return {1, n_tiles, (long long) ATT_P * max_keys * (long long) sizeof(float)};
+    const size_t lds_max = attention_tile_lds_limit();
+    if (attention_tile_first(tile_lds, lds_max, n_tiles)) return {0, n_tiles, 0, true};
+    return {1, n_tiles, (long long) ATT_P * max_keys * (long long) sizeof(float), tile_lds <= lds_max};
 }
 
 int64_t nxg_attention_workspace_bytes(int32_t T, int32_t n_head, int32_t n_kv_head, int32_t max_keys) {
@@ -3984,14 +4000,15 @@ int32_t nxg_attention_noalloc(const float * q, const float * k, const float * v,
     int rc = check_device();
     if (rc) return rc;
     const attn_plan pl = plan_attention(T, n_head, n_kv_head, max_keys);
-    if (pl.kind == 1 && pl.slot_bytes > (long long) NXG_NOALLOC_SCRATCH_BYTES) {
+    const bool use_scratch = pl.kind == 1 && pl.slot_bytes <= (long long) NXG_NOALLOC_SCRATCH_BYTES;
+    if (pl.kind == 1 && !use_scratch && !pl.tile_fits) {
         return fail(NXG_EINVAL,
                     "attention_noalloc: max_keys=%d needs %lld bytes per workgroup's scores; the static scratch "
                     "holds %lld (at most %lld keys)", max_keys, pl.slot_bytes, (long long) NXG_NOALLOC_SCRATCH_BYTES,
                     (long long) NXG_NOALLOC_SCRATCH_BYTES / (ATT_P * (long long) sizeof(float)));
     }
-    void * ws = nullptr;
-    if (pl.kind == 1) {
+    void * ws = nullptr;                       // none: the tile kernel, its scores in LDS
+    if (use_scratch) {
         rc = scratch_of_device(&ws);
         if (rc) return rc;
     }
@@ -4025,13 +4042,18 @@ int32_t nxg_attention_ws(const float * q, const float * k, const float * v, cons
     if (rc) return rc;
     attn_params p{q, k, v, cu_offsets, scale, out, n_seqs, T, n_head, n_kv_head, half < 0 ? -1 : half, max_keys};
     // the tiled kernel when its LDS (scores of ATT_P pairs + one staged tile) fits a workgroup
+    // and attention_tile_first prefers it, or no workspace slot is given
     const int rep = n_head / n_kv_head;
     const int smax = (max_keys + 3) & ~3;
     const size_t tile_lds = ((size_t) ATT_P * smax + (size_t) ATT_KT * ATT_KS) * sizeof(float);
     if (ATT_P % rep == 0) {
-        const long long n_tiles = (long long) n_kv_head * ((T + ATT_P / rep - 1) / (ATT_P / rep));
+        const attn_plan pl = plan_attention(T, n_head, n_kv_head, max_keys);
+        const long long n_tiles = pl.n_tiles;
         const size_t lds_max = attention_tile_lds_limit();
-        if (tile_lds <= lds_max) {
+        // scores written once into the workspace: as many slots as it holds, up to the resident workgroups
+        const long long n_slots =
+            pl.kind == 1 ? std::min({n_tiles, attention_long_slots(), (long long) (workspace_bytes / pl.slot_bytes)}) : 0;
+        if (tile_lds <= lds_max && n_slots < 1) {
             // fewer than 3 workgroups per CU by LDS (the static 1 KiB included): 16 pairs per lane group
             if (NXG_ATT_WIDE && 3 * (tile_lds + 1024) > lds_max + 1024) {
                 attention_tile_kernel<true><<<dim3((unsigned) n_tiles), dim3(256), tile_lds, (hipStream_t) stream>>>(p, smax);
@@ -4040,9 +4062,6 @@ int32_t nxg_attention_ws(const float * q, const float * k, const float * v, cons
             }
             return launch_check("attention_tile_kernel");
         }
-        // scores written once into the workspace: as many slots as it holds, up to the resident workgroups
-        const attn_plan pl = plan_attention(T, n_head, n_kv_head, max_keys);
-        const long long n_slots = std::min({n_tiles, attention_long_slots(), (long long) (workspace_bytes / pl.slot_bytes)});
         if (n_slots >= 1) {
             // e stored by pass 2 (4 more bytes per (pair, key)) pays while the slots in use stay
             // in the last-level cache: 4,096 keys 1.97 -> 1.94 ms, 16,384 keys in bands of 2,601

@@ -114,6 +114,25 @@ def test_attention_stored_scores(nxg, orc, torch, dev, lengths, half, H, G):
         assert (bits(y) == bits(ref)).all()
 
 
+@pytest.mark.parametrize("lengths", [[1536], [1024, 1024], [1100, 900, 48]])
+def test_attention_stored_where_tiles_fit(nxg, orc, torch, dev, lengths):
+    """Scores that fit in LDS with room for one workgroup per CU (1,536 keys), or for two in a
+    launch of more than two rounds (2,048 tiles), go to the stored kernel when a workspace is
+    given, to the tile kernel without one: both give the oracle's bits."""
+    say(f"attention stored where tiles fit lengths={lengths}")
+    rng = np.random.default_rng(sum(lengths) + 21)
+    H, G = 16, 8
+    cu = nxg.cu_offsets_of(lengths)
+    T = int(cu[-1])
+    assert nxg.attention_workspace_bytes(T, H, G, max(lengths)) > 0
+    q = rng.standard_normal((T, H * 64)).astype(np.float32)
+    k, v = (rng.standard_normal((G, T, 64)).astype(np.float32) for _ in range(2))
+    scale = rng.uniform(0.05, 0.2, len(lengths)).astype(np.float32)
+    ref = orc.attention(q, k, v, cu, scale, H, G, -1)
+    for ws in ("auto", None):
+        assert (bits(run(nxg, torch, q, k, v, cu, scale, H, G, -1, workspace=ws)) == bits(ref)).all(), ws
+
+
 def test_attention_workspace_ignored_when_scores_fit(nxg, orc, torch, dev):
     """Short documents keep their scores in LDS: no workspace is asked for, and one given is unused."""
     say("attention workspace with short documents")
