@@ -1034,6 +1034,9 @@ __device__ __forceinline__ void att_chain_tree(const float (&a)[8], float (&s)[1
         : "v"(c[0]), "v"(c[1]));
 }
 
+__device__ __forceinline__ bool finite4(const v4f & x) {
+    return __builtin_isfinite(x.x) && __builtin_isfinite(x.y) && __builtin_isfinite(x.z) && __builtin_isfinite(x.w);
+}
 #ifndef NXG_ATT_WIDE
 #define NXG_ATT_WIDE 1         // 16 pairs per lane group where LDS allows two workgroups per CU (0: always 8)
 #endif
@@ -1232,20 +1235,28 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
         if (vn[i] > smax) vn[i] = 0;
         acc[i] = 0.0f;
     }
+    // a staged value tile holding a non-finite value (by tile parity): without one, every tile,
+    // also one only partly in a pair's keys, takes the broadcast path, its keys outside the pair's
+    // range adding fma(0, v, acc) = acc (acc is never -0: it starts at +0): banded attention
+    // over 8 x 1,024 tokens 343 -> 291 us, documents of 300 / 45 / 700 tokens 217 -> 144 us
+    __shared__ int vbad_s[2];
+    if (tid < 2) vbad_s[tid] = 0;
+    int par = 0;
     if (kl < kh) fetch(vg, kl);
-    for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
+    for (int j0 = kl; j0 < kh; j0 += ATT_KT, par ^= 1) {
         __syncthreads();                                   // weights written / previous tile read
+        if (tid == 0) vbad_s[par ^ 1] = 0;                 // the previous tile's flag, read by all
         stage();
+        if (!(finite4(pre[0]) && finite4(pre[1]))) vbad_s[par] = 1;
         __syncthreads();
         if (j0 + ATT_KT < kh) fetch(vg, j0 + ATT_KT);
         const int jn = min(ATT_KT, kh - j0);
         int a[4], b[4];
-        bool full = jn == ATT_KT;
+        const bool full = vbad_s[par] == 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {                      // keys [a, b) of the tile are pair i's
             a[i] = min(max(vlo[i] - j0, 0), jn);
             b[i] = max(min(vlo[i] + vn[i] - j0, jn), a[i]);
-            full = full && a[i] == 0 && b[i] == jn;
         }
         // the tile's weights: pair i's weight of key j0 + l in lane l (l < 32), read once and
         // broadcast per key (readlane), so the key loop reads only the value row from LDS
@@ -1310,7 +1321,7 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
 #ifndef NXG_ATT_E_STORE_MIB
 #define NXG_ATT_E_STORE_MIB 192   // the largest workspace in use (all slots) for which pass 2 stores e
 #endif
-template <bool STORED, bool ESTORE = false>
+template <bool STORED, bool ESTORE, bool ZW>
 __device__ __forceinline__ void attention_long_tile(const attn_params & p, float * __restrict__ sc, int bt) {
     __shared__ __attribute__((aligned(16))) float tile[ATT_KT * ATT_KS];
     __shared__ float E[ATT_P][ATT_KT + 1];                 // one tile's e (pass 2) or w (pass 3)
@@ -1626,18 +1637,28 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
             snx[r] = valid && jr >= 0 && jr < n_p ? scp[jr] : 0.0f;
         }
     };
+    // ZW: a staged value tile holding a non-finite value (by tile parity), as attention_tile_kernel:
+    // without one, a partial tile takes the broadcast path with zero weights outside a pair's keys
+    __shared__ int vbad_s[2];
+    if (tid < 2) vbad_s[tid] = 0;
+    int par = 0;
     if (kl < kh) {
         fetch(STORED ? vg : kg, kl);
         if constexpr (STORED) sfetch(kl);
     }
-    for (int j0 = kl; j0 < kh; j0 += ATT_KT) {
+    for (int j0 = kl; j0 < kh; j0 += ATT_KT, par ^= 1) {
         __syncthreads();                                   // E and the tile are free
+        if (ZW && tid == 0) vbad_s[par ^ 1] = 0;           // the previous tile's flag, read by all
         stage();
         if constexpr (STORED) {
+            if (ZW && !(finite4(pre[0]) && finite4(pre[1]))) vbad_s[par] = 1;
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
                 const int kt = sk + 16 * r, jr = j0 + kt - plo;
-                if (!valid || jr < 0 || jr >= n_p) continue;
+                if (!valid || jr < 0 || jr >= n_p) {
+                    if (ZW) E[sp][kt] = 0.0f;
+                    continue;
+                }
                 const float s = snx[r];
                 if (ESTORE) E[sp][kt] = s * inv;          // s holds e = exp(score - m), written by pass 2
                 else E[sp][kt] = (jr < ng_p ? exp_cephes(s - m) : expf_libm(s - m)) * inv;
@@ -1653,25 +1674,29 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
                 const int kt = sk + 16 * r, jr = j0 + kt - plo;
-                if (!valid || jr < 0 || jr >= n_p) continue;
+                if (!valid || jr < 0 || jr >= n_p) {
+                    if (ZW) E[sp][kt] = 0.0f;
+                    continue;
+                }
                 const float s = score_d64(qv, tile + kt * ATT_KS, jr < ng_p) * scale;
                 E[sp][kt] = (jr < ng_p ? exp_cephes(s - m) : expf_libm(s - m)) * inv;
             }
             __syncthreads();                               // the keys have been read
             stage();
+            if (ZW && !(finite4(pre[0]) && finite4(pre[1]))) vbad_s[par] = 1;
             __syncthreads();
             if (j0 + ATT_KT < kh) fetch(kg, j0 + ATT_KT);
         }
         const int jn = min(ATT_KT, kh - j0);
         // pair i's weights of the tile: lane l holds key j0 + l (l < 32), broadcast per key
         int a[4], b[4];
-        bool full = jn == ATT_KT;
+        bool full = ZW ? vbad_s[par] == 0 : jn == ATT_KT;
         float w0[4], w1[4];                                // keys j0 + k, j0 + 16 + k in lane k of each row
 #pragma unroll
         for (int i = 0; i < 4; ++i) {                      // keys [a, b) of the tile are pair i's
             a[i] = min(max(vlo[i] - j0, 0), jn);
             b[i] = max(min(vlo[i] + vn[i] - j0, jn), a[i]);
-            full = full && a[i] == 0 && b[i] == jn;
+            if (!ZW) full = full && a[i] == 0 && b[i] == jn;
             w0[i] = E[4 * pg + i][d & 15];
             w1[i] = E[4 * pg + i][16 + (d & 15)];
         }
@@ -1703,24 +1728,27 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
 }
 
 __global__ __launch_bounds__(256) void attention_long_kernel(attn_params p) {
-    attention_long_tile<false>(p, nullptr, (int) blockIdx.x);
+    attention_long_tile<false, false, true>(p, nullptr, (int) blockIdx.x);
 }
 
 // The scores kept in the workspace: a persistent grid, one slot of sc per workgroup, which
 // takes tiles blockIdx.x, blockIdx.x + gridDim.x, ... ESTORE: pass 2 stores the exponentials.
+// ZW (banded launches, where most value tiles are partial for some pair): partial tiles on the
+// broadcast path (16,384 keys in bands of 2,601 5.27 -> 5.18 ms); without a band only a pair's
+// last tile is partial, and the flags cost 1-2% (8,192 keys 8.31 -> 8.46 ms).
 // Three workgroups per CU (at most 168 registers; 8 pairs per lane group in pass 1, as 16 would
 // spill): 16,384 keys 40.9 -> 34.7 ms, 8,192 keys 10.2 -> 8.4 ms against two workgroups per CU with
 // 16 pairs per group (256 registers); four per CU (128 registers) spill and lose 1-10%.
 #ifndef NXG_ATT_STORED_MINB
 #define NXG_ATT_STORED_MINB 3
 #endif
-template <bool ESTORE>
+template <bool ESTORE, bool ZW>
 __global__ __launch_bounds__(256, NXG_ATT_STORED_MINB) void attention_stored_kernel(attn_params p, float * __restrict__ sc) {
     const int nq = ATT_P / (p.H / p.G);
     const int n_tiles = p.G * ((p.T + nq - 1) / nq);
     for (int bt = (int) blockIdx.x; bt < n_tiles; bt += (int) gridDim.x) {
         __syncthreads();                                   // the previous tile's shared reads are done
-        attention_long_tile<true, ESTORE>(p, sc, bt);
+        attention_long_tile<true, ESTORE, ZW>(p, sc, bt);
     }
 }
 
@@ -3930,7 +3958,7 @@ static long long attention_long_slots() {
         int cus = 0, per_cu = 0;
         if (dev >= 0 &&
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attention_stored_kernel<false>, 256, 0) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attention_stored_kernel<false, false>, 256, 0) == hipSuccess &&
             cus > 0 && per_cu > 0) {
             slots = (long long) cus * per_cu;
         } else {
@@ -4068,11 +4096,13 @@ int32_t nxg_attention_ws(const float * q, const float * k, const float * v, cons
             // 5.39 -> 5.32 ms; beyond it even or slower (at two workgroups per CU: 8,192 keys even,
             // 16,384 keys 40.8 -> 44.6 ms)
             const bool e_store = (double) n_slots * (double) pl.slot_bytes <= (double) NXG_ATT_E_STORE_MIB * 1048576.0;
-            if (e_store) {
-                attention_stored_kernel<true><<<dim3((unsigned) n_slots), dim3(256), 0, (hipStream_t) stream>>>(p, (float *) workspace);
-            } else {
-                attention_stored_kernel<false><<<dim3((unsigned) n_slots), dim3(256), 0, (hipStream_t) stream>>>(p, (float *) workspace);
-            }
+            const dim3 grid((unsigned) n_slots), block(256);
+            float * const ws = (float *) workspace;
+            hipStream_t s = (hipStream_t) stream;
+            if (e_store && p.half >= 0) attention_stored_kernel<true, true><<<grid, block, 0, s>>>(p, ws);
+            else if (e_store)           attention_stored_kernel<true, false><<<grid, block, 0, s>>>(p, ws);
+            else if (p.half >= 0)       attention_stored_kernel<false, true><<<grid, block, 0, s>>>(p, ws);
+            else                        attention_stored_kernel<false, false><<<grid, block, 0, s>>>(p, ws);
             return launch_check("attention_stored_kernel");
         }
         attention_long_kernel<<<dim3((unsigned) n_tiles), dim3(256), 0, (hipStream_t) stream>>>(p);

@@ -179,6 +179,33 @@ def test_attention_extreme_scores(nxg, orc, torch, dev):
     assert (bits(y) == bits(orc.attention(q, k, v, cu, scale, H, G))).all()
 
 
+@pytest.mark.parametrize("lengths,half,H,G,ws", [([40, 300, 25], -1, 16, 8, None), ([600], 100, 16, 8, None),
+                                                 ([3000], 1300, 2, 1, "auto"), ([40, 2900, 25], -1, 2, 1, "auto"),
+                                                 ([40, 2900, 25], -1, 2, 1, None)])
+def test_attention_non_finite_values_outside_a_pair(nxg, orc, torch, dev, lengths, half, H, G, ws):
+    """Inf and NaN values at keys that other pairs of the same staged tile do not attend to (a
+    neighbour document, outside a band), on the tile, stored and recomputing kernels: value
+    tiles that hold them take the per-key path, the others the broadcast path with zero weights
+    outside a pair's keys; the pairs that do not see them stay finite and give the oracle's
+    bits, the others its NaN / Inf pattern."""
+    say(f"attention non-finite values lengths={lengths} half={half} H={H} G={G} ws={ws}")
+    rng = np.random.default_rng(sum(lengths) + 31)
+    cu = nxg.cu_offsets_of(lengths)
+    T = int(cu[-1])
+    q = rng.standard_normal((T, H * 64)).astype(np.float32)
+    k, v = (rng.standard_normal((G, T, 64)).astype(np.float32) for _ in range(2))
+    bad = [3, 30, T - 5] if len(lengths) > 1 else [5, T // 2, T - 3]
+    v[:, bad[0], 5] = np.inf
+    v[:, bad[1], 7] = np.nan
+    v[:, bad[2], 9] = -np.inf
+    scale = rng.uniform(0.05, 0.2, len(lengths)).astype(np.float32)
+    y = run(nxg, torch, q, k, v, cu, scale, H, G, half, workspace=ws)
+    ref = orc.attention(q, k, v, cu, scale, H, G, half)
+    same = (bits(y) == bits(ref)) | (np.isnan(y) & np.isnan(ref))
+    assert same.all()
+    assert np.isfinite(ref).mean() > 0.5 and not np.isfinite(ref).all()
+
+
 def test_attention_document_alone(nxg, torch, dev):
     say("attention: a document alone and in a batch")
     rng = np.random.default_rng(9)
