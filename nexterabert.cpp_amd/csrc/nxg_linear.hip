@@ -937,7 +937,9 @@ __device__ __forceinline__ void fmac_bcast4_16(float (&acc)[4], const float (&w)
 //   values    thread (dim d, 4 pairs): acc = fma(w_j, v_j[d], acc) over the keys in order;
 //             a tile's weights of a pair are read once, key j0 + 16h + k in lane k of every
 //             16-lane row of register h, and each fma takes its weight through DPP row_newbcast
-//             (readlane on partial tiles), so the key loop reads only v_j[d] from LDS.
+//             (keys outside a pair's range with weight 0, adding fma(0, v, acc) = acc; readlane
+//             and a per-key range test on tiles whose staged values hold an Inf or NaN), so the
+//             key loop reads only v_j[d] from LDS.
 // Keys are staged ATT_KT at a time ([key][ATT_KS] floats; the padding puts the 16 rows one
 // wave reads on different banks). Pairs whose keys exceed smax get NaN, as attention_kernel.
 // One key's score for a query held in registers, before the scale (scores_d64,
@@ -1306,7 +1308,8 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
 //           added after hsum256, in order
 //   pass 3  w = e * (1 / sum) per key through LDS, then thread (dim d, 4 pairs) acc = fma(w,
 //           v[d], acc) over the keys in order, as attention_tile_kernel (the tile's weights
-//           read once per lane and broadcast per key by DPP row_newbcast or readlane)
+//           read once per lane and broadcast per key by DPP row_newbcast, or by readlane with a
+//           per-key range test on partial tiles (ZW: only on tiles with an Inf or NaN value))
 // Keys and values are staged ATT_KT at a time ([key][ATT_KS]).
 // STORED: pass 1 also writes each score to the workgroup's slot of the workspace sc
 // ([gridDim.x][ATT_P][max_keys] floats, pair-relative key index), and passes 2 and 3 read the
