@@ -841,7 +841,7 @@ __device__ __forceinline__ void softmax_max_exp(float * Sp, int n, int sk) {
 #pragma unroll
     for (int sft = 8; sft >= 1; sft >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sft));
     const float m = __builtin_isnan(s0) ? s0 : mx;
-#pragma unroll 4
+#pragma unroll 8
     for (int j = sk; j < ng; j += 16) Sp[j] = exp_cephes(Sp[j] - m);
     for (int j = ng + sk; j < n; j += 16) Sp[j] = expf_libm(Sp[j] - m);
 }
@@ -871,7 +871,7 @@ __device__ __forceinline__ float softmax_inv(const float * Sp, int n, int sk, bo
 }
 
 __device__ __forceinline__ void softmax_weights(float * Sp, int n, int sk, float inv) {
-#pragma unroll 4
+#pragma unroll 8
     for (int j = sk; j < n; j += 16) Sp[j] = Sp[j] * inv;
 }
 
