@@ -875,47 +875,28 @@ __device__ __forceinline__ void softmax_weights(float * Sp, int n, int sk, float
     for (int j = sk; j < n; j += 16) Sp[j] = Sp[j] * inv;
 }
 
-// acc[i] = fma(w_i[lane L of this lane's 16-lane row], v, acc[i]) for i < 4: v_fmac_f32 (one
-// rounding, as fmaf) with its first operand broadcast by DPP row_newbcast. With w_i holding
-// key k of a 16-key group in lanes k, k + 16, k + 32, k + 48, every lane gets key L's weight.
-// The s_nop gives a DPP read its two wait states after any VALU write of w_i.
-template <int L>
-__device__ __forceinline__ void fmac_bcast4(float (&acc)[4], const float (&w)[4], float v) {
-    asm("s_nop 1\n\t"
-        "v_fmac_f32_dpp %0, %4, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_fmac_f32_dpp %1, %5, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_fmac_f32_dpp %2, %6, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_fmac_f32_dpp %3, %7, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
-        : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
-        : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(v), "n"(L));
-}
-
-// 16 keys of a tile in order: key k (< 16) has its weights in lane k of each row of w and its
-// value in vt[k]. BLOCK: one asm block, so that the 16 values are in registers before the first
-// FMA (their LDS reads issued together, one wait) and one s_nop covers the VALU writes of w --
-// for the launches of two workgroups per CU (full attention: 1,024 keys 170.5 -> 164.5 us,
-// 16,384 keys 44.6 -> 40.8 ms); with three or four per CU (banded attention) the per-key
-// blocks, whose reads the compiler spreads among the FMAs, stay ~1% faster.
+// acc[i] = fma(w_i[lane L of this lane's 16-lane row], v_L, acc[i]) for i < 4 and the 16 keys
+// L of a half tile in order: v_fmac_f32 (one rounding, as fmaf) with its first operand
+// broadcast by DPP row_newbcast. With w_i holding key k of a 16-key group in lanes k, k + 16,
+// k + 32, k + 48, every lane gets key L's weight; key L's value is vt[L]. One asm block, so that
+// the 16 values are in registers before the first FMA (their LDS reads issued together, one
+// wait; the compiler otherwise spread them among the FMAs, one wait per two keys), and one
+// s_nop gives the DPP reads their two wait states after the VALU writes of w: full attention
+// over 1,024 keys 170.5 -> 164.5 us, banded attention over 8 x 1,024 tokens 295 -> 282 us.
 #define NXG_FB4(k, vo) \
     "v_fmac_f32_dpp %0, %4, %" #vo " row_newbcast:" #k " row_mask:0xf bank_mask:0xf\n\t" \
     "v_fmac_f32_dpp %1, %5, %" #vo " row_newbcast:" #k " row_mask:0xf bank_mask:0xf\n\t" \
     "v_fmac_f32_dpp %2, %6, %" #vo " row_newbcast:" #k " row_mask:0xf bank_mask:0xf\n\t" \
     "v_fmac_f32_dpp %3, %7, %" #vo " row_newbcast:" #k " row_mask:0xf bank_mask:0xf\n\t"
-template <bool BLOCK, int L = 0>
 __device__ __forceinline__ void fmac_bcast4_16(float (&acc)[4], const float (&w)[4], const float * vt) {
-    if constexpr (BLOCK) {
-        asm("s_nop 1\n\t"
-            NXG_FB4(0, 8) NXG_FB4(1, 9) NXG_FB4(2, 10) NXG_FB4(3, 11) NXG_FB4(4, 12) NXG_FB4(5, 13)
-            NXG_FB4(6, 14) NXG_FB4(7, 15) NXG_FB4(8, 16) NXG_FB4(9, 17) NXG_FB4(10, 18) NXG_FB4(11, 19)
-            NXG_FB4(12, 20) NXG_FB4(13, 21) NXG_FB4(14, 22) NXG_FB4(15, 23)
-            : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
-            : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]),
-              "v"(vt[0]), "v"(vt[1]), "v"(vt[2]), "v"(vt[3]), "v"(vt[4]), "v"(vt[5]), "v"(vt[6]), "v"(vt[7]),
-              "v"(vt[8]), "v"(vt[9]), "v"(vt[10]), "v"(vt[11]), "v"(vt[12]), "v"(vt[13]), "v"(vt[14]), "v"(vt[15]));
-    } else {
-        fmac_bcast4<L>(acc, w, vt[L]);
-        if constexpr (L + 1 < 16) fmac_bcast4_16<false, L + 1>(acc, w, vt);
-    }
+    asm("s_nop 1\n\t"
+        NXG_FB4(0, 8) NXG_FB4(1, 9) NXG_FB4(2, 10) NXG_FB4(3, 11) NXG_FB4(4, 12) NXG_FB4(5, 13)
+        NXG_FB4(6, 14) NXG_FB4(7, 15) NXG_FB4(8, 16) NXG_FB4(9, 17) NXG_FB4(10, 18) NXG_FB4(11, 19)
+        NXG_FB4(12, 20) NXG_FB4(13, 21) NXG_FB4(14, 22) NXG_FB4(15, 23)
+        : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
+        : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]),
+          "v"(vt[0]), "v"(vt[1]), "v"(vt[2]), "v"(vt[3]), "v"(vt[4]), "v"(vt[5]), "v"(vt[6]), "v"(vt[7]),
+          "v"(vt[8]), "v"(vt[9]), "v"(vt[10]), "v"(vt[11]), "v"(vt[12]), "v"(vt[13]), "v"(vt[14]), "v"(vt[15]));
 }
 #undef NXG_FB4
 
@@ -1277,8 +1258,8 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(attn_params p, int 
             float vt[ATT_KT];                              // the tile's values of dimension d, read up front
 #pragma unroll
             for (int jj = 0; jj < ATT_KT; ++jj) vt[jj] = tile[jj * ATT_KS + d];
-            fmac_bcast4_16<WIDE>(acc, w0, vt);
-            fmac_bcast4_16<WIDE>(acc, w1, vt + 16);
+            fmac_bcast4_16(acc, w0, vt);
+            fmac_bcast4_16(acc, w1, vt + 16);
         } else {
             for (int jj = 0; jj < jn; ++jj) {
                 const float v = tile[jj * ATT_KS + d];
@@ -1710,8 +1691,8 @@ __device__ __forceinline__ void attention_long_tile(const attn_params & p, float
             float vt[ATT_KT];
 #pragma unroll
             for (int jj = 0; jj < ATT_KT; ++jj) vt[jj] = tile[jj * ATT_KS + d];
-            fmac_bcast4_16<true>(acc, w0, vt);
-            fmac_bcast4_16<true>(acc, w1, vt + 16);
+            fmac_bcast4_16(acc, w0, vt);
+            fmac_bcast4_16(acc, w1, vt + 16);
         } else {
             for (int jj = 0; jj < jn; ++jj) {
                 const float v = tile[jj * ATT_KS + d];
